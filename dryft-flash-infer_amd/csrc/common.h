@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 quantized-linear library.
+//
+// Number formats travel as raw bits: bf16 and fp16 as uint16_t, OCP e4m3fn as
+// uint8_t. Every conversion here rounds to nearest even, the way torch's casts
+// do, so quantize and pack kernels are bit-exact with the CPU statement of the
+// reference (engine/kernels/cuda_fp8.py:1127-1151, engine/kernels/fp8.py:20-28).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+namespace qlx {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+
+// ---- bf16 / fp16 -------------------------------------------------------------------
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, RNE by integer add (cuda_fp8.py:64-68); NaN -> sign | 0x7FC0.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// fp32 -> fp16 bits, RNE (hardware v_cvt_f16_f32 rounds to nearest even).
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// ---- OCP e4m3fn ------------------------------------------------------------------------
+
+// fp32 -> e4m3fn byte, RNE. Below 2^-6 the subnormal code is rint(|f| * 2^9);
+// above, 20 mantissa bits are dropped with round-half-even by integer add.
+// Anything that rounds past 448 (and Inf/NaN) becomes NaN (0x7F), as torch's cast.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  uint32_t code;
+  if (a > 0x7f800000u) {
+    code = 0x7fu;
+  } else if (a < (121u << 23)) {
+    code = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
+  } else {
+    const uint32_t ar = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (ar >> 20) - (120u << 3);
+    if (code > 0x7eu) code = 0x7fu;
+  }
+  return code | sign;
+}
+
+// Clamp to +-lim keeping NaN (torch.clamp propagates NaN; fminf/fmaxf would not).
+__device__ __forceinline__ float clamp_keep_nan(float v, float lim) {
+  return v < -lim ? -lim : (v > lim ? lim : v);
+}
+
+// ---- wave reductions (64 lanes) ----------------------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---- error reporting --------------------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);
+
+}  // namespace qlx
+
+#define QLX_OK 0
+#define QLX_EINVAL (-1)
+#define QLX_EHIP (-2)
+
+#define QLX_REQUIRE(cond, ...)                  \
+  do {                                          \
+    if (!(cond)) {                              \
+      qlx::set_error(__VA_ARGS__);              \
+      return QLX_EINVAL;                        \
+    }                                           \
+  } while (0)
+
+#define QLX_LAUNCH_CHECK(what) return qlx::hip_status(hipGetLastError(), what)

@@ -1,0 +1,170 @@
+// Split-K plane consumers and the small epilogues between projections.
+//
+// The bf16 roundings land where the reference puts them:
+//   reduce_planes     bf16(sum_s P[s]) in slice order      engine/kernels/cuda_fp8.py:965-981
+//   residual_planes   bf16(x + bf16(sum_s P[s]))           engine/kernels/cuda_small.py:43-55
+//   rms_norm          bf16(bf16(x * rsqrt(mean x^2 + eps)) * w)  engine/kernels/reference.py:13-16
+//   add_rms_norm      residual then rms_norm               engine/kernels/reference.py:19-28
+//   swiglu            bf16(bf16(silu(bf16 g)) * bf16 u)    engine/kernels/swiglu.py:37-53
+//   add_norm_quant    residual, rms_norm, INT8 quantize    engine/kernels/cuda_int8.py:17-44
+#include "common.h"
+#include "../../include/qlinear.h"
+
+namespace qlx {
+
+__global__ void __launch_bounds__(256)
+reduce_planes_kernel(const float* __restrict__ p, uint16_t* __restrict__ out, size_t width, int splits) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= width) return;
+  float acc = 0.f;
+  for (int s = 0; s < splits; ++s) acc += p[(size_t)s * width + i];
+  out[i] = f2bf(acc);
+}
+
+__global__ void __launch_bounds__(256)
+residual_planes_kernel(const uint16_t* __restrict__ x, const float* __restrict__ p,
+                       uint16_t* __restrict__ out, size_t width, int splits) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= width) return;
+  float acc = 0.f;
+  for (int s = 0; s < splits; ++s) acc += p[(size_t)s * width + i];
+  out[i] = f2bf(bf2f(x[i]) + round_bf(acc));
+}
+
+// delta: bf16 [rows][n] or (planes != null) fp32 planes [splits][rows][n]; res may be null
+// (plain rms_norm of x). One workgroup of 256 threads per row.
+__global__ void __launch_bounds__(256)
+add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
+                    const float* __restrict__ planes, int splits, const uint16_t* __restrict__ w,
+                    uint16_t* __restrict__ res, uint16_t* __restrict__ y, int8_t* __restrict__ q,
+                    float* __restrict__ qs, int rows, int n, float eps) {
+  extern __shared__ float rbuf[];  // the row's residual, fp32
+  __shared__ float part[4];
+  const int row = blockIdx.x;
+  const size_t base = (size_t)row * n;
+  const bool add = delta != nullptr || planes != nullptr;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    float r = bf2f(x[base + c]);
+    if (add) {
+      float d;
+      if (planes) {
+        d = 0.f;
+        for (int s = 0; s < splits; ++s) d += planes[(size_t)s * rows * n + base + c];
+        d = round_bf(d);
+      } else {
+        d = bf2f(delta[base + c]);
+      }
+      r = round_bf(r + d);
+      if (res) res[base + c] = f2bf(r);
+    }
+    rbuf[c] = r;
+    ss += r * r;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = ((part[0] + part[1]) + part[2]) + part[3];
+  const float scale = 1.0f / sqrtf(total / (float)n + eps);
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float v = round_bf(round_bf(rbuf[c] * scale) * bf2f(w[c]));
+    rbuf[c] = v;
+    if (y) y[base + c] = f2bf(v);
+  }
+  if (!q) return;
+  // INT8 activation quantize per 64-group, fragment order (cuda_int8.py:30-44).
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int groups = n / 64;
+  for (int g = threadIdx.x >> 6; g < groups; g += 4) {
+    const int nat = (lane >> 4) * 4 + ((lane & 15) >> 2) * 16 + (lane & 3);
+    const float v = rbuf[g * 64 + nat];
+    const float amax = wave_max(fabsf(v));
+    const float s = fmaxf(amax / 127.f, 1e-20f);
+    q[base + g * 64 + lane] = (int8_t)(int)rintf(v / s);
+    if (lane == 0) qs[(size_t)row * groups + g] = s;
+  }
+}
+
+// gate_up: bf16 [rows][2I] or (planes != null) fp32 planes [splits][rows][2I].
+__global__ void __launch_bounds__(256)
+swiglu_kernel(const uint16_t* __restrict__ gu, const float* __restrict__ planes, int splits,
+              uint16_t* __restrict__ out, int rows, int inter) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int row = blockIdx.y;
+  if (c >= inter) return;
+  const size_t base = (size_t)row * 2 * inter + c;
+  float g, u;
+  if (planes) {
+    g = 0.f;
+    u = 0.f;
+    const size_t plane = (size_t)rows * 2 * inter;
+    for (int s = 0; s < splits; ++s) {
+      g += planes[s * plane + base];
+      u += planes[s * plane + base + inter];
+    }
+    g = round_bf(g);
+    u = round_bf(u);
+  } else {
+    g = bf2f(gu[base]);
+    u = bf2f(gu[base + inter]);
+  }
+  const float silu = round_bf(g / (1.f + expf(-g)));
+  out[(size_t)row * inter + c] = f2bf(silu * u);
+}
+
+static inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace qlx
+
+using namespace qlx;
+
+extern "C" {
+
+int qlx_reduce_planes(const float* planes, void* out, long long width, int splits, void* stream) {
+  QLX_REQUIRE(width > 0 && splits >= 1, "bad reduce shape");
+  reduce_planes_kernel<<<blocks_for(width), 256, 0, (hipStream_t)stream>>>(planes, (uint16_t*)out,
+                                                                          (size_t)width, splits);
+  QLX_LAUNCH_CHECK("reduce_planes");
+}
+
+int qlx_residual_planes(const void* x, const float* planes, void* out, long long width, int splits,
+                        void* stream) {
+  QLX_REQUIRE(width > 0 && splits >= 1, "bad residual shape");
+  residual_planes_kernel<<<blocks_for(width), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, planes, (uint16_t*)out, (size_t)width, splits);
+  QLX_LAUNCH_CHECK("residual_planes");
+}
+
+int qlx_add_rms_norm(const void* x, const void* delta, const float* planes, int splits, const void* w,
+                     void* res, void* y, int rows, int n, float eps, void* stream) {
+  QLX_REQUIRE(rows > 0 && n > 0 && n <= 16384, "rows=%d n=%d: rows must be > 0 and n in 1..16384", rows, n);
+  QLX_REQUIRE(planes == nullptr || splits >= 1, "planes need splits >= 1");
+  add_rms_norm_kernel<<<rows, 256, n * sizeof(float), (hipStream_t)stream>>>(
+      (const uint16_t*)x, (const uint16_t*)delta, planes, splits, (const uint16_t*)w, (uint16_t*)res,
+      (uint16_t*)y, nullptr, nullptr, rows, n, eps);
+  QLX_LAUNCH_CHECK("add_rms_norm");
+}
+
+int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* planes, int splits,
+                            const void* w, void* res, void* q, float* q_scale, int rows, int n, float eps,
+                            void* stream) {
+  QLX_REQUIRE(rows > 0 && n > 0 && n <= 16384 && n % 64 == 0, "n=%d must be a multiple of 64 up to 16384", n);
+  QLX_REQUIRE(planes == nullptr || splits >= 1, "planes need splits >= 1");
+  add_rms_norm_kernel<<<rows, 256, n * sizeof(float), (hipStream_t)stream>>>(
+      (const uint16_t*)x, (const uint16_t*)delta, planes, splits, (const uint16_t*)w, (uint16_t*)res,
+      nullptr, (int8_t*)q, q_scale, rows, n, eps);
+  QLX_LAUNCH_CHECK("add_norm_quant_int8");
+}
+
+int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, int rows, int inter,
+               void* stream) {
+  QLX_REQUIRE(rows > 0 && inter > 0, "bad swiglu shape");
+  QLX_REQUIRE(gate_up != nullptr || (planes != nullptr && splits >= 1), "swiglu needs gate_up or planes");
+  dim3 grid((inter + 255) / 256, rows);
+  swiglu_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const uint16_t*)gate_up, planes, splits,
+                                                      (uint16_t*)out, rows, inter);
+  QLX_LAUNCH_CHECK("swiglu");
+}
+
+}  // extern "C"

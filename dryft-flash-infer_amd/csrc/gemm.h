@@ -1,0 +1,755 @@
+// Quantized skinny GEMM / GEMV for gfx950: y[m][n] = sum_k x[m][k] * deq(W)[n][k].
+//
+// One kernel skeleton serves every weight format; a small policy struct per format says
+// how a wave loads its weight chunk, turns it into MFMA operands and applies scales.
+//
+// Work decomposition (decode shapes: m = 1..64, n = 2560..151936, k = 2560..9728):
+//   * the weight is cut into 16-row tiles; a tile's k range is cut into "steps" of KSTEP
+//     values, and one step of one tile is what a wave's lanes load in one 16-byte-per-lane
+//     instruction (1 KB for 4-bit and 8-bit formats; 2 KB, two loads, for the reference's
+//     8-bit tiles);
+//   * a workgroup owns RT = (waves / kw) * rw consecutive tiles and one K slice of `sps`
+//     steps. kw waves split the slice of one tile step by step (interleaved), rw is the
+//     number of tiles each wave streams side by side so one activation fragment feeds rw
+//     MFMAs;
+//   * `splits` K slices of a row block are separate workgroups. The last one to finish
+//     (a ticket counter per row block) sums the fp32 partials in slice order and writes
+//     the output, so results do not depend on scheduling (engine/kernels/cuda_fp8.py:975
+//     sums split-K planes in the same fixed order).
+//
+// MFMA operand layout (v_mfma_f32_16x16x32_{bf16,fp8}, v_mfma_i32_16x16x64_i8): lane l
+// supplies A row (l & 15) and B column (l & 15) for the k chunk (l >> 4), and receives D
+// rows 4*(l >> 4) + 0..3 of column (l & 15). A rows are weight rows, B columns are
+// activation rows (tokens), so m <= 16 per fragment; lanes whose token index is past m
+// read the last real token and their output column is dropped.
+//
+// The k order inside an MFMA is free as long as A and B agree, so the activation is staged
+// into LDS in whatever order the weight chunk unpacks in ("B order"). Integer codes are
+// turned into exact bf16 by the magic-number method (Kim et al., 2022: OR the code into
+// the mantissa of 128.0 for 4-bit codes; v_cvt_f32_ubyte for bytes), which adds a bias
+// per value. The bias times the activation sum is subtracted per scale group, computed by
+// the same MFMA chain with the codes all at the bias, so zero weights cancel exactly.
+#pragma once
+
+#include "common.h"
+#include "../../include/qlinear.h"
+
+namespace qlx {
+
+struct GemmArgs {
+  const void* w;
+  const void* ws;   // weight scales
+  const void* x;    // activation (bf16, or int8 for FMT_INT8)
+  const float* xs;  // activation scales (FMT_INT8)
+  void* y;
+  float* work;
+  int* tickets;
+  int m, n, k;
+  int mode, splits, sps, nsteps;
+  int ntiles, kw, rt, tile_groups;
+  int group;         // FP8WO scale group
+  int tiled;         // REF8 storage
+  int half;          // SWIGLU: I = n / 2
+  int xstride;       // LDS bytes per staged activation row
+  int off_sc, off_xb, off_sx;  // LDS byte offsets (x region starts at 0)
+  int sc_stride;     // floats per staged scale row ([step*nsc + j][16*rt])
+  int xb_stride;     // floats per token in xb ([m][sps*nsc])
+};
+
+// Weight row held by tile row r (0..15). SwiGLU tiles pair gate rows 8t..8t+7 with the
+// matching up rows I+8t..I+8t+7 (engine/kernels/cuda_fp8.py:208-212 pairs them per lane).
+__device__ __forceinline__ int weight_row(const GemmArgs& a, int tile, int r) {
+  if (a.mode == QLX_MODE_SWIGLU) return r < 8 ? 8 * tile + r : a.half + 8 * tile + r - 8;
+  return 16 * tile + r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Two exact small-integer floats -> bf16 pair (the high halves are exact: <= 8 significant bits).
+__device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 4 bytes -> 4 bf16 values (byte value as float), natural order.
+__device__ __forceinline__ uint2 bytes_to_bf16(uint32_t d) {
+  uint2 r;
+  r.x = pack_hi((float)(d & 0xffu), (float)((d >> 8) & 0xffu));
+  r.y = pack_hi((float)((d >> 16) & 0xffu), (float)(d >> 24));
+  return r;
+}
+
+// Low nibbles of bytes (0,2) and (1,3) of d, shifted by `sh`, as bf16(128 + code) pairs.
+__device__ __forceinline__ uint32_t nib_pair(uint32_t d, int sh) {
+  return ((d >> sh) & 0x000f000fu) | 0x43004300u;
+}
+
+__device__ __forceinline__ uint32_t bf16_at(const uint16_t* p, int i) { return p[i]; }
+
+// ====================================================================================
+// Format policies. Each provides:
+//   KSTEP, LOADS (16-byte loads per lane per step), NSC (scales per step; 0 = per
+//   channel), BIAS (code bias removed via activation sums; 0 = none), XBYTES (staged
+//   bytes per activation value), load(), compute(), stage_chunk(), finish().
+// ====================================================================================
+
+// ---- W4A16: int32 [n][k/8] words (nibble i of word j = k 8j+i, code = q + 8),
+//      bf16 scale [n][k/128]. Step = one 128-group; lane chunk = 4 words = 32 k.
+struct FmtW4 {
+  static constexpr int KSTEP = 128, LOADS = 1, NSC = 1, XBYTES = 2;
+  static constexpr float BIAS = 136.f;  // bf16(128 + code) = q + 136
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(a.w) +
+                                          (size_t)wrow * (a.k >> 3) + step * 16 + (lane >> 4) * 4);
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 7) + step]);
+  }
+  // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword).
+  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) +
+                                                    (size_t)mm * a.k + kabs);
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    return o;
+  }
+  // The same MFMA chain with every code at the bias (q = 0): bias * sum(x) rounded exactly
+  // as the main loop rounds it, so an all-zero weight row gives exactly zero.
+  __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
+    const uint4 av = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136
+    const int kb = (srel * 128 + (lane >> 4) * 32) * 2;
+    f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff + kb + t * 16);
+      t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), t4, 0, 0, 0);
+    }
+    return t4;
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&mrow)[MT], int rowl) {
+    f32x4 tmp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t wd[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
+    const int kb = (srel * 128 + (lane >> 4) * 32) * 2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 av;
+      av.x = nib_pair(wd[t], 0);
+      av.y = nib_pair(wd[t], 4);
+      av.z = nib_pair(wd[t], 8);
+      av.w = nib_pair(wd[t], 12);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+      }
+    }
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(
+        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float xb = reinterpret_cast<const float*>(lds + a.off_xb)[mrow[mt] * a.xb_stride + srel];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(sc[i], tmp[mt][i] - xb, acc[mt][i]);
+    }
+  }
+  __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
+};
+
+// ---- W8A16 per output channel: int8 [n][k], bf16 scale [n]. Step = 64 k.
+struct FmtW8 {
+  static constexpr int KSTEP = 64, LOADS = 1, NSC = 0, XBYTES = 2;
+  static constexpr float BIAS = 128.f;  // (byte ^ 0x80) = q + 128
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(a.w) + (size_t)wrow * a.k +
+                                          step * 64 + (lane >> 4) * 16);
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
+  }
+  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
+  }
+  __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
+    const uint4 av = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
+    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
+    f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff + kb + t * 16);
+      t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), t4, 0, 0, 0);
+    }
+    return t4;
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&mrow)[MT], int) {
+    const uint32_t wd[4] = {c[0].x ^ 0x80808080u, c[0].y ^ 0x80808080u, c[0].z ^ 0x80808080u,
+                            c[0].w ^ 0x80808080u};
+    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
+    f32x4 tmp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint2 lo = bytes_to_bf16(wd[2 * t]), hi = bytes_to_bf16(wd[2 * t + 1]);
+      const uint4 av = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float xb = reinterpret_cast<const float*>(lds + a.off_xb)[mrow[mt] * a.xb_stride + srel];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[mt][i] - xb;
+    }
+  }
+  // Per-channel scale once, after the K sum.
+  __device__ static float finish(const GemmArgs& a, const char* lds, float v, int rl, int) {
+    return v * reinterpret_cast<const float*>(lds + a.off_sc)[rl];
+  }
+};
+
+// ---- FP8 W8A8: e4m3 [n][k], bf16 scale [n]; activation quantized per token in the
+//      prologue. Step = 64 k.
+struct FmtFP8 {
+  static constexpr int KSTEP = 64, LOADS = 1, NSC = 0, XBYTES = 1;
+  static constexpr float BIAS = 0.f;
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + (size_t)wrow * a.k +
+                                          step * 64 + (lane >> 4) * 16);
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs&, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&)[MT], int) {
+    const int kb = srel * 64 + (lane >> 4) * 16;
+    const long a0 = (long)(((unsigned long)c[0].y << 32) | c[0].x);
+    const long a1 = (long)(((unsigned long)c[0].w << 32) | c[0].z);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
+      const long b0 = (long)(((unsigned long)bv.y << 32) | bv.x);
+      const long b1 = (long)(((unsigned long)bv.w << 32) | bv.z);
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a0, b0, acc[mt], 0, 0, 0);
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a1, b1, acc[mt], 0, 0, 0);
+    }
+  }
+  __device__ static float finish(const GemmArgs& a, const char* lds, float v, int rl, int mm) {
+    const float sx = reinterpret_cast<const float*>(lds + a.off_sx)[mm];
+    return v * sx * reinterpret_cast<const float*>(lds + a.off_sc)[rl];
+  }
+};
+
+// Natural column at permuted position p of a 64-block (engine/kernels/cuda_fp8.py:1117-1124).
+__device__ __forceinline__ int ref_pos_natural(int p) {
+  const int t = p >> 4, s = (p >> 2) & 3, i = p & 3;
+  return 16 * s + 2 * t + ((i & 1) | ((i >> 1) << 3));
+}
+
+// ---- cuda_fp8 reference formats: offset codes, fp16 scale per 64 [n][k/64], columns of each
+//      64-block permuted (cuda_fp8.py:1117-1124). Step = 128 k = blocks j = 0, 1.
+//      BITS 8: tiled [rows/16][K/128][half][j][g][t][16 B] or row-major permuted;
+//      BITS 4: tiled [rows/16][K/128][half][g][t][16 B], block 0 low nibble, block 1 high.
+//      Lane (r, c) takes the chunk of row r at t = c, so B position
+//      64j + 16c + 8u + e holds permuted position 16c + 8u + e' of block j.
+template <int BITS>
+struct FmtRef {
+  static constexpr int KSTEP = 128, LOADS = BITS == 8 ? 2 : 1, NSC = 2, XBYTES = 2;
+  static constexpr float BIAS = BITS == 8 ? 128.f : 136.f;
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    const int r = wrow & 15, tile = wrow >> 4, c = lane >> 4;
+    const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
+    if (BITS == 4) {
+      const size_t tb = ((size_t)tile * (a.k >> 7) + step) * 1024;
+      return reinterpret_cast<const uint4*>(w + tb + (((r >> 3) * 8 + (r & 7)) * 4 + c) * 16);
+    }
+    if (a.tiled) {
+      const size_t tb = ((size_t)tile * (a.k >> 7) + step) * 2048;
+      return reinterpret_cast<const uint4*>(w + tb + ((((r >> 3) * 2) * 8 + (r & 7)) * 4 + c) * 16);
+    }
+    return reinterpret_cast<const uint4*>(w + (size_t)wrow * a.k + step * 128 + c * 16);
+  }
+  // Second load (block j = 1) of the 8-bit formats.
+  __device__ static const uint4* chunk_ptr1(const GemmArgs& a, const uint4* p0) {
+    return a.tiled ? p0 + 8 * 4 : p0 + 4;  // tiled: next j is 8 rows x 4 chunks further
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
+    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
+  }
+  // B position e (0..7) of chunk (c, u) of a 64-block holds permuted position 16c + 8u + sw(e):
+  // 8-bit codes unpack in byte order, 4-bit codes as bytes (0,2),(1,3) per dword.
+  __device__ static f32x4 bias_chain(const char* lds, int srel, int j, int lane, int xoff) {
+    const uint32_t b = BITS == 8 ? 0x43004300u : 0x43084308u;  // bf16 128 / 136
+    const uint4 av = {b, b, b, b};
+    const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
+    f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff + kb + u * 16);
+      t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), t4, 0, 0, 0);
+    }
+    return t4;
+  }
+  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
+    const uint16_t* row = reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k;
+    const int blk = kabs & ~63, p0 = kabs & 63;
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int es = BITS == 8 ? e : ((e & 4) | ((e & 1) << 1) | ((e >> 1) & 1));
+      v[e] = bf16_at(row, blk + ref_pos_natural(p0 + es));
+    }
+    return uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&mrow)[MT], int rowl) {
+    const float* sc = reinterpret_cast<const float*>(lds + a.off_sc);
+    const float* xbp = reinterpret_cast<const float*>(lds + a.off_xb);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint4 av[2];
+      if (BITS == 8) {
+        const uint4 ch = c[j];
+        const uint2 p0 = bytes_to_bf16(ch.x), p1 = bytes_to_bf16(ch.y);
+        const uint2 p2 = bytes_to_bf16(ch.z), p3 = bytes_to_bf16(ch.w);
+        av[0] = uint4{p0.x, p0.y, p1.x, p1.y};
+        av[1] = uint4{p2.x, p2.y, p3.x, p3.y};
+      } else {
+        const uint4 ch = c[0];
+        const int sh = 4 * j;
+        av[0] = uint4{nib_pair(ch.x, sh), nib_pair(ch.x, sh + 8), nib_pair(ch.y, sh), nib_pair(ch.y, sh + 8)};
+        av[1] = uint4{nib_pair(ch.z, sh), nib_pair(ch.z, sh + 8), nib_pair(ch.w, sh), nib_pair(ch.w, sh + 8)};
+      }
+      f32x4 tmp[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + u * 16);
+          tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[u]), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+        }
+      }
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + (srel * 2 + j) * a.sc_stride + rowl);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float xb = xbp[mrow[mt] * a.xb_stride + srel * 2 + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - xb, acc[mt][i]);
+      }
+    }
+  }
+  __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
+};
+
+// ---- fp8.fp8_matmul: e4m3 [n][k] weights, bf16 scale [n][k/group], bf16 activation.
+//      Step = 64 k; e4m3 -> fp32 by v_cvt_pk_f32_fp8 (exact), -> bf16 by truncation (exact).
+struct FmtFP8WO {
+  static constexpr int KSTEP = 64, LOADS = 1, NSC = 1, XBYTES = 2;
+  static constexpr float BIAS = 0.f;
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + (size_t)wrow * a.k +
+                                          step * 64 + (lane >> 4) * 16);
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int) {
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k / a.group) + (step * 64) / a.group]);
+  }
+  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
+  }
+  template <bool HI>
+  __device__ static uint32_t fp8pair(uint32_t d) {
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    const f2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, HI);
+    return pack_hi(f[0], f[1]);
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&)[MT], int rowl) {
+    const uint32_t wd[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
+    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
+    f32x4 tmp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint4 av = {fp8pair<false>(wd[2 * t]), fp8pair<true>(wd[2 * t]),
+                        fp8pair<false>(wd[2 * t + 1]), fp8pair<true>(wd[2 * t + 1])};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+      }
+    }
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(
+        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(sc[i], tmp[mt][i], acc[mt][i]);
+  }
+  __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
+};
+
+// ---- cuda_int8 W8A8: int8 [n][k] and int8 activation [m][k], both in fragment order
+//      (engine/kernels/cuda_int8.py:64, 100-108); fp16 weight scale [n][k/64], fp32
+//      activation scale [m][k/64]; per group acc = fma(float(dot) * sx, sw, acc)
+//      (engine/kernels/cuda_int8.py:198-199). Step = 64 k = one group.
+struct FmtInt8 {
+  static constexpr int KSTEP = 64, LOADS = 1, NSC = 1, XBYTES = 1;
+  static constexpr float BIAS = 0.f;
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(a.w) + (size_t)wrow * a.k +
+                                          step * 64 + (lane >> 4) * 16);
+  }
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int) {
+    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + step]);
+  }
+  template <int MT>
+  __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
+                                 const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
+                                 const int (&mrow)[MT], int rowl) {
+    const i32x4 av = {(int)c[0].x, (int)c[0].y, (int)c[0].z, (int)c[0].w};
+    const int kb = srel * 64 + (lane >> 4) * 16;
+    const f32x4 sw = *reinterpret_cast<const f32x4*>(
+        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
+      const i32x4 b = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+      const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+      const float sx = reinterpret_cast<const float*>(lds + a.off_sx)[mrow[mt] * a.xb_stride + srel];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf((float)d[i] * sx, sw[i], acc[mt][i]);
+    }
+  }
+  __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
+};
+
+// ====================================================================================
+// Prologue: stage the workgroup's activation slice (B order), its scales, bias sums.
+// ====================================================================================
+
+template <class F>
+__device__ void stage_bf16(const GemmArgs& a, char* lds, int step0, int nst) {
+  constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
+  const int cpr = nst * CPS;
+  const int total = a.m * cpr;
+  for (int q = threadIdx.x; q < total; q += blockDim.x) {
+    const int mm = q / cpr, kc = q - mm * cpr;
+    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = F::stage_chunk(a, mm, step0 * F::KSTEP + kc * 8);
+  }
+}
+
+// Bias totals per (token, scale group) from the staged activation, one MFMA chain per
+// (group, 16-token fragment), spread over the workgroup's waves. Needs the staged x.
+template <class F, int WAVES>
+__device__ void stage_bias(const GemmArgs& a, char* lds, int nst) {
+  constexpr int NJ = F::NSC > 1 ? F::NSC : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int frags = (a.m + 15) >> 4;
+  float* xb = reinterpret_cast<float*>(lds + a.off_xb);
+  for (int item = wave; item < nst * NJ * frags; item += WAVES) {
+    const int mt = item % frags, sj = item / frags;
+    const int mm = 16 * mt + (lane & 15);
+    const int mrow = min(mm, a.m - 1);
+    const f32x4 d = F::bias_chain(lds, sj / NJ, sj % NJ, lane, mrow * a.xstride);
+    if ((lane >> 4) == 0 && mm < a.m) xb[mm * a.xb_stride + sj] = d[0];
+  }
+}
+
+// FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice.
+__device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) {
+  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+  uint32_t* amax = reinterpret_cast<uint32_t*>(sx + a.m);
+  for (int i = threadIdx.x; i < a.m; i += blockDim.x) amax[i] = 0u;
+  __syncthreads();
+  const int cpr = a.k >> 3;
+  const int total = a.m * cpr;
+  int cur = -1;
+  float mx = 0.f;
+  for (int q = threadIdx.x; q < total; q += blockDim.x) {
+    const int mm = q / cpr;
+    if (mm != cur) {
+      if (cur >= 0) atomicMax(&amax[cur], __float_as_uint(mx));
+      cur = mm;
+      mx = 0.f;
+    }
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)q * 8);
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
+  }
+  if (cur >= 0) atomicMax(&amax[cur], __float_as_uint(mx));
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = fmaxf(__uint_as_float(amax[i]) / 448.f, 1e-12f);
+  __syncthreads();
+  const int cps = nst * 8;  // 8-value chunks per row of the slice
+  for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
+    const int mm = q / cps, kc = q - mm * cps;
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k +
+                                                    step0 * 64 + kc * 8);
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    const float s = sx[mm];
+    uint32_t c[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
+      c[e] = f32_to_e4m3(clamp_keep_nan(xv / s, 448.f));
+    }
+    uint2 o;
+    o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    *reinterpret_cast<uint2*>(lds + mm * a.xstride + kc * 8) = o;
+  }
+}
+
+// cuda_int8 prologue: int8 activation slice and its fp32 group scales.
+__device__ void stage_int8_act(const GemmArgs& a, char* lds, int step0, int nst) {
+  const int cps = nst * 4;
+  for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
+    const int mm = q / cps, kc = q - mm * cps;
+    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = *reinterpret_cast<const uint4*>(
+        reinterpret_cast<const int8_t*>(a.x) + (size_t)mm * a.k + step0 * 64 + kc * 16);
+  }
+  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+  for (int q = threadIdx.x; q < a.m * nst; q += blockDim.x) {
+    const int mm = q / nst, j = q - mm * nst;
+    sx[mm * a.xb_stride + j] = a.xs[(size_t)mm * (a.k >> 6) + step0 + j];
+  }
+}
+
+template <class F>
+__device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, int nst) {
+  float* sc = reinterpret_cast<float*>(lds + a.off_sc);
+  const int rows = 16 * a.rt;
+  if (F::NSC == 0) {
+    for (int rl = threadIdx.x; rl < rows; rl += blockDim.x) {
+      const int tile = tg * a.rt + (rl >> 4);
+      sc[rl] = tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), 0, 0) : 0.f;
+    }
+    return;
+  }
+  const int total = nst * F::NSC * rows;
+  for (int q = threadIdx.x; q < total; q += blockDim.x) {
+    const int sj = q / rows, rl = q - sj * rows;
+    const int tile = tg * a.rt + (rl >> 4);
+    sc[sj * a.sc_stride + rl] =
+        tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), step0 + sj / F::NSC, sj % F::NSC) : 0.f;
+  }
+}
+
+// ====================================================================================
+// The kernel.
+// ====================================================================================
+
+__device__ __forceinline__ void block_coords(const GemmArgs& a, int& tg, int& s) {
+  const int total = a.tile_groups * a.splits;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (total >= 8) {  // consecutive logical blocks (the splits of a row block) share an XCD
+    const int per = total >> 3, rem = total & 7, xcd = b & 7, idx = b >> 3;
+    logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
+  }
+  tg = logical / a.splits;
+  s = logical - tg * a.splits;
+}
+
+template <class F>
+__device__ __forceinline__ void load_chunk(uint4 (&c)[F::LOADS], const GemmArgs& a, int wrow, int step,
+                                           int lane) {
+  const uint4* p = F::chunk_ptr(a, wrow, step, lane);
+  const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  c[0] = uint4{v0[0], v0[1], v0[2], v0[3]};
+  if constexpr (F::LOADS == 2) {
+    const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(FmtRef<8>::chunk_ptr1(a, p)));
+    c[1] = uint4{v1[0], v1[1], v1[2], v1[3]};
+  }
+}
+
+template <class F, int MT, int RW, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  constexpr int PF = RW == 1 ? 8 : 4;  // steps in flight per wave
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int tg, s;
+  block_coords(a, tg, s);
+  const int step0 = s * a.sps;
+  const int nst = min(a.nsteps, step0 + a.sps) - step0;
+
+  // ---- prologue
+  if constexpr (std::is_same<F, FmtFP8>::value) {
+    stage_fp8_act(a, lds, step0, nst);
+  } else if constexpr (std::is_same<F, FmtInt8>::value) {
+    stage_int8_act(a, lds, step0, nst);
+  } else {
+    stage_bf16<F>(a, lds, step0, nst);
+  }
+  stage_scales<F>(a, lds, tg, step0, nst);
+  __syncthreads();
+  if constexpr (F::BIAS != 0.f) {
+    stage_bias<F, WAVES>(a, lds, nst);
+    __syncthreads();
+  }
+
+  // ---- main loop
+  const int wt = wave / a.kw, kwi = wave - wt * a.kw;   // tile slot, k-interleave index
+  const int tile0 = tg * a.rt + wt * RW;
+  f32x4 acc[RW][MT];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[r][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int xoff[MT], mrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    mrow[mt] = min(16 * mt + (lane & 15), a.m - 1);
+    xoff[mt] = mrow[mt] * a.xstride;
+  }
+  if (tile0 < a.ntiles) {
+    int wrow[RW];
+    bool live[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      live[r] = tile0 + r < a.ntiles;
+      wrow[r] = weight_row(a, live[r] ? tile0 + r : tile0, lane & 15);
+    }
+    const int my = (nst - kwi + a.kw - 1) / a.kw;  // steps of this wave: kwi, kwi + kw, ...
+    uint4 buf[PF][RW][F::LOADS];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (p < my)
+#pragma unroll
+        for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + p * a.kw, lane);
+    for (int j0 = 0; j0 < my; j0 += PF) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int j = j0 + p;
+        if (j < my) {
+          uint4 cur[RW][F::LOADS];
+#pragma unroll
+          for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int l = 0; l < F::LOADS; ++l) cur[r][l] = buf[p][r][l];
+          if (j + PF < my)
+#pragma unroll
+            for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + (j + PF) * a.kw, lane);
+          const int srel = kwi + j * a.kw;
+#pragma unroll
+          for (int r = 0; r < RW; ++r)
+            if (live[r])
+              F::template compute<MT>(acc[r], cur[r], lds, a, srel, lane, xoff, mrow,
+                                      (wt * RW + r) * 16 + 4 * (lane >> 4));
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: combine the kw waves of each tile through LDS
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);  // [wave][RW][16 rows][16*MT]
+  constexpr int RC = 16 * MT;
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[((wave * RW + r) * 16 + 4 * (lane >> 4) + i) * RC + 16 * mt + (lane & 15)] = acc[r][mt][i];
+  __syncthreads();
+
+  auto combined = [&](int tl, int nl, int mm) -> float {
+    const int slot = tl / RW, r = tl - slot * RW;  // tile tl of the block = slot's r-th tile
+    float v = 0.f;
+    for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
+    return F::finish(a, lds, v, tl * 16 + nl, mm);
+  };
+
+  const int rows_out = a.mode == QLX_MODE_SWIGLU ? 8 : 16;
+  const int per_tile = rows_out * a.m;
+  const int total = a.rt * per_tile;
+  const bool direct = a.splits == 1 || a.mode == QLX_MODE_PLANES;
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int tl = idx / per_tile, rem = idx - tl * per_tile;
+    const int mm = rem / rows_out, nl = rem - mm * rows_out;
+    const int tile = tg * a.rt + tl;
+    if (tile >= a.ntiles) continue;
+    if (a.mode == QLX_MODE_SWIGLU) {
+      const float g = combined(tl, nl, mm), u = combined(tl, nl + 8, mm);
+      if (direct) {
+        const float gb = round_bf(g), ub = round_bf(u);
+        y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
+      } else {
+        float* pl = a.work + ((size_t)s * a.m + mm) * a.n;
+        pl[8 * tile + nl] = g;
+        pl[a.half + 8 * tile + nl] = u;
+      }
+    } else {
+      const float v = combined(tl, nl, mm);
+      const int row = 16 * tile + nl;
+      if (a.mode == QLX_MODE_PLANES || !direct)
+        a.work[((size_t)s * a.m + mm) * a.n + row] = v;
+      else
+        y[(size_t)mm * a.n + row] = f2bf(v);
+    }
+  }
+  if (direct) return;
+
+  // ---- split-K: the last workgroup of this row block reduces the planes in slice order
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(&a.tickets[tg], 1);
+    s_last = prev == a.splits - 1;
+    if (s_last) a.tickets[tg] = 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const size_t plane = (size_t)a.m * a.n;
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int tl = idx / per_tile, rem = idx - tl * per_tile;
+    const int mm = rem / rows_out, nl = rem - mm * rows_out;
+    const int tile = tg * a.rt + tl;
+    if (tile >= a.ntiles) continue;
+    if (a.mode == QLX_MODE_SWIGLU) {
+      const float* pg = a.work + (size_t)mm * a.n + 8 * tile + nl;
+      float g = 0.f, u = 0.f;
+      for (int sp = 0; sp < a.splits; ++sp) {
+        g += __builtin_nontemporal_load(pg + sp * plane);
+        u += __builtin_nontemporal_load(pg + sp * plane + a.half);
+      }
+      const float gb = round_bf(g), ub = round_bf(u);
+      y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
+    } else {
+      const int row = 16 * tile + nl;
+      const float* p = a.work + (size_t)mm * a.n + row;
+      float v = 0.f;
+      for (int sp = 0; sp < a.splits; ++sp) v += __builtin_nontemporal_load(p + sp * plane);
+      y[(size_t)mm * a.n + row] = f2bf(v);
+    }
+  }
+}
+
+}  // namespace qlx

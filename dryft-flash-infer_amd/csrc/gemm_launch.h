@@ -1,0 +1,104 @@
+// Host side of the quantized GEMM: plan validation, LDS layout, template dispatch.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm.h"
+
+namespace qlx {
+
+// Dynamic LDS kept per workgroup; two workgroups of 4 waves then fit one CU.
+constexpr int kLdsLimit = 64 * 1024;
+
+struct FmtInfo {
+  int kstep, nsc, xbytes, bias;
+};
+
+template <class F>
+constexpr FmtInfo info() {
+  return FmtInfo{F::KSTEP, F::NSC, F::XBYTES, F::BIAS != 0.f};
+}
+
+inline int round16(int v) { return (v + 15) & ~15; }
+
+// Fill the derived fields of GemmArgs for (plan, shape); returns total LDS bytes or -1.
+inline int layout(const FmtInfo& fi, const qlx_plan& p, int m, int n, int k, GemmArgs& a) {
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.mode = p.mode;
+  a.nsteps = k / fi.kstep;
+  a.sps = (a.nsteps + p.splits - 1) / p.splits;
+  a.splits = (a.nsteps + a.sps - 1) / a.sps;
+  a.ntiles = n / 16;  // SwiGLU tiles hold 8 gate + 8 up rows: (n/2)/8 = n/16 as well
+  a.kw = p.kw;
+  a.rt = (p.waves / p.kw) * p.rw;
+  a.tile_groups = (a.ntiles + a.rt - 1) / a.rt;
+  a.half = n / 2;
+  const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  a.xstride = round16(a.sps * fi.kstep * fi.xbytes + 16);
+  const int xbytes = m * a.xstride;
+  const int red = p.waves * p.rw * 16 * 16 * mt * 4;
+  a.off_sc = round16(xbytes > red ? xbytes : red);
+  a.sc_stride = 16 * a.rt;
+  const int sc_floats = fi.nsc == 0 ? a.sc_stride : a.sps * fi.nsc * a.sc_stride;
+  a.off_xb = round16(a.off_sc + sc_floats * 4);
+  a.xb_stride = a.sps * (fi.nsc > 1 ? fi.nsc : 1);
+  const int xb_floats = fi.bias ? m * a.xb_stride : 0;
+  a.off_sx = round16(a.off_xb + xb_floats * 4);
+  return a.off_sx + m * (a.xb_stride > 2 ? a.xb_stride : 2) * 4;
+}
+
+inline int check_plan(const qlx_plan* p, int m, int n, int k, int kstep) {
+  QLX_REQUIRE(p != nullptr, "plan is NULL");
+  QLX_REQUIRE(m >= 1 && m <= 64, "m=%d must be in 1..64", m);
+  QLX_REQUIRE(n >= 16 && n % 16 == 0, "n=%d must be a positive multiple of 16", n);
+  QLX_REQUIRE(k >= kstep && k % kstep == 0, "K=%d must be a positive multiple of %d", k, kstep);
+  QLX_REQUIRE(p->mode >= 0 && p->mode <= 2, "bad mode %d", p->mode);
+  QLX_REQUIRE(p->waves == 4 || p->waves == 8, "waves must be 4 or 8");
+  QLX_REQUIRE(p->kw >= 1 && p->waves % p->kw == 0, "kw must divide waves");
+  QLX_REQUIRE(p->rw == 1 || p->rw == 2, "rw must be 1 or 2");
+  QLX_REQUIRE(p->splits >= 1, "splits must be >= 1");
+  return QLX_OK;
+}
+
+template <class F, int MT, int RW, int WAVES>
+hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
+  const int grid = a.tile_groups * a.splits;
+  gemm_kernel<F, MT, RW, WAVES><<<grid, WAVES * 64, lds, st>>>(a);
+  return hipGetLastError();
+}
+
+template <class F, int MT>
+hipError_t launch_mt(const GemmArgs& a, const qlx_plan& p, int lds, hipStream_t st) {
+  if (p.waves == 4) return p.rw == 1 ? launch_one<F, MT, 1, 4>(a, lds, st) : launch_one<F, MT, 2, 4>(a, lds, st);
+  return p.rw == 1 ? launch_one<F, MT, 1, 8>(a, lds, st) : launch_one<F, MT, 2, 8>(a, lds, st);
+}
+
+template <class F>
+int launch_gemm(const char* name, GemmArgs a, const qlx_plan* plan, int m, int n, int k, void* stream) {
+  int rc = check_plan(plan, m, n, k, F::KSTEP);
+  if (rc) return rc;
+  const qlx_plan& p = *plan;
+  const int lds = layout(info<F>(), p, m, n, k, a);
+  QLX_REQUIRE(lds <= kLdsLimit, "%s: plan needs %d bytes of LDS (> %d); use more splits", name, lds, kLdsLimit);
+  QLX_REQUIRE(p.mode != QLX_MODE_PLANES || a.splits == p.splits,
+              "%s: %d splits over %d steps leave %d non-empty planes", name, p.splits, a.nsteps, a.splits);
+  if (p.mode == QLX_MODE_PLANES || a.splits > 1)
+    QLX_REQUIRE(p.workspace != nullptr, "%s: split-K needs a workspace", name);
+  if (p.mode != QLX_MODE_PLANES && a.splits > 1) QLX_REQUIRE(p.tickets != nullptr, "%s: split-K needs tickets", name);
+  a.work = p.workspace;
+  a.tickets = p.tickets;
+  const int mt = (m + 15) / 16;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (mt == 1)
+    e = launch_mt<F, 1>(a, p, lds, st);
+  else if (mt == 2)
+    e = launch_mt<F, 2>(a, p, lds, st);
+  else
+    e = launch_mt<F, 4>(a, p, lds, st);
+  return hip_status(e, name);
+}
+
+}  // namespace qlx

@@ -1,0 +1,12 @@
+// W4A16 group-128 linear (int32 k32 words, bf16 scales): instantiations and C entry point.
+#include "gemm_launch.h"
+
+extern "C" int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y, int m,
+                                int n, int k, const qlx_plan* plan, void* stream) {
+  qlx::GemmArgs a = {};
+  a.w = w;
+  a.ws = w_scale;
+  a.x = x;
+  a.y = y;
+  return qlx::launch_gemm<qlx::FmtW4>("linear_w4a16", a, plan, m, n, k, stream);
+}

@@ -1,0 +1,12 @@
+// W8A16 per-output-channel linear (signed int8, bf16 scales): instantiations and C entry point.
+#include "gemm_launch.h"
+
+extern "C" int qlx_linear_w8a16(const void* w, const void* w_scale, const void* x, void* y, int m,
+                                int n, int k, const qlx_plan* plan, void* stream) {
+  qlx::GemmArgs a = {};
+  a.w = w;
+  a.ws = w_scale;
+  a.x = x;
+  a.y = y;
+  return qlx::launch_gemm<qlx::FmtW8>("linear_w8a16", a, plan, m, n, k, stream);
+}

@@ -1,0 +1,131 @@
+"""ctypes binding of ``libqlinear.so`` (declared in ``include/qlinear.h``).
+
+The reference reaches its kernels the same way -- ctypes into a native loader
+(engine/kernels/cuda_jit.py:141-289) -- so this module is the MI355X counterpart
+of ``cuda_jit``: it loads one prebuilt gfx950 library instead of compiling CUDA at
+run time. There is no fallback: without the library every op raises.
+"""
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library then shares)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqlinear.so")
+
+QLX_OK, QLX_EINVAL, QLX_EHIP = 0, -1, -2
+MODE_BF16, MODE_PLANES, MODE_SWIGLU = 0, 1, 2
+SCALE_F16, SCALE_BF16 = 0, 1
+STORE_OFFSET, STORE_SIGNED, STORE_K32 = 0, 1, 2
+FMT_W8A16, FMT_W4A16, FMT_FP8, FMT_REF8, FMT_REF4, FMT_FP8WO, FMT_INT8 = range(7)
+
+
+class Plan(ctypes.Structure):
+    """``qlx_plan``: mode, splits, waves, kw, rw, workspace, tickets."""
+
+    _fields_ = [
+        ("mode", ctypes.c_int), ("splits", ctypes.c_int), ("waves", ctypes.c_int),
+        ("kw", ctypes.c_int), ("rw", ctypes.c_int),
+        ("workspace", ctypes.c_void_p), ("tickets", ctypes.c_void_p),
+    ]
+
+
+_P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
+_PLAN = ctypes.POINTER(Plan)
+
+#: Every exported entry point and its argument types (the header's declarations).
+SIGNATURES = {
+    "qlx_last_error": ([], ctypes.c_char_p),
+    "qlx_abi_version": ([], _I),
+    "qlx_quantize_weight": ([_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qlx_dequantize": ([_P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qlx_prepare_ref": ([_P, _P, _I, _I, _I, _I, _P], _I),
+    "qlx_row_major_ref": ([_P, _P, _I, _I, _P], _I),
+    "qlx_quantize_fp8_weight": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "qlx_quantize_fp8_act": ([_P, _P, _P, _I, _I, _P], _I),
+    "qlx_int8_prepare": ([_P, _P, _I, _I, _P], _I),
+    "qlx_quantize_act_int8": ([_P, _P, _P, _I, _I, _P], _I),
+    "qlx_plan_linear": ([_I, _I, _I, _I, _I, _PLAN], _I),
+    "qlx_plan_tickets": ([_PLAN, _I, _I, _I, _I], _I),
+    "qlx_linear_w8a16": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_fp8wo": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_int8": ([_P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_reduce_planes": ([_P, _P, _LL, _I, _P], _I),
+    "qlx_residual_planes": ([_P, _P, _P, _LL, _I, _P], _I),
+    "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),
+    "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises RuntimeError if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(there is no CPU or Python fallback for these ops)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def last_error():
+    return lib().qlx_last_error().decode(errors="replace")
+
+
+def check(rc, what):
+    """Map a status to the reference's conventions: ValueError for contract violations,
+    RuntimeError for runtime failures (engine/kernels/cuda_jit.py:43-45)."""
+    if rc == QLX_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == QLX_EINVAL:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name, *args):
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_device(*tensors):
+    """The ops run only on a ROCm device; CPU tensors are a contract violation."""
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("quantized linear ops need tensors on a ROCm GPU (no CPU path)")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("tensors must be contiguous")
+
+
+_tickets = {}
+
+
+def tickets(device, count):
+    """Per-device ticket counters for split-K, zero between calls (kernels reset them)."""
+    index = torch.device(device).index or 0
+    buf = _tickets.get(index)
+    if buf is None or buf.numel() < count:
+        size = max(count, 1 << 16)
+        buf = torch.zeros(size, dtype=torch.int32, device=device)
+        _tickets[index] = buf
+    return buf

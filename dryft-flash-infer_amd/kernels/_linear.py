@@ -1,0 +1,65 @@
+"""Shared host logic of every quantized linear: plan, workspace, tickets, launch.
+
+A config is ``(waves, kw, rw, splits)``: waves per workgroup (4 or 8), waves splitting
+one 16-row tile's K range, 16-row tiles per wave, and K slices across workgroups.
+``None`` takes the library's default for the shape (``qlx_plan_linear``).
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def make_plan(fmt, mode, m, n, k, config=None):
+    plan = _lib.Plan()
+    if config is None:
+        _lib.check(_lib.lib().qlx_plan_linear(fmt, mode, m, n, k, plan), "plan_linear")
+        return plan
+    waves, kw, rw, splits = config
+    plan.mode, plan.waves, plan.kw, plan.rw, plan.splits = mode, waves, kw, rw, splits
+    return plan
+
+
+def effective_splits(fmt, kstep, k, splits):
+    """Non-empty K slices for a requested split count (every slice holds >= 1 step)."""
+    steps = k // kstep
+    per = -(-steps // max(1, min(splits, steps)))
+    return -(-steps // per)
+
+
+KSTEP = {_lib.FMT_W8A16: 64, _lib.FMT_W4A16: 128, _lib.FMT_FP8: 64, _lib.FMT_REF8: 128,
+         _lib.FMT_REF4: 128, _lib.FMT_FP8WO: 64, _lib.FMT_INT8: 64}
+
+
+def run(fmt, entry, x, n, k, args_before_y, args_after_dims=(), mode=_lib.MODE_BF16, config=None,
+        m=None):
+    """Launch ``entry(*args_before_y, y, m, n, k, *args_after_dims, plan, stream)``.
+
+    Returns bf16 ``[m, n]`` (``[m, n/2]`` for SwiGLU) or fp32 planes ``[splits, m, n]``.
+    """
+    m = x.shape[0] if m is None else m
+    device = x.device
+    plan = make_plan(fmt, mode, m, n, k, config)
+    splits = effective_splits(fmt, KSTEP[fmt], k, plan.splits)
+    if mode == _lib.MODE_PLANES:
+        plan.splits = splits
+        out = torch.empty((splits, m, n), dtype=torch.float32, device=device)
+        plan.workspace = out.data_ptr()
+    else:
+        width = n // 2 if mode == _lib.MODE_SWIGLU else n
+        out = torch.empty((m, width), dtype=torch.bfloat16, device=device)
+        if splits > 1:
+            work = torch.empty((splits, m, n), dtype=torch.float32, device=device)
+            plan.workspace = work.data_ptr()
+            count = _lib.lib().qlx_plan_tickets(plan, fmt, m, n, k)
+            plan.tickets = _lib.tickets(device, count).data_ptr()
+    _lib.call(entry, *args_before_y, _lib.ptr(out), m, n, k, *args_after_dims,
+              ctypes.byref(plan), _lib.stream(device))
+    return out
+
+
+def splits_for(fmt, mode, m, n, k, config=None):
+    plan = make_plan(fmt, mode, m, n, k, config)
+    return effective_splits(fmt, KSTEP[fmt], k, plan.splits)

@@ -1,0 +1,163 @@
+"""The north-star quantized formats: W8A16 per channel, W4A16 group 128, FP8 W8A8.
+
+Each format is the reference's quantizer (engine/kernels/cuda_fp8.py:1127-1151,
+engine/kernels/fp8.py:20-28) with documented substitutions, and each linear is a drop-in
+for the ``cuda_fp8.matmul`` call the engine makes per projection
+(engine/engine.py:881-884):
+
+* W8A16: ``cuda_fp8.quantize(w, group=K, bits=8)`` with bf16 scales and signed int8
+  storage -> ``(int8 [N, K], bf16 [N])``.
+* W4A16: ``cuda_fp8.quantize(w, group=128, bits=4)`` with bf16 scales; codes ``q + 8``
+  packed eight per int32 along K, nibble i of word j holding k = 8j + i ->
+  ``(int32 [N, K/8], bf16 [N, K/128])``.
+* FP8 W8A8: ``fp8.quantize(w, group=K)`` -> ``(e4m3 [N, K], bf16 [N])``; the activation
+  is quantized per token inside the linear: ``s = max(amax/448, 1e-12)`` (fp32),
+  ``e4m3(clamp(x/s, +-448))``.
+
+All work runs in the gfx950 library; tensors must be on the GPU.
+"""
+
+import torch
+
+from . import _lib, _linear
+
+
+def _bf16_2d(t, what):
+    if t.dtype != torch.bfloat16 or t.dim() != 2:
+        raise ValueError(f"{what} must be a 2-D bfloat16 tensor")
+    _lib.require_device(t)
+
+
+# ---- quantize / pack ------------------------------------------------------------------
+
+def quantize_w8(weight):
+    """bf16 ``[N, K]`` -> (int8 ``[N, K]``, bf16 per-channel scales ``[N]``)."""
+    _bf16_2d(weight, "weight")
+    n, k = weight.shape
+    if k % 8:
+        raise ValueError(f"K={k} must be a multiple of 8")
+    q = torch.empty((n, k), dtype=torch.int8, device=weight.device)
+    s = torch.empty((n, 1), dtype=torch.bfloat16, device=weight.device)
+    _lib.call("qlx_quantize_weight", _lib.ptr(weight), _lib.ptr(q), _lib.ptr(s), n, k, k, 8,
+              _lib.SCALE_BF16, 1, _lib.STORE_SIGNED, _lib.stream(weight.device))
+    return q, s.view(n)
+
+
+def quantize_w4(weight, group=128):
+    """bf16 ``[N, K]`` -> (int32 k32 words ``[N, K/8]``, bf16 scales ``[N, K/group]``)."""
+    _bf16_2d(weight, "weight")
+    n, k = weight.shape
+    if k % group or group % 8:
+        raise ValueError(f"{k} is not a multiple of {group}")
+    q = torch.empty((n, k // 8), dtype=torch.int32, device=weight.device)
+    s = torch.empty((n, k // group), dtype=torch.bfloat16, device=weight.device)
+    _lib.call("qlx_quantize_weight", _lib.ptr(weight), _lib.ptr(q), _lib.ptr(s), n, k, group, 4,
+              _lib.SCALE_BF16, 1, _lib.STORE_K32, _lib.stream(weight.device))
+    return q, s
+
+
+def quantize_fp8(weight):
+    """bf16 ``[N, K]`` -> (e4m3 ``[N, K]`` as ``torch.float8_e4m3fn``, bf16 scales ``[N]``)."""
+    _bf16_2d(weight, "weight")
+    n, k = weight.shape
+    if k % 8:
+        raise ValueError(f"K={k} must be a multiple of 8")
+    q = torch.empty((n, k), dtype=torch.uint8, device=weight.device)
+    s = torch.empty((n, 1), dtype=torch.bfloat16, device=weight.device)
+    _lib.call("qlx_quantize_fp8_weight", _lib.ptr(weight), _lib.ptr(q), _lib.ptr(s), n, k, k,
+              _lib.stream(weight.device))
+    return q.view(torch.float8_e4m3fn), s.view(n)
+
+
+def quantize_fp8_activation(x):
+    """bf16 ``[M, K]`` -> (e4m3 ``[M, K]``, fp32 per-token scales ``[M]``)."""
+    _bf16_2d(x, "activation")
+    m, k = x.shape
+    if k % 8:
+        raise ValueError(f"K={k} must be a multiple of 8")
+    q = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    _lib.call("qlx_quantize_fp8_act", _lib.ptr(x), _lib.ptr(q), _lib.ptr(s), m, k, _lib.stream(x.device))
+    return q.view(torch.float8_e4m3fn), s
+
+
+def dequantize_w8(packed):
+    q, s = packed
+    n, k = q.shape
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=q.device)
+    _lib.call("qlx_dequantize", _lib.ptr(q), _lib.ptr(s), _lib.ptr(out), n, k, 1, 8,
+              _lib.SCALE_BF16, _lib.STORE_SIGNED, _lib.stream(q.device))
+    return out
+
+
+def dequantize_w4(packed):
+    q, s = packed
+    n, k = q.shape[0], q.shape[1] * 8
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=q.device)
+    _lib.call("qlx_dequantize", _lib.ptr(q), _lib.ptr(s), _lib.ptr(out), n, k, s.shape[1], 4,
+              _lib.SCALE_BF16, _lib.STORE_K32, _lib.stream(q.device))
+    return out
+
+
+# ---- linears ---------------------------------------------------------------------------
+
+def _check_x(x, k):
+    _bf16_2d(x, "activation")
+    if x.shape[1] != k:
+        raise ValueError("activation width does not match the weight")
+    if not 1 <= x.shape[0] <= 64:
+        raise ValueError(f"batch {x.shape[0]} exceeds 64 rows")
+
+
+def _mode(swiglu=False, planes=False):
+    return _lib.MODE_SWIGLU if swiglu else (_lib.MODE_PLANES if planes else _lib.MODE_BF16)
+
+
+def linear_w8a16(x, packed, config=None, planes=False, swiglu=False):
+    """``x @ deq(W).T`` for W8A16 per-channel weights; bf16 ``[M, N]`` (SwiGLU: ``[M, N/2]``)."""
+    q, s = packed
+    n, k = q.shape
+    _check_x(x, k)
+    _lib.require_device(q, s)
+    return _linear.run(_lib.FMT_W8A16, "qlx_linear_w8a16", x, n, k,
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+
+
+def linear_w4a16(x, packed, config=None, planes=False, swiglu=False):
+    """``x @ deq(W).T`` for W4A16 group-128 weights."""
+    q, s = packed
+    n, k = q.shape[0], q.shape[1] * 8
+    _check_x(x, k)
+    _lib.require_device(q, s)
+    if q.dtype != torch.int32 or s.shape != (n, k // 128):
+        raise ValueError("W4A16 weights are int32 [N, K/8] with bf16 scales [N, K/128]")
+    return _linear.run(_lib.FMT_W4A16, "qlx_linear_w4a16", x, n, k,
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+
+
+def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False):
+    """``(x_q s_x) @ (W_q s_w).T`` with the activation quantized per token in the kernel."""
+    q, s = packed
+    n, k = q.shape
+    _check_x(x, k)
+    _lib.require_device(q, s)
+    return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8", x, n, k,
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+
+
+def splits(fmt, m, n, k, config=None, swiglu=False):
+    """How many fp32 planes a linear of this shape and config reduces."""
+    return _linear.splits_for(fmt, _mode(swiglu), m, n, k, config)
+
+
+FORMATS = {
+    "w8a16": (quantize_w8, linear_w8a16, _lib.FMT_W8A16),
+    "w4a16": (quantize_w4, linear_w4a16, _lib.FMT_W4A16),
+    "fp8": (quantize_fp8, linear_fp8_w8a8, _lib.FMT_FP8),
+}
+
+
+def weight_bytes(packed):
+    """Bytes a linear streams for its weight (codes + scales)."""
+    q, s = packed
+    return q.numel() * q.element_size() + s.numel() * s.element_size()

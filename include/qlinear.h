@@ -1,0 +1,187 @@
+/*
+ * qlinear.h -- C ABI of the MI355X (gfx950) quantized decode linear-layer library.
+ *
+ * Plain pointers and sizes only. Every pointer argument is device memory (HBM) unless
+ * it says otherwise; `stream` is a hipStream_t (NULL = the default stream). No entry
+ * point allocates, synchronises or reads device memory on the host, so every call is
+ * safe to capture into a hipGraph. Each returns QLX_OK (0) or a negative status;
+ * qlx_last_error() then holds a message (thread-local).
+ *
+ * Number formats travel as raw bits: bf16 and fp16 as uint16, OCP e4m3fn as one byte.
+ *
+ * The reference binds its kernels through ctypes to the CUDA driver
+ * (engine/kernels/cuda_jit.py:141-289, cuLaunchKernel with arrays of c_void_p/c_int);
+ * each function below replaces one Python-level operator of engine/kernels, cited per
+ * entry. The Python shims in dryft-flash-infer_amd/kernels keep the reference names.
+ */
+#ifndef QLINEAR_H
+#define QLINEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QLX_ABI_VERSION 1
+
+/* status codes */
+#define QLX_OK 0
+#define QLX_EINVAL (-1) /* contract violation, detected before any launch */
+#define QLX_EHIP (-2)   /* HIP runtime error */
+
+/* scale_kind */
+#define QLX_SCALE_F16 0
+#define QLX_SCALE_BF16 1
+
+/* storage */
+#define QLX_STORE_OFFSET 0 /* q + offset (128 or 8) as one uint8 per value */
+#define QLX_STORE_SIGNED 1 /* q as int8 */
+#define QLX_STORE_K32 2    /* int4 codes q + 8, eight per int32 along K: nibble i of word j is k = 8j+i */
+
+/* linear modes */
+#define QLX_MODE_BF16 0   /* y[m][n] bf16 */
+#define QLX_MODE_PLANES 1 /* fp32 split-K planes [splits][m][n], not reduced */
+#define QLX_MODE_SWIGLU 2 /* weight rows = [gate; up] (2I), y[m][i] = bf16(bf16(silu(g)) * u) */
+
+/* Launch plan of a linear call. `splits` K-slices run as separate workgroups; with
+ * splits > 1 and mode != PLANES the last workgroup of each row block sums the slices in
+ * slice order (deterministic) from `workspace` ([splits][m][n] fp32) and finishes the
+ * epilogue, using `tickets` (>= qlx_plan_tickets(plan) int32, zero before the first call;
+ * every call leaves them zero again). Calls that share `tickets` must not overlap. */
+typedef struct qlx_plan {
+  int mode;         /* QLX_MODE_* */
+  int splits;       /* K slices, >= 1 */
+  int waves;        /* waves per workgroup: 4 or 8 */
+  int kw;           /* waves per 16-row tile (1, 2, 4 or 8; divides waves) */
+  int rw;           /* 16-row tiles per wave (1 or 2), reusing each activation fragment */
+  float* workspace; /* fp32 [splits][m][n] (mode PLANES: the output planes) */
+  int* tickets;     /* per-row-block counters */
+} qlx_plan;
+
+const char* qlx_last_error(void);
+int qlx_abi_version(void);
+
+/* ---- quantize / pack / relayout (load time) ------------------------------------- */
+
+/* Symmetric absmax weight quantize of bf16 w[rows][k], one scale per `group` values.
+ * Replaces cuda_fp8.quantize (engine/kernels/cuda_fp8.py:1127-1151): the defaults of that
+ * function are scale_kind=F16, nudge=1, storage=OFFSET. The north-star formats are
+ * W8A16 per-channel (group=k, BF16, SIGNED) and W4A16 (group=128, BF16, K32).
+ * data: uint8/int8 [rows][k], or int32 [rows][k/8] for K32; scale: [rows][k/group]. */
+int qlx_quantize_weight(const void* w, void* data, void* scale, int rows, int k, int group,
+                        int bits, int scale_kind, int nudge, int storage, void* stream);
+
+/* bf16((q - offset) * scale) -> out[rows][k]. Replaces cuda_fp8.dequantize
+ * (engine/kernels/cuda_fp8.py:1154-1161). */
+int qlx_dequantize(const void* data, const void* scale, void* out, int rows, int k, int groups,
+                   int bits, int scale_kind, int storage, void* stream);
+
+/* cuda_fp8.Prepared weight layout (engine/kernels/cuda_fp8.py:1164-1205): tiled 8-bit,
+ * row-major fragment-permuted 8-bit (tiled=0), or tiled 4-bit nibbles. */
+int qlx_prepare_ref(const void* data, void* out, int rows, int k, int bits, int tiled, void* stream);
+
+/* Prepared.row_major for the tiled 8-bit layout (engine/kernels/cuda_fp8.py:1207-1214). */
+int qlx_row_major_ref(const void* weight, void* out, int rows, int k, void* stream);
+
+/* E4M3 weight quantize, bf16 scales per `group` (engine/kernels/fp8.py:20-28).
+ * group = k is the per-output-channel FP8 W8A8 weight. */
+int qlx_quantize_fp8_weight(const void* w, void* code, void* scale, int rows, int k, int group,
+                            void* stream);
+
+/* Dynamic per-token e4m3 activation quantize: scale[m] = max(amax/448, 1e-12) (fp32),
+ * code = e4m3(clamp(x/scale, +-448)). The W8A8 path of cuda_int8.quantize_activation
+ * (engine/kernels/cuda_int8.py:58-88) with the north star's FP8 per-token granularity. */
+int qlx_quantize_fp8_act(const void* x, void* code, float* scale, int m, int k, void* stream);
+
+/* cuda_int8.Prepared weight (engine/kernels/cuda_int8.py:100-108) from the fragment-permuted
+ * row-major bytes. */
+int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void* stream);
+
+/* cuda_int8.quantize_activation, one component (engine/kernels/cuda_int8.py:58-88):
+ * q int8 [m][k] in fragment order, scale fp32 [m][k/64]. */
+int qlx_quantize_act_int8(const void* x, void* q, float* scale, int m, int k, void* stream);
+
+/* ---- linear layers: y = x . W^T (x bf16 [m][k] unless stated) ------------------------ */
+
+/* Default plan for a linear call (the selection the reference races in
+ * engine/kernels/gemm.py:134-261 / cuda_fp8._plan:1255-1276). fmt is one of QLX_FMT_*. */
+#define QLX_FMT_W8A16 0   /* int8 [n][k] signed, bf16 scale [n] */
+#define QLX_FMT_W4A16 1   /* int32 [n][k/8] k32 codes, bf16 scale [n][k/128] */
+#define QLX_FMT_FP8 2     /* e4m3 [n][k], bf16 scale [n], x quantized per token in-kernel */
+#define QLX_FMT_REF8 3    /* cuda_fp8 8-bit: offset bytes, fp16 scale [n][k/64] */
+#define QLX_FMT_REF4 4    /* cuda_fp8 4-bit tiled nibbles, fp16 scale [n][k/64] */
+#define QLX_FMT_FP8WO 5   /* fp8.fp8_matmul: e4m3 [n][k], bf16 scale [n][k/group], x bf16 */
+#define QLX_FMT_INT8 6    /* cuda_int8: int8 [n][k] fragment order, fp16 scale [n][k/64] */
+int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan* plan);
+int qlx_plan_tickets(const qlx_plan* plan, int fmt, int m, int n, int k);
+
+/* W8A16 per output channel. Replaces the W8A16 call of cuda_fp8.matmul
+ * (engine/kernels/cuda_fp8.py:1316-1330) for the north-star per-channel format. */
+int qlx_linear_w8a16(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                     int k, const qlx_plan* plan, void* stream);
+
+/* W4A16, group-128 bf16 scales, int32 k32 words. Replaces cuda_fp8.matmul / matmul_partials /
+ * gate_up_swiglu at bits=4 (engine/kernels/cuda_fp8.py:1307-1330, 1381-1390). */
+int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                     int k, const qlx_plan* plan, void* stream);
+
+/* FP8 e4m3 W8A8: per-channel bf16 weight scales, activation quantized per token inside the
+ * kernel (same arithmetic as qlx_quantize_fp8_act). Replaces cuda_int8.matmul's role
+ * (engine/kernels/cuda_int8.py:251-281) for the north-star FP8 format. */
+int qlx_linear_fp8_w8a8(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                        int k, const qlx_plan* plan, void* stream);
+
+/* cuda_fp8.matmul / matmul_partials / gate_up_swiglu on the reference's own Prepared weights
+ * (engine/kernels/cuda_fp8.py:1279-1330, 1381-1390): bits 8 (tiled or row-major) or 4. */
+int qlx_linear_ref(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                   int k, int bits, int tiled, const qlx_plan* plan, void* stream);
+
+/* fp8.fp8_matmul: E4M3 weights with bf16 scales per `group` along K, bf16 activations
+ * (engine/kernels/fp8.py:121-150). */
+int qlx_linear_fp8wo(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                     int k, int group, const qlx_plan* plan, void* stream);
+
+/* cuda_int8.matmul_quantized (engine/kernels/cuda_int8.py:251-276): int8 weights and
+ * activations in fragment order, fp16 weight scales [n][k/64], fp32 activation scales
+ * [m][k/64]. */
+int qlx_linear_int8(const void* w, const void* w_scale, const void* xq, const float* x_scale,
+                    void* y, int m, int n, int k, const qlx_plan* plan, void* stream);
+
+/* ---- split-K plane consumers and epilogues ----------------------------------------- */
+
+/* out[i] = bf16(sum_s planes[s][i]), s in order. Replaces the reduce_partials kernel of
+ * cuda_fp8.matmul (engine/kernels/cuda_fp8.py:965-981, 1324-1330). */
+int qlx_reduce_planes(const float* planes, void* out, long long width, int splits, void* stream);
+
+/* out[i] = bf16(x[i] + bf16(sum_s planes[s][i])). Replaces cuda_small.residual_partials
+ * (engine/kernels/cuda_small.py:43-55, 154-160). */
+int qlx_residual_planes(const void* x, const float* planes, void* out, long long width, int splits,
+                        void* stream);
+
+/* Residual add then RMSNorm over rows of n: res = bf16(x + delta) with delta bf16 [rows][n]
+ * or bf16(sum of fp32 planes [splits][rows][n]); y = bf16(bf16(res * rsqrt(mean res^2 + eps)) * w).
+ * delta = planes = NULL gives plain RMSNorm of x (res untouched). Replaces norm.add_rms_norm,
+ * add_rms_norm_partials, rms_norm (engine/kernels/reference.py:13-28, norm.py:125-154,
+ * cuda_small.py:57-87, 145-165). */
+int qlx_add_rms_norm(const void* x, const void* delta, const float* planes, int splits, const void* w,
+                     void* res, void* y, int rows, int n, float eps, void* stream);
+
+/* Residual + RMSNorm + INT8 activation quantize (per 64-group, fragment order).
+ * Replaces cuda_int8.add_norm_quant (engine/kernels/cuda_int8.py:17-55). */
+int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* planes, int splits,
+                            const void* w, void* res, void* q, float* q_scale, int rows, int n, float eps,
+                            void* stream);
+
+/* out[r][i] = bf16(bf16(silu(g)) * u) from bf16 gate_up [rows][2I] or fp32 planes
+ * [splits][rows][2I] (g and u rounded to bf16 after the plane sum). Replaces swiglu.swiglu,
+ * swiglu.swiglu_partials, cuda_small.swiglu_partials (engine/kernels/swiglu.py:12-64,
+ * cuda_small.py:89-110). */
+int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, int rows, int inter,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLINEAR_H */

@@ -1,0 +1,207 @@
+"""GPU parity of the north-star formats (W8A16, W4A16 g128, FP8 W8A8) against the CPU oracle.
+
+Quantize and pack must be bit-exact; linear outputs must be within relative L2 1e-2 of
+the reference's dequantize-then-matmul and close to the exact
+per-group statement of what the kernel computes. Every call goes through the C ABI.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from kernels import _lib, qlinear
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def bits16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def weights(n, k, seed, std=0.02, edge=True):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * std).to(torch.bfloat16)
+    if edge and n >= 8:
+        w[0].zero_()
+        w[1] = (torch.randn(k, generator=g) * 1e-9).to(torch.bfloat16)
+        w[2] = (torch.randn(k, generator=g) * 300.0).to(torch.bfloat16)
+        w[3, : k // 2] = 0
+    return w
+
+
+def acts(m, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(m, k, generator=g).to(torch.bfloat16)
+
+
+def test_single_hip_runtime_in_process():
+    """The library shares torch's HIP runtime (one libamdhip64 mapped)."""
+    _lib.lib()
+    torch.zeros(1, device=DEV)
+    maps = open("/proc/self/maps").read()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+    assert any("libqlinear.so" in line for line in maps.splitlines())
+
+
+@pytest.mark.parametrize("n,k,seed", [(64, 256, 0), (256, 2560, 1), (96, 9728, 2)])
+def test_quantize_w4_bit_exact(n, k, seed):
+    w = weights(n, k, seed)
+    q, s = qlinear.quantize_w4(w.to(DEV))
+    oq, os_ = O.quantize_int4_g128(bits16(w))
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(bits16(s), os_)
+    deq = qlinear.dequantize_w4((q, s))
+    assert np.array_equal(bits16(deq), O.dequantize(O.unpack_int4_k32(oq), os_, bits=4, scale_dtype="bf16"))
+
+
+@pytest.mark.parametrize("n,k,seed", [(64, 256, 0), (128, 9728, 3)])
+def test_quantize_w8_bit_exact(n, k, seed):
+    w = weights(n, k, seed)
+    q, s = qlinear.quantize_w8(w.to(DEV))
+    oq, os_ = O.quantize_w8_per_channel(bits16(w))
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(bits16(s), os_)
+
+
+@pytest.mark.parametrize("n,k,seed", [(64, 256, 0), (128, 2560, 4)])
+def test_quantize_fp8_bit_exact(n, k, seed):
+    w = weights(n, k, seed)
+    q, s = qlinear.quantize_fp8(w.to(DEV))
+    oq, os_ = O.fp8_quantize(bits16(w), group=k)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq)
+    assert np.array_equal(bits16(s), os_[:, 0])
+
+
+@pytest.mark.parametrize("m,k", [(1, 2560), (3, 9728), (16, 256), (64, 4096)])
+def test_quantize_fp8_activation_bit_exact(m, k):
+    x = acts(m, k, 11 + m)
+    x[0, :7] = torch.tensor([0.0, -0.0, 1e-30, 448.0, -3e4, 2.0 ** -10, 7.0], dtype=torch.bfloat16)
+    if m > 1:
+        x[1].zero_()
+    q, s = qlinear.quantize_fp8_activation(x.to(DEV))
+    oq, os_ = O.quantize_fp8_activation(bits16(x))
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+
+
+SHAPES = [(256, 512), (6144, 2560), (2560, 9728), (2560, 4096)]
+BATCHES = [1, 3, 8, 16, 17, 32, 64]
+
+
+def _check(y, ref_deq, ref_exact, tag):
+    yf = y.float().cpu().numpy()
+    err = O.rel_l2(yf, ref_deq)
+    assert np.isfinite(yf).all(), tag
+    assert err <= 1e-2, f"{tag}: rel-L2 vs dequantize-then-matmul {err}"
+    exact = O.rel_l2(yf, O.round_bf16(ref_exact.astype(np.float32)))
+    assert exact <= 4e-3, f"{tag}: rel-L2 vs exact per-group product {exact}"
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_linear_w4a16(n, k):
+    w = weights(n, k, 5)
+    q, s = qlinear.quantize_w4(w.to(DEV))
+    oq, os_ = O.quantize_int4_g128(bits16(w))
+    codes = O.unpack_int4_k32(oq)
+    deq = O.dequantize(codes, os_, bits=4, scale_dtype="bf16")
+    for m in BATCHES:
+        x = acts(m, k, 100 + m)
+        y = qlinear.linear_w4a16(x.to(DEV), (q, s))
+        ref = O.linear_dequant(bits16(x), deq)
+        exact = O.linear_exact_grouped(bits16(x), codes.astype(np.float64) - 8, O.bf16_to_f32(os_), 128)
+        _check(y, ref, exact, f"w4 n={n} k={k} m={m}")
+        assert not y[:, 0].float().abs().sum().item(), "zero weight row must give zero"
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_linear_w8a16(n, k):
+    w = weights(n, k, 6)
+    q, s = qlinear.quantize_w8(w.to(DEV))
+    oq, os_ = O.quantize_w8_per_channel(bits16(w))
+    deq = O.dequantize(oq, os_[:, None], scale_dtype="bf16", storage="signed")
+    for m in BATCHES:
+        x = acts(m, k, 200 + m)
+        y = qlinear.linear_w8a16(x.to(DEV), (q, s))
+        ref = O.linear_dequant(bits16(x), deq)
+        exact = O.linear_exact_grouped(bits16(x), oq, O.bf16_to_f32(os_)[:, None], k)
+        _check(y, ref, exact, f"w8 n={n} k={k} m={m}")
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_linear_fp8_w8a8(n, k):
+    w = weights(n, k, 7)
+    q, s = qlinear.quantize_fp8(w.to(DEV))
+    oq, os_ = O.fp8_quantize(bits16(w), group=k)
+    for m in BATCHES:
+        x = acts(m, k, 300 + m)
+        y = qlinear.linear_fp8_w8a8(x.to(DEV), (q, s))
+        ref = O.linear_fp8_w8a8(bits16(x), oq, os_)
+        yf = y.float().cpu().numpy()
+        err = O.rel_l2(yf, ref)
+        assert err <= 1e-2, f"fp8 n={n} k={k} m={m}: {err}"
+        # the kernel computes the same products in fp32: far tighter than the contract
+        assert O.rel_l2(yf, O.round_bf16(ref.astype(np.float32))) <= 4e-3
+
+
+CONFIGS = [(4, 1, 1, 1), (4, 4, 1, 3), (8, 2, 1, 5), (4, 2, 2, 2), (8, 8, 1, 2), (4, 1, 2, 4)]
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+def test_configs_agree_and_planes_reduce_exactly(fmt):
+    quant, linear, code = qlinear.FORMATS[fmt]
+    n, k = 1024, 2560
+    w = weights(n, k, 8).to(DEV)
+    packed = quant(w)
+    for m in (1, 5, 16, 33):
+        x = acts(m, k, 400 + m).to(DEV)
+        base = linear(x, packed).float()
+        for cfg in CONFIGS:
+            try:
+                y = linear(x, packed, config=cfg)
+            except ValueError as exc:  # the plan's activation slice does not fit LDS
+                assert "LDS" in str(exc)
+                continue
+            assert (y.float() - base).abs().max().item() <= 2e-2 * base.abs().max().item() + 1e-6, (fmt, m, cfg)
+            planes = linear(x, packed, config=cfg, planes=True)
+            acc = torch.zeros_like(planes[0])
+            for p in planes:
+                acc += p
+            assert torch.equal(acc.to(torch.bfloat16), y), (fmt, m, cfg, "planes summed in order == split path")
+            again = linear(x, packed, config=cfg)
+            assert torch.equal(again, y), "deterministic"
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+def test_swiglu_epilogue(fmt):
+    quant, linear, code = qlinear.FORMATS[fmt]
+    inter, k = 512, 2560
+    w = weights(2 * inter, k, 9, edge=False).to(DEV)
+    packed = quant(w)
+    for m in (1, 4, 16, 32):
+        x = acts(m, k, 500 + m).to(DEV)
+        gu = linear(x, packed)
+        want = O.swiglu(bits16(gu))
+        for cfg in (None, (4, 1, 1, 4), (4, 4, 1, 4), (4, 2, 2, 5)):
+            got = linear(x, packed, config=cfg, swiglu=True)
+            planes = linear(x, packed, config=cfg, planes=True) if cfg else None
+            if planes is not None:
+                ref = O.swiglu_partials(planes.cpu().numpy())
+                ulp = np.abs(bits16(got).astype(np.int32) - ref.astype(np.int32)).max()
+                assert ulp <= 1, (fmt, m, cfg, "fused SwiGLU vs planes + SwiGLU", ulp)
+            err = O.rel_l2(got.float().cpu().numpy(), O.bf16_to_f32(want))
+            assert err < 2e-2, (fmt, m, cfg, err)
+
+
+def test_contract_violations_raise_before_launch():
+    q, s = qlinear.quantize_w4(weights(64, 256, 0).to(DEV))
+    with pytest.raises(ValueError):
+        qlinear.linear_w4a16(acts(1, 128, 0).to(DEV), (q, s))
+    with pytest.raises(ValueError):
+        qlinear.linear_w4a16(acts(65, 256, 0).to(DEV), (q, s))
+    with pytest.raises(ValueError):
+        qlinear.linear_w4a16(acts(1, 256, 0), (q, s))  # CPU activation
+    with pytest.raises(ValueError):
+        qlinear.linear_w4a16(acts(1, 256, 0).to(DEV), (q, s), config=(4, 3, 1, 1))
