@@ -1,0 +1,302 @@
+#!/usr/bin/env python
+"""Decode-step linear stack of a Qwen3-4B-shaped model on one MI355X.
+
+One step is the quantized linear stream of one decode step at batch M: 36 layers x
+(qkv 2560->6144, o 4096->2560, gate_up 2560->2x9728 with the fused SwiGLU epilogue,
+down 9728->2560) plus the lm_head 2560->151936, each layer with its own synthetic
+weights (4.03 GB in FP8, so the 256 MB Infinity Cache cannot serve repeats). The step is
+captured once in a HIP graph and replayed; activations are resident in HBM.
+
+Prints one JSON line (the driver's contract). ``value`` is microseconds per step for
+the default workload, FP8 e4m3 W8A8 at M=1.
+"""
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dryft-flash-infer_amd"))
+
+import torch  # noqa: E402
+
+PEAK_HBM = 8.0e12
+LAYERS = 36
+PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
+LM_HEAD = ("lm_head", 151936, 2560)
+METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Stack:
+    """Quantized weights of every projection of the model, plus resident activations."""
+
+    def __init__(self, fmt, m, seed=0, layers=LAYERS):
+        from kernels import qlinear
+        self.fmt, self.m = fmt, m
+        self.quant, self.linear, _ = qlinear.FORMATS[fmt]
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        self.calls = []  # (name, packed, k, swiglu)
+        for _ in range(layers):
+            for name, n, k in PROJ:
+                self.calls.append((name, self._make(gen, n, k), k, name == "gate_up"))
+        self.calls.append((LM_HEAD[0], self._make(gen, LM_HEAD[1], LM_HEAD[2]), LM_HEAD[2], False))
+        xg = torch.Generator(device="cuda").manual_seed(seed + 1)
+        self.x = {k: torch.randn(m, k, generator=xg, device="cuda").to(torch.bfloat16)
+                  for k in (2560, 4096, 9728)}
+        torch.cuda.synchronize()
+
+    def _make(self, gen, n, k):
+        from kernels import qlinear
+        w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        packed = self.quant(w)
+        del w
+        return qlinear.prepare(packed, self.fmt)  # load-time relayout into MI355X tiles
+
+    def run(self, which=None):
+        for name, packed, k, sw in self.calls:
+            if which is None or name == which:
+                self.linear(self.x[k], packed, swiglu=sw)
+
+    def bytes_alg(self, which=None):
+        """Algorithmic bytes: weight codes + scales + M*K*2 (x in) + M*N_out*2 (y out)."""
+        total = 0
+        for name, t, k, sw in self.calls:
+            if which is None or name == which:
+                total += t.bytes_moved() + self.m * k * 2 + self.m * (t.rows // 2 if sw else t.rows) * 2
+        return total
+
+    def weight_bytes(self, which=None):
+        return sum(t.bytes_moved() for name, t, _, _ in self.calls if which is None or name == which)
+
+    def count(self, which):
+        return sum(1 for c in self.calls if c[0] == which)
+
+
+def graph_of(fn):
+    fn()  # eager warmup: allocates the ticket counters outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, reps, warmup):
+    """ms per replay over `reps` replays, events on the replaying stream, synced both sides."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def median_graph_ms(g, reps, warmup, trials=5):
+    return statistics.median(time_graph(g, reps, warmup if i == 0 else 1) for i in range(trials))
+
+
+def stream_floor(nbytes=4 << 30):
+    """Best pure-read rate over `nbytes` resident bytes (GB/s), via qlx_stream_read."""
+    from kernels import _lib
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    best = 0.0
+    for blocks in (2048, 4096, 8192):
+        sink = torch.empty(blocks, dtype=torch.int32, device="cuda")
+
+        def run():
+            _lib.call("qlx_stream_read", _lib.ptr(buf), nbytes, _lib.ptr(sink), blocks,
+                      _lib.stream(buf.device))
+        g = graph_of(run)
+        ms = median_graph_ms(g, 5, 2, trials=3)
+        best = max(best, nbytes / (ms * 1e-3) / 1e9)
+    del buf
+    torch.cuda.empty_cache()
+    return best
+
+
+def untile(tiled):
+    """Row-major bytes of a tile-layout weight (inverse of qlx_tile_rows), on the host."""
+    rows, cols = tiled.shape
+    b = tiled.contiguous().view(torch.uint8).view(rows, -1)
+    width = b.shape[1]
+    v = b.reshape(rows // 16, width // 128, 2, 4, 16, 16).permute(0, 4, 1, 2, 3, 5)
+    return v.reshape(rows, width).contiguous().view(tiled.dtype).view(rows, cols)
+
+
+def cpu_baseline(stack, reps=3):
+    """The reference's torch CPU dequantize-then-matmul path, timed on the host cores.
+
+    Sample: layer 0's four projections plus the lm_head (the same synthetic weights and
+    activations, copied to host), median of `reps` after one warmup; scaled to a step as
+    36 x layer + lm_head."""
+    sys.path.insert(0, ROOT)
+    from oracle import cpu_baseline as cb
+    fn = cb.LINEARS[stack.fmt]
+    threads = torch.get_num_threads()
+    sample = [c for c in stack.calls[:4]] + [stack.calls[-1]]
+    host = []
+    for name, t, k, sw in sample:
+        # the CPU path reads the row-major packed weight: undo the tile relayout on the host
+        qc = untile(t.weight.cpu())
+        host.append((name, qc, t.scale.cpu(), stack.x[k].cpu()))
+    times = {}
+    for name, q, s, x in host:
+        fn(x, q, s)  # warmup
+        runs = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn(x, q, s)
+            runs.append(time.perf_counter() - t0)
+        times[name] = statistics.median(runs)
+    layer = sum(times[n] for n, _, _, _ in host[:4])
+    step_s = LAYERS * layer + times["lm_head"]
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {
+        "value": round(step_s * 1e6, 1), "unit": "us per step", "cores": threads,
+        "kind": "port",
+        "sample": (f"dequantize+matmul (torch CPU, {stack.fmt}, M={stack.m}) of layer 0's qkv/o/gate_up/down "
+                   f"and the lm_head, median of {reps}; step = 36 x layer + lm_head"),
+        "per_call_ms": {k: round(v * 1e3, 3) for k, v in times.items()},
+        "cpu_model": model or platform.processor(), "os_cpu_count": os.cpu_count(),
+        "effective_weight_GBps": round(stack.weight_bytes() / step_s / 1e9, 2),
+    }
+
+
+def measure_stack(fmt, m, steps, warmup, breakdown=True):
+    stack = Stack(fmt, m)
+    g = graph_of(stack.run)
+    ms = median_graph_ms(g, steps, warmup)
+    out = {
+        "us": ms * 1e3,
+        "weight_GB": stack.weight_bytes() / 1e9,
+        "alg_GB": stack.bytes_alg() / 1e9,
+    }
+    out["effective_weight_GBps"] = stack.weight_bytes() / (ms * 1e-3) / 1e9
+    out["alg_GBps"] = stack.bytes_alg() / (ms * 1e-3) / 1e9
+    out["hbm_frac"] = out["alg_GBps"] * 1e9 / PEAK_HBM
+    if breakdown:
+        per = {}
+        for name, _, _ in PROJ + [LM_HEAD]:
+            gp = graph_of(lambda: stack.run(name))
+            cnt = stack.count(name)
+            reps = max(3, steps // 2) if name != "lm_head" else max(10, steps)
+            t = median_graph_ms(gp, reps, 2, trials=3) / cnt
+            b = stack.bytes_alg(name) / cnt
+            per[name] = {"us": round(t * 1e3, 2), "alg_MB": round(b / 1e6, 3),
+                         "GBps": round(b / (t * 1e-3) / 1e9, 1)}
+            del gp
+        out["per_projection"] = per
+    del g
+    return stack, out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="fp8", choices=["fp8", "w4a16", "w8a16"])
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline stack only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(sharding is described in DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        sys.exit(2)
+    from kernels import _lib
+    _lib.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
+    log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step, "
+        f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
+
+    # Roofline of the dominant kernel: the fused gate_up+SwiGLU projection (the largest
+    # share of the step's bytes), averaged over its 36 launches in one graph.
+    dom = head.get("per_projection", {}).get("gate_up")
+    if dom is None:
+        gp = graph_of(lambda: stack.run("gate_up"))
+        t = median_graph_ms(gp, max(3, args.steps // 2), 2, trials=3) / stack.count("gate_up")
+        b = stack.bytes_alg("gate_up") / stack.count("gate_up")
+        dom = {"us": t * 1e3, "alg_MB": b / 1e6, "GBps": b / (t * 1e-3) / 1e9}
+    roofline = {
+        "bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+        "frac": round(dom["GBps"] * 1e9 / PEAK_HBM, 4), "traffic": None,
+        "kernel": f"gemm_kernel<{ {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload] }, ..., SwiGLU> "
+                  f"(gate_up 2560->2x9728, M={args.m})",
+        "us_per_launch": round(dom["us"], 2), "alg_MB_per_launch": round(dom["alg_MB"], 3),
+    }
+
+    extra = {}
+    if not args.quick:
+        extra["stream_floor_GBps"] = round(stream_floor(), 1)
+        extra["stack_frac_of_stream_floor"] = round(head["alg_GBps"] / extra["stream_floor_GBps"], 4)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(stack)
+    del stack
+    torch.cuda.empty_cache()
+    if not args.quick:
+        for fmt, m in (("w4a16", 1), ("fp8", 8), ("w4a16", 8)):
+            if (fmt, m) == (args.workload, args.m):
+                continue
+            st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=False)
+            extra[f"{fmt}_M{m}_stack"] = {k: round(v, 4 if k == "hbm_frac" else 2) for k, v in res.items()}
+            log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s")
+            del st
+            torch.cuda.empty_cache()
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["us"], 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp8": "fp8e4m3", "w4a16": "int4xbf16", "w8a16": "int8xbf16"}[args.workload],
+        "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) activations)",
+        "config": {
+            "workload": f"Qwen3-4B decode-step linear stack, {args.workload}, 36 layers x "
+                        f"(qkv, o, gate_up+SwiGLU, down) + lm_head",
+            "m": args.m, "hidden": 2560, "intermediate": 9728, "vocab": 151936, "layers": LAYERS,
+            "weight_GB": round(head["weight_GB"], 4), "alg_GB": round(head["alg_GB"], 4),
+        },
+        "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
+        "hbm_frac": round(head["hbm_frac"], 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_projection": head.get("per_projection"),
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

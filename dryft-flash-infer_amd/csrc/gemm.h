@@ -48,7 +48,7 @@ struct GemmArgs {
   int mode, splits, sps, nsteps;
   int ntiles, kw, rt, tile_groups;
   int group;         // FP8WO scale group
-  int tiled;         // REF8 storage
+  int tiled;         // weight stored in tiles (see tile_offset; REF8: the reference's tiles)
   int half;          // SWIGLU: I = n / 2
   int xstride;       // LDS bytes per staged activation row
   int off_sc, off_xb, off_sx;  // LDS byte offsets (x region starts at 0)
@@ -64,6 +64,25 @@ __device__ __forceinline__ int weight_row(const GemmArgs& a, int tile, int r) {
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// MI355X tile layout of a row-major [rows][row_bytes] weight (row_bytes % 128 == 0): a
+// 16-row x 128-byte step is one contiguous 2 KB block, ordered [j][c][r][16 B] -- exactly
+// the order in which a wave's two 16-byte-per-lane loads consume it (lane = 16c + r, load j
+// takes bytes 64j + 16c of row r) -- and a tile's steps follow each other. Each load
+// instruction then reads 1 KB of consecutive bytes.
+__device__ __forceinline__ size_t tile_offset(int wrow, int step_bytes_idx, int j, int lane, int row_bytes) {
+  return ((size_t)(wrow >> 4) * (row_bytes >> 7) + step_bytes_idx) * 2048 +
+         (size_t)((j * 4 + (lane >> 4)) * 16 + (wrow & 15)) * 16;
+}
+
+// Device-coherent (agent scope) store/load: written through to / read from the level all
+// XCDs share, so split-K partials need no cache-wide write-back to be seen by another CU.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Two exact small-integer floats -> bf16 pair (the high halves are exact: <= 8 significant bits).
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
@@ -93,16 +112,21 @@ __device__ __forceinline__ uint32_t bf16_at(const uint16_t* p, int i) { return p
 // ====================================================================================
 
 // ---- W4A16: int32 [n][k/8] words (nibble i of word j = k 8j+i, code = q + 8),
-//      bf16 scale [n][k/128]. Step = one 128-group; lane chunk = 4 words = 32 k.
+//      bf16 scale [n][k/128]. Step = 256 k = 128 bytes of a row = two groups; lane chunk j
+//      (j = 0, 1) is the 4 words at byte 64j + 16c, i.e. group 2*step + j, so one wave's two
+//      loads complete 16 full 128-byte lines.
 struct FmtW4 {
-  static constexpr int KSTEP = 128, LOADS = 1, NSC = 1, XBYTES = 2;
+  static constexpr int KSTEP = 256, LOADS = 2, NSC = 2, XBYTES = 2;
   static constexpr float BIAS = 136.f;  // bf16(128 + code) = q + 136
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
+    if (a.tiled)
+      return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) +
+                                            tile_offset(wrow, step, j, lane, a.k >> 1));
     return reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(a.w) +
-                                          (size_t)wrow * (a.k >> 3) + step * 16 + (lane >> 4) * 4);
+                                          (size_t)wrow * (a.k >> 3) + step * 32 + j * 16 + (lane >> 4) * 4);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 7) + step]);
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 7) + 2 * step + j]);
   }
   // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword).
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
@@ -117,9 +141,9 @@ struct FmtW4 {
   }
   // The same MFMA chain with every code at the bias (q = 0): bias * sum(x) rounded exactly
   // as the main loop rounds it, so an all-zero weight row gives exactly zero.
-  __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
+  __device__ static f32x4 bias_chain(const char* lds, int srel, int j, int lane, int xoff) {
     const uint4 av = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136
-    const int kb = (srel * 128 + (lane >> 4) * 32) * 2;
+    const int kb = (srel * 256 + j * 128 + (lane >> 4) * 32) * 2;
     f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -132,43 +156,50 @@ struct FmtW4 {
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int rowl) {
-    f32x4 tmp[MT];
+    const float* sc = reinterpret_cast<const float*>(lds + a.off_sc);
+    const float* xbp = reinterpret_cast<const float*>(lds + a.off_xb);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t wd[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
-    const int kb = (srel * 128 + (lane >> 4) * 32) * 2;
+    for (int j = 0; j < 2; ++j) {
+      f32x4 tmp[MT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint4 av;
-      av.x = nib_pair(wd[t], 0);
-      av.y = nib_pair(wd[t], 4);
-      av.z = nib_pair(wd[t], 8);
-      av.w = nib_pair(wd[t], 12);
+      for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t wd[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
+      const int kb = (srel * 256 + j * 128 + (lane >> 4) * 32) * 2;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint4 av;
+        av.x = nib_pair(wd[t], 0);
+        av.y = nib_pair(wd[t], 4);
+        av.z = nib_pair(wd[t], 8);
+        av.w = nib_pair(wd[t], 12);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+          tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+        }
+      }
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + (srel * 2 + j) * a.sc_stride + rowl);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
-        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+        const float xb = xbp[mrow[mt] * a.xb_stride + srel * 2 + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - xb, acc[mt][i]);
       }
-    }
-    const f32x4 sc = *reinterpret_cast<const f32x4*>(
-        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float xb = reinterpret_cast<const float*>(lds + a.off_xb)[mrow[mt] * a.xb_stride + srel];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(sc[i], tmp[mt][i] - xb, acc[mt][i]);
     }
   }
   __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
 };
 
-// ---- W8A16 per output channel: int8 [n][k], bf16 scale [n]. Step = 64 k.
+// ---- W8A16 per output channel: int8 [n][k], bf16 scale [n]. Step = 128 k (a full
+//      128-byte row segment); lane chunk j is the 16 bytes at 64j + 16c.
 struct FmtW8 {
-  static constexpr int KSTEP = 64, LOADS = 1, NSC = 0, XBYTES = 2;
+  static constexpr int KSTEP = 128, LOADS = 2, NSC = 0, XBYTES = 2;
   static constexpr float BIAS = 128.f;  // (byte ^ 0x80) = q + 128
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
+    if (a.tiled)
+      return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + tile_offset(wrow, step, j, lane, a.k));
     return reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(a.w) + (size_t)wrow * a.k +
-                                          step * 64 + (lane >> 4) * 16);
+                                          step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
     return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
@@ -178,12 +209,15 @@ struct FmtW8 {
   }
   __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
     const uint4 av = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
-    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
     f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff + kb + t * 16);
-      t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), t4, 0, 0, 0);
+    for (int j = 0; j < 2; ++j) {
+      const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff + kb + t * 16);
+        t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), t4, 0, 0, 0);
+      }
     }
     return t4;
   }
@@ -191,20 +225,23 @@ struct FmtW8 {
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int) {
-    const uint32_t wd[4] = {c[0].x ^ 0x80808080u, c[0].y ^ 0x80808080u, c[0].z ^ 0x80808080u,
-                            c[0].w ^ 0x80808080u};
-    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
     f32x4 tmp[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint2 lo = bytes_to_bf16(wd[2 * t]), hi = bytes_to_bf16(wd[2 * t + 1]);
-      const uint4 av = {lo.x, lo.y, hi.x, hi.y};
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t wd[4] = {c[j].x ^ 0x80808080u, c[j].y ^ 0x80808080u, c[j].z ^ 0x80808080u,
+                              c[j].w ^ 0x80808080u};
+      const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
-        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+      for (int t = 0; t < 2; ++t) {
+        const uint2 lo = bytes_to_bf16(wd[2 * t]), hi = bytes_to_bf16(wd[2 * t + 1]);
+        const uint4 av = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+          tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+        }
       }
     }
 #pragma unroll
@@ -221,13 +258,15 @@ struct FmtW8 {
 };
 
 // ---- FP8 W8A8: e4m3 [n][k], bf16 scale [n]; activation quantized per token in the
-//      prologue. Step = 64 k.
+//      prologue. Step = 128 k (a full 128-byte row segment), chunk j at byte 64j + 16c.
 struct FmtFP8 {
-  static constexpr int KSTEP = 64, LOADS = 1, NSC = 0, XBYTES = 1;
+  static constexpr int KSTEP = 128, LOADS = 2, NSC = 0, XBYTES = 1;
   static constexpr float BIAS = 0.f;
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
+    if (a.tiled)
+      return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + tile_offset(wrow, step, j, lane, a.k));
     return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + (size_t)wrow * a.k +
-                                          step * 64 + (lane >> 4) * 16);
+                                          step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
     return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
@@ -236,16 +275,19 @@ struct FmtFP8 {
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs&, int srel, int lane, const int (&xoff)[MT],
                                  const int (&)[MT], int) {
-    const int kb = srel * 64 + (lane >> 4) * 16;
-    const long a0 = (long)(((unsigned long)c[0].y << 32) | c[0].x);
-    const long a1 = (long)(((unsigned long)c[0].w << 32) | c[0].z);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
-      const long b0 = (long)(((unsigned long)bv.y << 32) | bv.x);
-      const long b1 = (long)(((unsigned long)bv.w << 32) | bv.z);
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a0, b0, acc[mt], 0, 0, 0);
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a1, b1, acc[mt], 0, 0, 0);
+    for (int j = 0; j < 2; ++j) {
+      const int kb = srel * 128 + j * 64 + (lane >> 4) * 16;
+      const long a0 = (long)(((unsigned long)c[j].y << 32) | c[j].x);
+      const long a1 = (long)(((unsigned long)c[j].w << 32) | c[j].z);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
+        const long b0 = (long)(((unsigned long)bv.y << 32) | bv.x);
+        const long b1 = (long)(((unsigned long)bv.w << 32) | bv.z);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a0, b0, acc[mt], 0, 0, 0);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a1, b1, acc[mt], 0, 0, 0);
+      }
     }
   }
   __device__ static float finish(const GemmArgs& a, const char* lds, float v, int rl, int mm) {
@@ -270,22 +312,18 @@ template <int BITS>
 struct FmtRef {
   static constexpr int KSTEP = 128, LOADS = BITS == 8 ? 2 : 1, NSC = 2, XBYTES = 2;
   static constexpr float BIAS = BITS == 8 ? 128.f : 136.f;
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     const int r = wrow & 15, tile = wrow >> 4, c = lane >> 4;
     const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
     if (BITS == 4) {
       const size_t tb = ((size_t)tile * (a.k >> 7) + step) * 1024;
       return reinterpret_cast<const uint4*>(w + tb + (((r >> 3) * 8 + (r & 7)) * 4 + c) * 16);
     }
-    if (a.tiled) {
+    if (a.tiled) {  // [half][j][g][t][16 B]
       const size_t tb = ((size_t)tile * (a.k >> 7) + step) * 2048;
-      return reinterpret_cast<const uint4*>(w + tb + ((((r >> 3) * 2) * 8 + (r & 7)) * 4 + c) * 16);
+      return reinterpret_cast<const uint4*>(w + tb + ((((r >> 3) * 2 + j) * 8 + (r & 7)) * 4 + c) * 16);
     }
-    return reinterpret_cast<const uint4*>(w + (size_t)wrow * a.k + step * 128 + c * 16);
-  }
-  // Second load (block j = 1) of the 8-bit formats.
-  __device__ static const uint4* chunk_ptr1(const GemmArgs& a, const uint4* p0) {
-    return a.tiled ? p0 + 8 * 4 : p0 + 4;  // tiled: next j is 8 rows x 4 chunks further
+    return reinterpret_cast<const uint4*>(w + (size_t)wrow * a.k + step * 128 + j * 64 + c * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
     return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
@@ -361,16 +399,18 @@ struct FmtRef {
 };
 
 // ---- fp8.fp8_matmul: e4m3 [n][k] weights, bf16 scale [n][k/group], bf16 activation.
-//      Step = 64 k; e4m3 -> fp32 by v_cvt_pk_f32_fp8 (exact), -> bf16 by truncation (exact).
+//      Step = 128 k, chunk j (64-wide block 2*step + j) at byte 64j + 16c; e4m3 -> fp32 by
+//      v_cvt_pk_f32_fp8 (exact), -> bf16 by truncation (exact: e4m3 has 4 significant bits).
 struct FmtFP8WO {
-  static constexpr int KSTEP = 64, LOADS = 1, NSC = 1, XBYTES = 2;
+  static constexpr int KSTEP = 128, LOADS = 2, NSC = 2, XBYTES = 2;
   static constexpr float BIAS = 0.f;
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + (size_t)wrow * a.k +
-                                          step * 64 + (lane >> 4) * 16);
+                                          step * 128 + j * 64 + (lane >> 4) * 16);
   }
-  __device__ static float scale(const GemmArgs& a, int wrow, int step, int) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k / a.group) + (step * 64) / a.group]);
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
+    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k / a.group) +
+                                                        (step * 128 + j * 64) / a.group]);
   }
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
     return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
@@ -385,27 +425,30 @@ struct FmtFP8WO {
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&)[MT], int rowl) {
-    const uint32_t wd[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
-    const int kb = (srel * 64 + (lane >> 4) * 16) * 2;
-    f32x4 tmp[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t wd[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
+      const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
+      f32x4 tmp[MT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint4 av = {fp8pair<false>(wd[2 * t]), fp8pair<true>(wd[2 * t]),
-                        fp8pair<false>(wd[2 * t + 1]), fp8pair<true>(wd[2 * t + 1])};
+      for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
-        tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+      for (int t = 0; t < 2; ++t) {
+        const uint4 av = {fp8pair<false>(wd[2 * t]), fp8pair<true>(wd[2 * t]),
+                          fp8pair<false>(wd[2 * t + 1]), fp8pair<true>(wd[2 * t + 1])};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
+          tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+        }
       }
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(
+          reinterpret_cast<const float*>(lds + a.off_sc) + (srel * 2 + j) * a.sc_stride + rowl);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(sc[i], tmp[mt][i], acc[mt][i]);
     }
-    const f32x4 sc = *reinterpret_cast<const f32x4*>(
-        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(sc[i], tmp[mt][i], acc[mt][i]);
   }
   __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
 };
@@ -413,33 +456,37 @@ struct FmtFP8WO {
 // ---- cuda_int8 W8A8: int8 [n][k] and int8 activation [m][k], both in fragment order
 //      (engine/kernels/cuda_int8.py:64, 100-108); fp16 weight scale [n][k/64], fp32
 //      activation scale [m][k/64]; per group acc = fma(float(dot) * sx, sw, acc)
-//      (engine/kernels/cuda_int8.py:198-199). Step = 64 k = one group.
+//      (engine/kernels/cuda_int8.py:198-199). Step = 128 k = groups 2*step + j, chunk j at
+//      byte 64j + 16c.
 struct FmtInt8 {
-  static constexpr int KSTEP = 64, LOADS = 1, NSC = 1, XBYTES = 1;
+  static constexpr int KSTEP = 128, LOADS = 2, NSC = 2, XBYTES = 1;
   static constexpr float BIAS = 0.f;
-  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane) {
+  __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     return reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(a.w) + (size_t)wrow * a.k +
-                                          step * 64 + (lane >> 4) * 16);
+                                          step * 128 + j * 64 + (lane >> 4) * 16);
   }
-  __device__ static float scale(const GemmArgs& a, int wrow, int step, int) {
-    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + step]);
+  __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
+    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
   }
   template <int MT>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int rowl) {
-    const i32x4 av = {(int)c[0].x, (int)c[0].y, (int)c[0].z, (int)c[0].w};
-    const int kb = srel * 64 + (lane >> 4) * 16;
-    const f32x4 sw = *reinterpret_cast<const f32x4*>(
-        reinterpret_cast<const float*>(lds + a.off_sc) + srel * a.sc_stride + rowl);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
-      const i32x4 b = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
-      const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
-      const float sx = reinterpret_cast<const float*>(lds + a.off_sx)[mrow[mt] * a.xb_stride + srel];
+    for (int j = 0; j < 2; ++j) {
+      const i32x4 av = {(int)c[j].x, (int)c[j].y, (int)c[j].z, (int)c[j].w};
+      const int kb = srel * 128 + j * 64 + (lane >> 4) * 16;
+      const f32x4 sw = *reinterpret_cast<const f32x4*>(
+          reinterpret_cast<const float*>(lds + a.off_sc) + (srel * 2 + j) * a.sc_stride + rowl);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf((float)d[i] * sx, sw[i], acc[mt][i]);
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
+        const i32x4 b = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+        const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+        const float sx = reinterpret_cast<const float*>(lds + a.off_sx)[mrow[mt] * a.xb_stride + srel * 2 + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf((float)d[i] * sx, sw[i], acc[mt][i]);
+      }
     }
   }
   __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
@@ -503,11 +550,11 @@ __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) 
   __syncthreads();
   for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = fmaxf(__uint_as_float(amax[i]) / 448.f, 1e-12f);
   __syncthreads();
-  const int cps = nst * 8;  // 8-value chunks per row of the slice
+  const int cps = nst * 16;  // 8-value chunks per row of the slice
   for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
     const int mm = q / cps, kc = q - mm * cps;
     const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k +
-                                                    step0 * 64 + kc * 8);
+                                                    step0 * 128 + kc * 8);
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
     const float s = sx[mm];
     uint32_t c[8];
@@ -525,16 +572,17 @@ __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) 
 
 // cuda_int8 prologue: int8 activation slice and its fp32 group scales.
 __device__ void stage_int8_act(const GemmArgs& a, char* lds, int step0, int nst) {
-  const int cps = nst * 4;
+  const int cps = nst * 8;
   for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
     const int mm = q / cps, kc = q - mm * cps;
     *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = *reinterpret_cast<const uint4*>(
-        reinterpret_cast<const int8_t*>(a.x) + (size_t)mm * a.k + step0 * 64 + kc * 16);
+        reinterpret_cast<const int8_t*>(a.x) + (size_t)mm * a.k + step0 * 128 + kc * 16);
   }
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
-  for (int q = threadIdx.x; q < a.m * nst; q += blockDim.x) {
-    const int mm = q / nst, j = q - mm * nst;
-    sx[mm * a.xb_stride + j] = a.xs[(size_t)mm * (a.k >> 6) + step0 + j];
+  const int gps = 2 * nst;
+  for (int q = threadIdx.x; q < a.m * gps; q += blockDim.x) {
+    const int mm = q / gps, j = q - mm * gps;
+    sx[mm * a.xb_stride + j] = a.xs[(size_t)mm * (a.k >> 6) + 2 * step0 + j];
   }
 }
 
@@ -577,24 +625,39 @@ __device__ __forceinline__ void block_coords(const GemmArgs& a, int& tg, int& s)
 template <class F>
 __device__ __forceinline__ void load_chunk(uint4 (&c)[F::LOADS], const GemmArgs& a, int wrow, int step,
                                            int lane) {
-  const uint4* p = F::chunk_ptr(a, wrow, step, lane);
-  const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  c[0] = uint4{v0[0], v0[1], v0[2], v0[3]};
-  if constexpr (F::LOADS == 2) {
-    const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(FmtRef<8>::chunk_ptr1(a, p)));
-    c[1] = uint4{v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+  for (int j = 0; j < F::LOADS; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(F::chunk_ptr(a, wrow, step, lane, j)));
+    c[j] = uint4{v[0], v[1], v[2], v[3]};
   }
 }
 
-template <class F, int MT, int RW, int WAVES>
+// SW: the SwiGLU epilogue (a separate instantiation, so profiles tell it apart).
+template <class F, int MT, int RW, int WAVES, bool SW>
 __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) char lds[];
-  constexpr int PF = RW == 1 ? 8 : 4;  // steps in flight per wave
+  constexpr int PF = RW == 1 ? 4 : 2;  // steps in flight per wave (each 2 KB for RW = 1)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int tg, s;
   block_coords(a, tg, s);
   const int step0 = s * a.sps;
   const int nst = min(a.nsteps, step0 + a.sps) - step0;
+
+  // ---- first weight loads: they depend on nothing, so they are in flight while the
+  // prologue stages the activation
+  const int wt = wave / a.kw, kwi = wave - wt * a.kw;   // tile slot, k-interleave index
+  const int tile0 = tg * a.rt + wt * RW;
+  const bool active = tile0 < a.ntiles;
+  int wrow[RW];  // a tile past the end streams its neighbour's rows; its output is dropped
+#pragma unroll
+  for (int r = 0; r < RW; ++r) wrow[r] = active ? weight_row(a, tile0 + r < a.ntiles ? tile0 + r : tile0, lane & 15) : 0;
+  const int my = active ? (nst - kwi + a.kw - 1) / a.kw : 0;  // this wave's steps: kwi, kwi + kw, ...
+  uint4 buf[PF][RW][F::LOADS];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (p < my)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + p * a.kw, lane);
 
   // ---- prologue
   if constexpr (std::is_same<F, FmtFP8>::value) {
@@ -612,8 +675,6 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   }
 
   // ---- main loop
-  const int wt = wave / a.kw, kwi = wave - wt * a.kw;   // tile slot, k-interleave index
-  const int tile0 = tg * a.rt + wt * RW;
   f32x4 acc[RW][MT];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -625,42 +686,34 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
     mrow[mt] = min(16 * mt + (lane & 15), a.m - 1);
     xoff[mt] = mrow[mt] * a.xstride;
   }
-  if (tile0 < a.ntiles) {
-    int wrow[RW];
-    bool live[RW];
+  // Steady state: PF steps per trip, every load unconditional. Prefetch addresses past the
+  // wave's last step are clamped to it (a cache hit), so the body has no branches and the
+  // compiler keeps PF steps of loads in flight instead of draining at every join.
+  const int last = step0 + kwi + (my - 1) * a.kw;
+  int j0 = 0;
+  for (; j0 + PF <= my; j0 += PF) {
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      live[r] = tile0 + r < a.ntiles;
-      wrow[r] = weight_row(a, live[r] ? tile0 + r : tile0, lane & 15);
+    for (int p = 0; p < PF; ++p) {
+      const int srel = kwi + (j0 + p) * a.kw;
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+        F::template compute<MT>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
+      // Refill the slot just consumed (same registers: no copies across the loop edge),
+      // and keep the refill here rather than letting the scheduler sink it to the end.
+      const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, last);
+#pragma unroll
+      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], nxt, lane);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    const int my = (nst - kwi + a.kw - 1) / a.kw;  // steps of this wave: kwi, kwi + kw, ...
-    uint4 buf[PF][RW][F::LOADS];
+  }
+  // Tail: the remaining (< PF) steps are already loaded.
 #pragma unroll
-    for (int p = 0; p < PF; ++p)
-      if (p < my)
+  for (int p = 0; p < PF; ++p) {
+    if (j0 + p < my) {
+      const int srel = kwi + (j0 + p) * a.kw;
 #pragma unroll
-        for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + p * a.kw, lane);
-    for (int j0 = 0; j0 < my; j0 += PF) {
-#pragma unroll
-      for (int p = 0; p < PF; ++p) {
-        const int j = j0 + p;
-        if (j < my) {
-          uint4 cur[RW][F::LOADS];
-#pragma unroll
-          for (int r = 0; r < RW; ++r)
-#pragma unroll
-            for (int l = 0; l < F::LOADS; ++l) cur[r][l] = buf[p][r][l];
-          if (j + PF < my)
-#pragma unroll
-            for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + (j + PF) * a.kw, lane);
-          const int srel = kwi + j * a.kw;
-#pragma unroll
-          for (int r = 0; r < RW; ++r)
-            if (live[r])
-              F::template compute<MT>(acc[r], cur[r], lds, a, srel, lane, xoff, mrow,
-                                      (wt * RW + r) * 16 + 4 * (lane >> 4));
-        }
-      }
+      for (int r = 0; r < RW; ++r)
+        F::template compute<MT>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
     }
   }
 
@@ -684,7 +737,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
     return F::finish(a, lds, v, tl * 16 + nl, mm);
   };
 
-  const int rows_out = a.mode == QLX_MODE_SWIGLU ? 8 : 16;
+  const int rows_out = SW ? 8 : 16;
   const int per_tile = rows_out * a.m;
   const int total = a.rt * per_tile;
   const bool direct = a.splits == 1 || a.mode == QLX_MODE_PLANES;
@@ -694,51 +747,57 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
     const int mm = rem / rows_out, nl = rem - mm * rows_out;
     const int tile = tg * a.rt + tl;
     if (tile >= a.ntiles) continue;
-    if (a.mode == QLX_MODE_SWIGLU) {
+    if (SW) {
       const float g = combined(tl, nl, mm), u = combined(tl, nl + 8, mm);
       if (direct) {
         const float gb = round_bf(g), ub = round_bf(u);
         y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
       } else {
         float* pl = a.work + ((size_t)s * a.m + mm) * a.n;
-        pl[8 * tile + nl] = g;
-        pl[a.half + 8 * tile + nl] = u;
+        store_coherent(pl + 8 * tile + nl, g);
+        store_coherent(pl + a.half + 8 * tile + nl, u);
       }
     } else {
       const float v = combined(tl, nl, mm);
       const int row = 16 * tile + nl;
-      if (a.mode == QLX_MODE_PLANES || !direct)
+      if (a.mode == QLX_MODE_PLANES)
         a.work[((size_t)s * a.m + mm) * a.n + row] = v;
+      else if (!direct)
+        store_coherent(a.work + ((size_t)s * a.m + mm) * a.n + row, v);
       else
         y[(size_t)mm * a.n + row] = f2bf(v);
     }
   }
   if (direct) return;
 
-  // ---- split-K: the last workgroup of this row block reduces the planes in slice order
+  // ---- split-K: the last workgroup of this row block reduces the planes in slice order.
+  // The partials went out with device-coherent stores; a workgroup release waits for them
+  // to complete before the ticket is taken, and the last workgroup reads them with
+  // device-coherent loads. No L2 write-back/invalidate of the whole cache is needed (an
+  // agent-scope fence would emit one per workgroup).
   __shared__ int s_last;
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&a.tickets[tg], 1);
+    const int prev = __hip_atomic_fetch_add(&a.tickets[tg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == a.splits - 1;
-    if (s_last) a.tickets[tg] = 0;
+    if (s_last) __hip_atomic_store(&a.tickets[tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   const size_t plane = (size_t)a.m * a.n;
   for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
     const int tl = idx / per_tile, rem = idx - tl * per_tile;
     const int mm = rem / rows_out, nl = rem - mm * rows_out;
     const int tile = tg * a.rt + tl;
     if (tile >= a.ntiles) continue;
-    if (a.mode == QLX_MODE_SWIGLU) {
+    if (SW) {
       const float* pg = a.work + (size_t)mm * a.n + 8 * tile + nl;
       float g = 0.f, u = 0.f;
       for (int sp = 0; sp < a.splits; ++sp) {
-        g += __builtin_nontemporal_load(pg + sp * plane);
-        u += __builtin_nontemporal_load(pg + sp * plane + a.half);
+        g += load_coherent(pg + sp * plane);
+        u += load_coherent(pg + sp * plane + a.half);
       }
       const float gb = round_bf(g), ub = round_bf(u);
       y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
@@ -746,7 +805,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
       const int row = 16 * tile + nl;
       const float* p = a.work + (size_t)mm * a.n + row;
       float v = 0.f;
-      for (int sp = 0; sp < a.splits; ++sp) v += __builtin_nontemporal_load(p + sp * plane);
+      for (int sp = 0; sp < a.splits; ++sp) v += load_coherent(p + sp * plane);
       y[(size_t)mm * a.n + row] = f2bf(v);
     }
   }

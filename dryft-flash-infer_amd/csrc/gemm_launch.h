@@ -65,7 +65,10 @@ inline int check_plan(const qlx_plan* p, int m, int n, int k, int kstep) {
 template <class F, int MT, int RW, int WAVES>
 hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   const int grid = a.tile_groups * a.splits;
-  gemm_kernel<F, MT, RW, WAVES><<<grid, WAVES * 64, lds, st>>>(a);
+  if (a.mode == QLX_MODE_SWIGLU)
+    gemm_kernel<F, MT, RW, WAVES, true><<<grid, WAVES * 64, lds, st>>>(a);
+  else
+    gemm_kernel<F, MT, RW, WAVES, false><<<grid, WAVES * 64, lds, st>>>(a);
   return hipGetLastError();
 }
 

@@ -2,11 +2,12 @@
 #include "gemm_launch.h"
 
 extern "C" int qlx_linear_w8a16(const void* w, const void* w_scale, const void* x, void* y, int m,
-                                int n, int k, const qlx_plan* plan, void* stream) {
+                                int n, int k, int tiled, const qlx_plan* plan, void* stream) {
   qlx::GemmArgs a = {};
   a.w = w;
   a.ws = w_scale;
   a.x = x;
   a.y = y;
+  a.tiled = tiled;
   return qlx::launch_gemm<qlx::FmtW8>("linear_w8a16", a, plan, m, n, k, stream);
 }

@@ -23,8 +23,10 @@ qlx::FmtInfo fmt_info(int fmt) {
   }
 }
 
-// Waves the chip should have in flight for a streaming GEMV: 256 CUs x 8.
-constexpr int kTargetWaves = 2048;
+// Workgroups a streaming GEMV should at least have. Measured on MI355X at M = 1 over the
+// Qwen3-4B shapes: fewer, larger workgroups win (each pays the activation staging and a
+// reduction once) as long as there are about 150 or more of them.
+constexpr int kMinGroups = 160;
 
 }  // namespace
 
@@ -36,17 +38,22 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
               "shape m=%d n=%d k=%d does not fit format %d", m, n, k, fmt);
   qlx_plan p = {};
   p.mode = mode;
-  p.waves = 4;
+  p.waves = 8;
   p.rw = m > 16 ? 2 : 1;
+  p.splits = 1;
   const int nsteps = k / fi.kstep;
   const int ntiles = n / 16;
-  const int slots = (ntiles + p.rw - 1) / p.rw;  // waves if every wave took whole tiles
-  int need = slots >= kTargetWaves ? 1 : (kTargetWaves + slots - 1) / slots;
-  int max_par = nsteps / 2 > 1 ? nsteps / 2 : 1;  // keep >= 2 steps per wave
-  if (need > max_par) need = max_par;
-  p.kw = need >= 4 ? 4 : (need >= 2 ? 2 : 1);
-  p.splits = (need + p.kw - 1) / p.kw;
-  // Large m stages a wide activation slice: split K further until LDS fits.
+  // kw: waves sharing one tile's K range, the smallest that still gives kMinGroups groups
+  // (and at least one step per wave).
+  p.kw = 8;
+  for (int kw = 1; kw <= 8; kw *= 2) {
+    const int groups = (ntiles + (p.waves / kw) * p.rw - 1) / ((p.waves / kw) * p.rw);
+    if (groups >= kMinGroups || kw >= nsteps) {
+      p.kw = kw;
+      break;
+    }
+  }
+  // Large m stages a wide activation slice: split K until the workgroup's LDS fits.
   qlx::GemmArgs a = {};
   for (;;) {
     const int lds = qlx::layout(fi, p, m, n, k, a);
@@ -55,7 +62,6 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
   }
   qlx::layout(fi, p, m, n, k, a);
   p.splits = a.splits;  // normalised: every slice non-empty
-  if (mode == QLX_MODE_PLANES && p.splits < 1) p.splits = 1;
   *plan = p;
   return QLX_OK;
 }

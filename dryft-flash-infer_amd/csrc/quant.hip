@@ -396,3 +396,33 @@ int qlx_quantize_act_int8(const void* x, void* q, float* scale, int m, int k, vo
 }
 
 }  // extern "C"
+
+// ---- MI355X tile layout (load time) ------------------------------------------------------
+
+namespace qlx {
+
+// dst block (tile t, step s) = 2 KB ordered [j][c][r][16 B], taken from row 16t + r, bytes
+// 128s + 64j + 16c of the row-major source. One thread per 16-byte chunk.
+__global__ void __launch_bounds__(256)
+tile_rows_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, int rows, int row_bytes) {
+  const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)rows * row_bytes / 16;
+  if (o >= total) return;
+  const int within = (int)(o & 127);  // 128 chunks per 2 KB block
+  const size_t blk = o >> 7;
+  const int steps = row_bytes >> 7;
+  const int t = (int)(blk / steps), s = (int)(blk % steps);
+  const int j = within >> 6, c = (within >> 4) & 3, r = within & 15;
+  dst[o] = src[((size_t)(16 * t + r) * row_bytes + 128 * s + 64 * j + 16 * c) / 16];
+}
+
+}  // namespace qlx
+
+extern "C" int qlx_tile_rows(const void* src, void* dst, int rows, int row_bytes, void* stream) {
+  QLX_REQUIRE(rows > 0 && rows % 16 == 0, "rows=%d must be a positive multiple of 16", rows);
+  QLX_REQUIRE(row_bytes > 0 && row_bytes % 128 == 0, "row bytes %d must be a multiple of 128", row_bytes);
+  const size_t chunks = (size_t)rows * row_bytes / 16;
+  qlx::tile_rows_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint4*)src, (uint4*)dst, rows, row_bytes);
+  QLX_LAUNCH_CHECK("tile_rows");
+}

@@ -48,9 +48,10 @@ SIGNATURES = {
     "qlx_quantize_act_int8": ([_P, _P, _P, _I, _I, _P], _I),
     "qlx_plan_linear": ([_I, _I, _I, _I, _I, _PLAN], _I),
     "qlx_plan_tickets": ([_PLAN, _I, _I, _I, _I], _I),
-    "qlx_linear_w8a16": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
-    "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
-    "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_tile_rows": ([_P, _P, _I, _I, _P], _I),
+    "qlx_linear_w8a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8wo": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_int8": ([_P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
@@ -59,6 +60,7 @@ SIGNATURES = {
     "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
+    "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 
 _lib = None

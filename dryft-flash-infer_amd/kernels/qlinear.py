@@ -14,12 +14,60 @@ for the ``cuda_fp8.matmul`` call the engine makes per projection
   is quantized per token inside the linear: ``s = max(amax/448, 1e-12)`` (fp32),
   ``e4m3(clamp(x/s, +-448))``.
 
+``prepare(packed)`` relays a packed weight into the MI355X tile layout at load time (the
+role of ``cuda_fp8.prepare``, engine/kernels/cuda_fp8.py:1220-1224); every linear accepts
+either the row-major packed tuple or the prepared ``Tiled`` weight.
+
 All work runs in the gfx950 library; tensors must be on the GPU.
 """
 
 import torch
 
 from . import _lib, _linear
+
+
+class Tiled:
+    """A packed weight relaid into 16-row x 128-byte tiles (``qlx_tile_rows``).
+
+    ``weight`` holds the same bytes as the packed codes, in tile order; ``scale`` is
+    unchanged; ``rows`` and ``k`` are the logical shape; ``fmt`` names the format.
+    """
+
+    __slots__ = ("weight", "scale", "rows", "k", "fmt")
+
+    def __init__(self, weight, scale, rows, k, fmt):
+        self.weight, self.scale, self.rows, self.k, self.fmt = weight, scale, rows, k, fmt
+
+    def bytes_moved(self):
+        return self.weight.numel() * self.weight.element_size() + self.scale.numel() * self.scale.element_size()
+
+
+def prepare(packed, fmt=None):
+    """Relay ``(codes, scales)`` of any north-star format into the tile layout."""
+    q, s = packed
+    _lib.require_device(q, s)
+    rows = q.shape[0]
+    row_bytes = q.shape[1] * q.element_size()
+    if fmt is None:
+        fmt = "w4a16" if q.dtype == torch.int32 else ("fp8" if q.dtype == torch.float8_e4m3fn else "w8a16")
+    k = row_bytes * 2 if fmt == "w4a16" else row_bytes
+    if rows % 16 or row_bytes % 128:
+        raise ValueError(f"tiles need rows % 16 == 0 and 128-byte rows (got {rows} x {row_bytes} B)")
+    out = torch.empty_like(q)
+    _lib.call("qlx_tile_rows", _lib.ptr(q), _lib.ptr(out), rows, row_bytes, _lib.stream(q.device))
+    return Tiled(out, s, rows, k, fmt)
+
+
+def _unpack(packed, fmt):
+    """(codes, scales, rows, k, tiled) of a packed tuple or a Tiled weight."""
+    if isinstance(packed, Tiled):
+        if packed.fmt != fmt:
+            raise ValueError(f"a {packed.fmt} weight cannot feed a {fmt} linear")
+        return packed.weight, packed.scale, packed.rows, packed.k, 1
+    q, s = packed
+    rows = q.shape[0]
+    k = q.shape[1] * 8 if fmt == "w4a16" else q.shape[1]
+    return q, s, rows, k, 0
 
 
 def _bf16_2d(t, what):
@@ -115,34 +163,35 @@ def _mode(swiglu=False, planes=False):
 
 def linear_w8a16(x, packed, config=None, planes=False, swiglu=False):
     """``x @ deq(W).T`` for W8A16 per-channel weights; bf16 ``[M, N]`` (SwiGLU: ``[M, N/2]``)."""
-    q, s = packed
-    n, k = q.shape
+    q, s, n, k, tiled = _unpack(packed, "w8a16")
     _check_x(x, k)
     _lib.require_device(q, s)
+    if s.numel() != n:
+        raise ValueError("W8A16 scales are one bf16 per output channel")
     return _linear.run(_lib.FMT_W8A16, "qlx_linear_w8a16", x, n, k,
-                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
 def linear_w4a16(x, packed, config=None, planes=False, swiglu=False):
     """``x @ deq(W).T`` for W4A16 group-128 weights."""
-    q, s = packed
-    n, k = q.shape[0], q.shape[1] * 8
+    q, s, n, k, tiled = _unpack(packed, "w4a16")
     _check_x(x, k)
     _lib.require_device(q, s)
-    if q.dtype != torch.int32 or s.shape != (n, k // 128):
+    if q.dtype != torch.int32 or tuple(s.shape) != (n, k // 128):
         raise ValueError("W4A16 weights are int32 [N, K/8] with bf16 scales [N, K/128]")
     return _linear.run(_lib.FMT_W4A16, "qlx_linear_w4a16", x, n, k,
-                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
 def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False):
     """``(x_q s_x) @ (W_q s_w).T`` with the activation quantized per token in the kernel."""
-    q, s = packed
-    n, k = q.shape
+    q, s, n, k, tiled = _unpack(packed, "fp8")
     _check_x(x, k)
     _lib.require_device(q, s)
+    if s.numel() != n:
+        raise ValueError("FP8 W8A8 weight scales are one bf16 per output channel")
     return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8", x, n, k,
-                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), mode=_mode(swiglu, planes), config=config)
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
 def splits(fmt, m, n, k, config=None, swiglu=False):
@@ -159,5 +208,7 @@ FORMATS = {
 
 def weight_bytes(packed):
     """Bytes a linear streams for its weight (codes + scales)."""
+    if isinstance(packed, Tiled):
+        return packed.bytes_moved()
     q, s = packed
     return q.numel() * q.element_size() + s.numel() * s.element_size()

@@ -102,7 +102,17 @@ int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void
  * q int8 [m][k] in fragment order, scale fp32 [m][k/64]. */
 int qlx_quantize_act_int8(const void* x, void* q, float* scale, int m, int k, void* stream);
 
+/* MI355X tile layout of a row-major [rows][row_bytes] weight (rows % 16 == 0, row_bytes %
+ * 128 == 0): the 16-row x 128-byte block (tile t, step s) is stored contiguously at
+ * (t * row_bytes/128 + s) * 2048, ordered [j 2][c 4][r 16][16 bytes] = row 16t + r, bytes
+ * 128s + 64j + 16c -- the order a wave's loads consume it, so every load instruction reads
+ * 1 KB of consecutive bytes. The load-time relayout counterpart of cuda_fp8.Prepared's tiles
+ * (engine/kernels/cuda_fp8.py:1183-1205). */
+int qlx_tile_rows(const void* src, void* dst, int rows, int row_bytes, void* stream);
+
 /* ---- linear layers: y = x . W^T (x bf16 [m][k] unless stated) ------------------------ */
+/* The north-star linears take `tiled` = 1 for a weight relaid by qlx_tile_rows, 0 for the
+ * row-major packed weight. */
 
 /* Default plan for a linear call (the selection the reference races in
  * engine/kernels/gemm.py:134-261 / cuda_fp8._plan:1255-1276). fmt is one of QLX_FMT_*. */
@@ -119,18 +129,18 @@ int qlx_plan_tickets(const qlx_plan* plan, int fmt, int m, int n, int k);
 /* W8A16 per output channel. Replaces the W8A16 call of cuda_fp8.matmul
  * (engine/kernels/cuda_fp8.py:1316-1330) for the north-star per-channel format. */
 int qlx_linear_w8a16(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
-                     int k, const qlx_plan* plan, void* stream);
+                     int k, int tiled, const qlx_plan* plan, void* stream);
 
 /* W4A16, group-128 bf16 scales, int32 k32 words. Replaces cuda_fp8.matmul / matmul_partials /
  * gate_up_swiglu at bits=4 (engine/kernels/cuda_fp8.py:1307-1330, 1381-1390). */
 int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
-                     int k, const qlx_plan* plan, void* stream);
+                     int k, int tiled, const qlx_plan* plan, void* stream);
 
 /* FP8 e4m3 W8A8: per-channel bf16 weight scales, activation quantized per token inside the
  * kernel (same arithmetic as qlx_quantize_fp8_act). Replaces cuda_int8.matmul's role
  * (engine/kernels/cuda_int8.py:251-281) for the north-star FP8 format. */
 int qlx_linear_fp8_w8a8(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
-                        int k, const qlx_plan* plan, void* stream);
+                        int k, int tiled, const qlx_plan* plan, void* stream);
 
 /* cuda_fp8.matmul / matmul_partials / gate_up_swiglu on the reference's own Prepared weights
  * (engine/kernels/cuda_fp8.py:1279-1330, 1381-1390): bits 8 (tiled or row-major) or 4. */
@@ -179,6 +189,13 @@ int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* plane
  * cuda_small.py:89-110). */
 int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, int rows, int inter,
                void* stream);
+
+/* ---- measurement ------------------------------------------------------------------- */
+
+/* Read `bytes` (multiple of 16) from p with 16-byte loads over `blocks` workgroups of 256
+ * threads, writing one word per workgroup to sink[blocks]: the HBM read floor the linears
+ * are compared with (the reference's stream probe, bench/tiled_probe.py:20-31). */
+int qlx_stream_read(const void* p, long long bytes, void* sink, int blocks, void* stream);
 
 #ifdef __cplusplus
 }

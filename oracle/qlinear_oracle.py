@@ -15,7 +15,7 @@ __all__ = [
     "f32_to_e4m3", "e4m3_to_f32",
     "permutation", "quantize", "dequantize", "prepare_weight", "row_major",
     "fp8_quantize", "int8_natural", "int8_prepare", "int8_quantize_activation",
-    "pack_int4_k32", "unpack_int4_k32", "quantize_int4_g128", "quantize_w8_per_channel",
+    "pack_int4_k32", "unpack_int4_k32", "tile_rows", "quantize_int4_g128", "quantize_w8_per_channel",
     "quantize_fp8_activation",
     "linear_dequant", "linear_exact_grouped", "linear_fp8_w8a8", "linear_w8a8_int8",
     "reduce_partials", "residual_partials", "rms_norm", "add_rms_norm",
@@ -293,6 +293,19 @@ def unpack_int4_k32(words):
     for i in range(8):
         out[:, :, i] = (w >> (4 * i)) & 0xF
     return out.reshape(n, kw * 8)
+
+
+def tile_rows(data):
+    """MI355X tile layout of a row-major weight (any dtype, viewed as bytes).
+
+    Block (tile t, step s) -- rows 16t..16t+15, bytes 128s..128s+127 -- is stored as
+    [j 2][c 4][r 16][16 bytes] holding row 16t + r, bytes 128s + 64j + 16c. Pinned by a
+    brute-force per-byte check and by round trip in the tests.
+    """
+    b = np.ascontiguousarray(data).view(np.uint8)
+    rows, width = b.shape
+    v = b.reshape(rows // 16, 16, width // 128, 2, 4, 16)        # t, r, s, j, c, byte
+    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5)).reshape(rows, width)
 
 
 def quantize_int4_g128(w_bits, group=128):

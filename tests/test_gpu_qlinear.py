@@ -205,3 +205,27 @@ def test_contract_violations_raise_before_launch():
         qlinear.linear_w4a16(acts(1, 256, 0), (q, s))  # CPU activation
     with pytest.raises(ValueError):
         qlinear.linear_w4a16(acts(1, 256, 0).to(DEV), (q, s), config=(4, 3, 1, 1))
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+def test_tiled_weights_match_oracle_and_row_major_bitwise(fmt):
+    """prepare() relays bytes exactly as the oracle's tile map; linears give identical bits."""
+    quant, linear, code = qlinear.FORMATS[fmt]
+    n, k = 4096, 2560
+    w = weights(n, k, 10).to(DEV)
+    packed = quant(w)
+    tiled = qlinear.prepare(packed)
+    raw = packed[0].view(torch.uint8).cpu().numpy() if fmt == "fp8" else packed[0].cpu().numpy()
+    want = O.tile_rows(raw)
+    assert np.array_equal(tiled.weight.cpu().view(torch.uint8).numpy().reshape(want.shape), want)
+    for m in (1, 8, 33):
+        x = acts(m, k, 600 + m).to(DEV)
+        for cfg in (None, (4, 4, 1, 2), (8, 2, 2, 1)):
+            for sw in (False, True):
+                try:
+                    a = linear(x, packed, config=cfg, swiglu=sw)
+                except ValueError as exc:
+                    assert "LDS" in str(exc)
+                    continue
+                b = linear(x, tiled, config=cfg, swiglu=sw)
+                assert torch.equal(a, b), (fmt, m, cfg, sw)
