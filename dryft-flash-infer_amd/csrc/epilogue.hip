@@ -39,11 +39,13 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
                     uint16_t* __restrict__ res, uint16_t* __restrict__ y, int8_t* __restrict__ q,
                     float* __restrict__ qs, int rows, int n, float eps) {
   extern __shared__ float rbuf[];  // the row's residual, fp32
-  __shared__ float part[4];
+  __shared__ double part[4];
   const int row = blockIdx.x;
   const size_t base = (size_t)row * n;
   const bool add = delta != nullptr || planes != nullptr;
-  float ss = 0.f;
+  // Sum of squares in fp64: each square of a bf16 value is exact there and so is the sum of
+  // a hidden row's worth, which makes the scale independent of the summation order.
+  double ss = 0.0;
   for (int c = threadIdx.x; c < n; c += 256) {
     float r = bf2f(x[base + c]);
     if (add) {
@@ -59,13 +61,15 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
       if (res) res[base + c] = f2bf(r);
     }
     rbuf[c] = r;
-    ss += r * r;
+    ss += (double)r * (double)r;
   }
-  ss = wave_sum(ss);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
-  const float total = ((part[0] + part[1]) + part[2]) + part[3];
-  const float scale = 1.0f / sqrtf(total / (float)n + eps);
+  const double total = ((part[0] + part[1]) + part[2]) + part[3];
+  // mean rounded to fp32, + eps and 1/sqrt in fp32, as torch's rsqrt(mean + eps)
+  const float scale = 1.0f / sqrtf((float)(total / (double)n) + eps);
   for (int c = threadIdx.x; c < n; c += 256) {
     const float v = round_bf(round_bf(rbuf[c] * scale) * bf2f(w[c]));
     rbuf[c] = v;

@@ -41,6 +41,9 @@ struct GemmArgs {
   const void* ws;   // weight scales
   const void* x;    // activation (bf16, or int8 for FMT_INT8)
   const float* xs;  // activation scales (FMT_INT8)
+  const void* x2;   // FMT_INT8 second (residual) activation component, or null
+  const float* xs2;
+  int comp;         // FMT_INT8 activation components (1 or 2)
   void* y;
   float* work;
   int* tickets;
@@ -58,9 +61,11 @@ struct GemmArgs {
 
 // Weight row held by tile row r (0..15). SwiGLU tiles pair gate rows 8t..8t+7 with the
 // matching up rows I+8t..I+8t+7 (engine/kernels/cuda_fp8.py:208-212 pairs them per lane).
+// Rows past n (a partial last tile of a row-major weight) read row n - 1; their outputs are
+// dropped.
 __device__ __forceinline__ int weight_row(const GemmArgs& a, int tile, int r) {
   if (a.mode == QLX_MODE_SWIGLU) return r < 8 ? 8 * tile + r : a.half + 8 * tile + r - 8;
-  return 16 * tile + r;
+  return min(16 * tile + r, a.n - 1);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -483,9 +488,18 @@ struct FmtInt8 {
         const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb);
         const i32x4 b = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
         const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
-        const float sx = reinterpret_cast<const float*>(lds + a.off_sx)[mrow[mt] * a.xb_stride + srel * 2 + j];
+        const float* sxp = reinterpret_cast<const float*>(lds + a.off_sx);
+        const float sx = sxp[mrow[mt] * a.xb_stride + srel * 2 + j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf((float)d[i] * sx, sw[i], acc[mt][i]);
+        if (a.comp == 2) {  // the residual component, accumulated after the first (cuda_int8.py:207-216)
+          const uint4 rv = *reinterpret_cast<const uint4*>(lds + a.m * a.xstride + xoff[mt] + kb);
+          const i32x4 rb = {(int)rv.x, (int)rv.y, (int)rv.z, (int)rv.w};
+          const i32x4 d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, rb, i32x4{0, 0, 0, 0}, 0, 0, 0);
+          const float sr = sxp[(a.m + mrow[mt]) * a.xb_stride + srel * 2 + j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf((float)d2[i] * sr, sw[i], acc[mt][i]);
+        }
       }
     }
   }
@@ -573,16 +587,20 @@ __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) 
 // cuda_int8 prologue: int8 activation slice and its fp32 group scales.
 __device__ void stage_int8_act(const GemmArgs& a, char* lds, int step0, int nst) {
   const int cps = nst * 8;
-  for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
-    const int mm = q / cps, kc = q - mm * cps;
-    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = *reinterpret_cast<const uint4*>(
-        reinterpret_cast<const int8_t*>(a.x) + (size_t)mm * a.k + step0 * 128 + kc * 16);
-  }
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
   const int gps = 2 * nst;
-  for (int q = threadIdx.x; q < a.m * gps; q += blockDim.x) {
-    const int mm = q / gps, j = q - mm * gps;
-    sx[mm * a.xb_stride + j] = a.xs[(size_t)mm * (a.k >> 6) + 2 * step0 + j];
+  for (int c = 0; c < a.comp; ++c) {  // component c at token rows c*m .. c*m + m - 1
+    const int8_t* xq = reinterpret_cast<const int8_t*>(c ? a.x2 : a.x);
+    const float* xsc = c ? a.xs2 : a.xs;
+    for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
+      const int mm = q / cps, kc = q - mm * cps;
+      *reinterpret_cast<uint4*>(lds + (c * a.m + mm) * a.xstride + kc * 16) =
+          *reinterpret_cast<const uint4*>(xq + (size_t)mm * a.k + step0 * 128 + kc * 16);
+    }
+    for (int q = threadIdx.x; q < a.m * gps; q += blockDim.x) {
+      const int mm = q / gps, j = q - mm * gps;
+      sx[(c * a.m + mm) * a.xb_stride + j] = xsc[(size_t)mm * (a.k >> 6) + 2 * step0 + j];
+    }
   }
 }
 
@@ -758,8 +776,9 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
         store_coherent(pl + a.half + 8 * tile + nl, u);
       }
     } else {
-      const float v = combined(tl, nl, mm);
       const int row = 16 * tile + nl;
+      if (row >= a.n) continue;
+      const float v = combined(tl, nl, mm);
       if (a.mode == QLX_MODE_PLANES)
         a.work[((size_t)s * a.m + mm) * a.n + row] = v;
       else if (!direct)
@@ -803,6 +822,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
       y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
     } else {
       const int row = 16 * tile + nl;
+      if (row >= a.n) continue;
       const float* p = a.work + (size_t)mm * a.n + row;
       float v = 0.f;
       for (int sp = 0; sp < a.splits; ++sp) v += load_coherent(p + sp * plane);

@@ -7,8 +7,10 @@
 
 namespace qlx {
 
-// Dynamic LDS kept per workgroup; two workgroups of 4 waves then fit one CU.
-constexpr int kLdsLimit = 64 * 1024;
+// LDS per workgroup: plans aim at <= 64 KB (two or more workgroups per CU); gfx950 allows up
+// to 160 KB for one workgroup, used when a wide batch cannot fit otherwise.
+constexpr int kLdsTarget = 64 * 1024;
+constexpr int kLdsLimit = 159 * 1024;  // 160 KB less room for the kernel's static LDS
 
 struct FmtInfo {
   int kstep, nsc, xbytes, bias;
@@ -30,14 +32,16 @@ inline int layout(const FmtInfo& fi, const qlx_plan& p, int m, int n, int k, Gem
   a.nsteps = k / fi.kstep;
   a.sps = (a.nsteps + p.splits - 1) / p.splits;
   a.splits = (a.nsteps + a.sps - 1) / a.sps;
-  a.ntiles = n / 16;  // SwiGLU tiles hold 8 gate + 8 up rows: (n/2)/8 = n/16 as well
+  // SwiGLU tiles hold 8 gate + 8 up rows: (n/2)/8 = n/16; otherwise the last tile may be partial.
+  a.ntiles = p.mode == QLX_MODE_SWIGLU ? n / 16 : (n + 15) / 16;
+  const int copies = a.comp > 1 ? a.comp : 1;  // activation components staged
   a.kw = p.kw;
   a.rt = (p.waves / p.kw) * p.rw;
   a.tile_groups = (a.ntiles + a.rt - 1) / a.rt;
   a.half = n / 2;
   const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   a.xstride = round16(a.sps * fi.kstep * fi.xbytes + 16);
-  const int xbytes = m * a.xstride;
+  const int xbytes = copies * m * a.xstride;
   const int red = p.waves * p.rw * 16 * 16 * mt * 4;
   a.off_sc = round16(xbytes > red ? xbytes : red);
   a.sc_stride = 16 * a.rt;
@@ -46,13 +50,14 @@ inline int layout(const FmtInfo& fi, const qlx_plan& p, int m, int n, int k, Gem
   a.xb_stride = a.sps * (fi.nsc > 1 ? fi.nsc : 1);
   const int xb_floats = fi.bias ? m * a.xb_stride : 0;
   a.off_sx = round16(a.off_xb + xb_floats * 4);
-  return a.off_sx + m * (a.xb_stride > 2 ? a.xb_stride : 2) * 4;
+  return a.off_sx + copies * m * (a.xb_stride > 2 ? a.xb_stride : 2) * 4;
 }
 
 inline int check_plan(const qlx_plan* p, int m, int n, int k, int kstep) {
   QLX_REQUIRE(p != nullptr, "plan is NULL");
   QLX_REQUIRE(m >= 1 && m <= 64, "m=%d must be in 1..64", m);
-  QLX_REQUIRE(n >= 16 && n % 16 == 0, "n=%d must be a positive multiple of 16", n);
+  QLX_REQUIRE(n >= 1, "n=%d must be positive", n);
+  QLX_REQUIRE(p == nullptr || p->mode != QLX_MODE_SWIGLU || n % 16 == 0, "SwiGLU needs 2I rows with I %% 8 == 0");
   QLX_REQUIRE(k >= kstep && k % kstep == 0, "K=%d must be a positive multiple of %d", k, kstep);
   QLX_REQUIRE(p->mode >= 0 && p->mode <= 2, "bad mode %d", p->mode);
   QLX_REQUIRE(p->waves == 4 || p->waves == 8, "waves must be 4 or 8");
@@ -62,13 +67,28 @@ inline int check_plan(const qlx_plan* p, int m, int n, int k, int kstep) {
   return QLX_OK;
 }
 
+// Opt a kernel into more than 64 KB of dynamic LDS (raised to what the launch needs).
+template <class F, int MT, int RW, int WAVES, bool SW>
+hipError_t allow_lds(int lds) {
+  static int allowed = 64 * 1024;
+  if (lds <= allowed) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<F, MT, RW, WAVES, SW>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e == hipSuccess) allowed = lds;
+  return e;
+}
+
 template <class F, int MT, int RW, int WAVES>
 hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   const int grid = a.tile_groups * a.splits;
-  if (a.mode == QLX_MODE_SWIGLU)
+  hipError_t e;
+  if (a.mode == QLX_MODE_SWIGLU) {
+    if ((e = allow_lds<F, MT, RW, WAVES, true>(lds)) != hipSuccess) return e;
     gemm_kernel<F, MT, RW, WAVES, true><<<grid, WAVES * 64, lds, st>>>(a);
-  else
+  } else {
+    if ((e = allow_lds<F, MT, RW, WAVES, false>(lds)) != hipSuccess) return e;
     gemm_kernel<F, MT, RW, WAVES, false><<<grid, WAVES * 64, lds, st>>>(a);
+  }
   return hipGetLastError();
 }
 
@@ -82,6 +102,7 @@ template <class F>
 int launch_gemm(const char* name, GemmArgs a, const qlx_plan* plan, int m, int n, int k, void* stream) {
   int rc = check_plan(plan, m, n, k, F::KSTEP);
   if (rc) return rc;
+  QLX_REQUIRE(!a.tiled || n % 16 == 0, "%s: tiled weights have rows %% 16 == 0 (n=%d)", name, n);
   const qlx_plan& p = *plan;
   const int lds = layout(info<F>(), p, m, n, k, a);
   QLX_REQUIRE(lds <= kLdsLimit, "%s: plan needs %d bytes of LDS (> %d); use more splits", name, lds, kLdsLimit);

@@ -15,12 +15,17 @@ extern "C" int qlx_linear_fp8wo(const void* w, const void* w_scale, const void* 
 }
 
 extern "C" int qlx_linear_int8(const void* w, const void* w_scale, const void* xq, const float* x_scale,
-                               void* y, int m, int n, int k, const qlx_plan* plan, void* stream) {
+                               const void* xq2, const float* x_scale2, void* y, int m, int n, int k,
+                               const qlx_plan* plan, void* stream) {
   qlx::GemmArgs a = {};
   a.w = w;
   a.ws = w_scale;
   a.x = xq;
   a.xs = x_scale;
+  a.x2 = xq2;
+  a.xs2 = x_scale2;
+  a.comp = xq2 ? 2 : 1;
   a.y = y;
+  QLX_REQUIRE(!xq2 || x_scale2, "a second activation component needs its scales");
   return qlx::launch_gemm<qlx::FmtInt8>("linear_int8", a, plan, m, n, k, stream);
 }

@@ -34,7 +34,7 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
   QLX_REQUIRE(plan != nullptr, "plan is NULL");
   const qlx::FmtInfo fi = fmt_info(fmt);
   QLX_REQUIRE(fi.kstep > 0, "unknown format %d", fmt);
-  QLX_REQUIRE(m >= 1 && m <= 64 && n >= 16 && n % 16 == 0 && k >= fi.kstep && k % fi.kstep == 0,
+  QLX_REQUIRE(m >= 1 && m <= 64 && n >= 1 && k >= fi.kstep && k % fi.kstep == 0,
               "shape m=%d n=%d k=%d does not fit format %d", m, n, k, fmt);
   qlx_plan p = {};
   p.mode = mode;
@@ -42,7 +42,7 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
   p.rw = m > 16 ? 2 : 1;
   p.splits = 1;
   const int nsteps = k / fi.kstep;
-  const int ntiles = n / 16;
+  const int ntiles = (n + 15) / 16;
   // kw: waves sharing one tile's K range, the smallest that still gives kMinGroups groups
   // (and at least one step per wave).
   p.kw = 8;
@@ -53,11 +53,21 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
       break;
     }
   }
-  // Large m stages a wide activation slice: split K until the workgroup's LDS fits.
+  // Large m stages a wide activation slice: split K until the workgroup's LDS fits the
+  // 64 KB target; a plan whose reduction buffer alone is larger drops to 4 waves.
   qlx::GemmArgs a = {};
   for (;;) {
     const int lds = qlx::layout(fi, p, m, n, k, a);
-    if (lds <= qlx::kLdsLimit || p.splits >= nsteps) break;
+    if (lds <= qlx::kLdsTarget) break;
+    if (p.splits >= nsteps) {
+      if (p.waves == 8) {
+        p.waves = 4;
+        if (p.kw > 4) p.kw = 4;
+        p.splits = 1;
+        continue;
+      }
+      break;  // <= 160 KB is still launchable
+    }
     ++p.splits;
   }
   qlx::layout(fi, p, m, n, k, a);
@@ -73,4 +83,27 @@ extern "C" int qlx_plan_tickets(const qlx_plan* plan, int fmt, int m, int n, int
   qlx::GemmArgs a = {};
   qlx::layout(fi, *plan, m, n, k, a);
   return a.tile_groups;
+}
+
+// Normalise a plan's K splits (every slice non-empty); with `grow`, first raise them until
+// the LDS fits, as the reference's _plan grows split-K until shared memory fits
+// (engine/kernels/cuda_fp8.py:1255-1276). comp: activation components (FMT_INT8).
+extern "C" int qlx_plan_fit(qlx_plan* plan, int fmt, int m, int n, int k, int comp, int grow) {
+  QLX_REQUIRE(plan != nullptr, "plan is NULL");
+  const qlx::FmtInfo fi = fmt_info(fmt);
+  QLX_REQUIRE(fi.kstep > 0, "unknown format %d", fmt);
+  int rc = qlx::check_plan(plan, m, n, k, fi.kstep);
+  if (rc) return rc;
+  qlx::GemmArgs a = {};
+  a.comp = comp;
+  const int nsteps = k / fi.kstep;
+  if (plan->splits > nsteps) plan->splits = nsteps;
+  while (grow) {
+    const int lds = qlx::layout(fi, *plan, m, n, k, a);
+    if (lds <= qlx::kLdsTarget || plan->splits >= nsteps) break;
+    ++plan->splits;
+  }
+  qlx::layout(fi, *plan, m, n, k, a);
+  plan->splits = a.splits;
+  return QLX_OK;
 }

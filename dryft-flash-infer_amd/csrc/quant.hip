@@ -292,9 +292,11 @@ int8_prepare_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ dst, i
 }
 
 // One wave per (row, 64-group): s = max(amax/127, 1e-20); q = rint(x/s) at fragment position.
+// With q2 != null the residual x - q*s is quantized the same way (cuda_int8.py:69-74).
 __global__ void __launch_bounds__(256)
 quantize_act_int8_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-                         float* __restrict__ scale, int m, int k) {
+                         float* __restrict__ scale, int8_t* __restrict__ q2, float* __restrict__ scale2,
+                         int m, int k) {
   const int lane = threadIdx.x & 63;
   const long long gid = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int groups = k / 64;
@@ -303,8 +305,16 @@ quantize_act_int8_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q,
   const float v = bf2f(x[(size_t)row * k + g * 64 + i8_natural(lane)]);
   const float amax = wave_max(fabsf(v));
   const float s = fmaxf(amax / 127.f, 1e-20f);
-  q[(size_t)row * k + g * 64 + lane] = (int8_t)(int)rintf(v / s);
+  const float qv = rintf(v / s);
+  q[(size_t)row * k + g * 64 + lane] = (int8_t)(int)qv;
   if (lane == 0) scale[(size_t)row * groups + g] = s;
+  if (q2) {
+    const float r = v - qv * s;
+    const float ramax = wave_max(fabsf(r));
+    const float sr = fmaxf(ramax / 127.f, 1e-20f);
+    q2[(size_t)row * k + g * 64 + lane] = (int8_t)(int)rintf(r / sr);
+    if (lane == 0) scale2[(size_t)row * groups + g] = sr;
+  }
 }
 
 static inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
@@ -387,11 +397,13 @@ int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void
   QLX_LAUNCH_CHECK("int8_prepare");
 }
 
-int qlx_quantize_act_int8(const void* x, void* q, float* scale, int m, int k, void* stream) {
+int qlx_quantize_act_int8(const void* x, void* q, float* scale, void* q2, float* scale2, int m, int k,
+                          void* stream) {
   QLX_REQUIRE(m > 0 && k > 0 && k % 64 == 0, "activation K=%d must be a multiple of 64", k);
+  QLX_REQUIRE(!q2 || scale2, "a second component needs its scales");
   const size_t work = (size_t)m * (k / 64);
   quantize_act_int8_kernel<<<blocks_for(work, 4), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)x, (int8_t*)q, scale, m, k);
+      (const uint16_t*)x, (int8_t*)q, scale, (int8_t*)q2, scale2, m, k);
   QLX_LAUNCH_CHECK("quantize_act_int8");
 }
 

@@ -45,16 +45,17 @@ SIGNATURES = {
     "qlx_quantize_fp8_weight": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "qlx_quantize_fp8_act": ([_P, _P, _P, _I, _I, _P], _I),
     "qlx_int8_prepare": ([_P, _P, _I, _I, _P], _I),
-    "qlx_quantize_act_int8": ([_P, _P, _P, _I, _I, _P], _I),
+    "qlx_quantize_act_int8": ([_P, _P, _P, _P, _P, _I, _I, _P], _I),
     "qlx_plan_linear": ([_I, _I, _I, _I, _I, _PLAN], _I),
     "qlx_plan_tickets": ([_PLAN, _I, _I, _I, _I], _I),
+    "qlx_plan_fit": ([_PLAN, _I, _I, _I, _I, _I, _I], _I),
     "qlx_tile_rows": ([_P, _P, _I, _I, _P], _I),
     "qlx_linear_w8a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8wo": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
-    "qlx_linear_int8": ([_P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_int8": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
     "qlx_reduce_planes": ([_P, _P, _LL, _I, _P], _I),
     "qlx_residual_planes": ([_P, _P, _P, _LL, _I, _P], _I),
     "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),

@@ -12,37 +12,31 @@ import torch
 from . import _lib
 
 
-def make_plan(fmt, mode, m, n, k, config=None):
+def make_plan(fmt, mode, m, n, k, config=None, fit=False, comp=1):
+    """A plan from ``config`` (or the library default) with its splits normalised by the
+    library (every K slice non-empty); ``fit`` first grows the splits until the LDS fits.
+    The library default always fits."""
     plan = _lib.Plan()
     if config is None:
         _lib.check(_lib.lib().qlx_plan_linear(fmt, mode, m, n, k, plan), "plan_linear")
-        return plan
-    waves, kw, rw, splits = config
-    plan.mode, plan.waves, plan.kw, plan.rw, plan.splits = mode, waves, kw, rw, splits
+        fit = True
+    else:
+        waves, kw, rw, splits = config
+        plan.mode, plan.waves, plan.kw, plan.rw, plan.splits = mode, waves, kw, rw, splits
+    _lib.check(_lib.lib().qlx_plan_fit(plan, fmt, m, n, k, comp, int(fit)), "plan_fit")
     return plan
 
 
-def effective_splits(fmt, kstep, k, splits):
-    """Non-empty K slices for a requested split count (every slice holds >= 1 step)."""
-    steps = k // kstep
-    per = -(-steps // max(1, min(splits, steps)))
-    return -(-steps // per)
-
-
-KSTEP = {_lib.FMT_W8A16: 64, _lib.FMT_W4A16: 128, _lib.FMT_FP8: 64, _lib.FMT_REF8: 128,
-         _lib.FMT_REF4: 128, _lib.FMT_FP8WO: 64, _lib.FMT_INT8: 64}
-
-
 def run(fmt, entry, x, n, k, args_before_y, args_after_dims=(), mode=_lib.MODE_BF16, config=None,
-        m=None):
+        m=None, fit=False, comp=1):
     """Launch ``entry(*args_before_y, y, m, n, k, *args_after_dims, plan, stream)``.
 
     Returns bf16 ``[m, n]`` (``[m, n/2]`` for SwiGLU) or fp32 planes ``[splits, m, n]``.
     """
     m = x.shape[0] if m is None else m
     device = x.device
-    plan = make_plan(fmt, mode, m, n, k, config)
-    splits = effective_splits(fmt, KSTEP[fmt], k, plan.splits)
+    plan = make_plan(fmt, mode, m, n, k, config, fit, comp)
+    splits = plan.splits
     if mode == _lib.MODE_PLANES:
         plan.splits = splits
         out = torch.empty((splits, m, n), dtype=torch.float32, device=device)
@@ -60,6 +54,5 @@ def run(fmt, entry, x, n, k, args_before_y, args_after_dims=(), mode=_lib.MODE_B
     return out
 
 
-def splits_for(fmt, mode, m, n, k, config=None):
-    plan = make_plan(fmt, mode, m, n, k, config)
-    return effective_splits(fmt, KSTEP[fmt], k, plan.splits)
+def splits_for(fmt, mode, m, n, k, config=None, fit=False, comp=1):
+    return make_plan(fmt, mode, m, n, k, config, fit, comp).splits

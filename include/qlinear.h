@@ -98,9 +98,11 @@ int qlx_quantize_fp8_act(const void* x, void* code, float* scale, int m, int k, 
  * row-major bytes. */
 int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void* stream);
 
-/* cuda_int8.quantize_activation, one component (engine/kernels/cuda_int8.py:58-88):
- * q int8 [m][k] in fragment order, scale fp32 [m][k/64]. */
-int qlx_quantize_act_int8(const void* x, void* q, float* scale, int m, int k, void* stream);
+/* cuda_int8.quantize_activation (engine/kernels/cuda_int8.py:58-88): q int8 [m][k] in
+ * fragment order, scale fp32 [m][k/64]; with q2 != NULL also the residual component
+ * (components=2). */
+int qlx_quantize_act_int8(const void* x, void* q, float* scale, void* q2, float* scale2, int m, int k,
+                          void* stream);
 
 /* MI355X tile layout of a row-major [rows][row_bytes] weight (rows % 16 == 0, row_bytes %
  * 128 == 0): the 16-row x 128-byte block (tile t, step s) is stored contiguously at
@@ -125,6 +127,10 @@ int qlx_tile_rows(const void* src, void* dst, int rows, int row_bytes, void* str
 #define QLX_FMT_INT8 6    /* cuda_int8: int8 [n][k] fragment order, fp16 scale [n][k/64] */
 int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan* plan);
 int qlx_plan_tickets(const qlx_plan* plan, int fmt, int m, int n, int k);
+/* Normalise plan->splits so every K slice is non-empty; with `grow`, first raise it until the
+ * plan's LDS fits (the reference's _plan, engine/kernels/cuda_fp8.py:1255-1276). comp =
+ * activation components (2 only for QLX_FMT_INT8 with a residual component). */
+int qlx_plan_fit(qlx_plan* plan, int fmt, int m, int n, int k, int comp, int grow);
 
 /* W8A16 per output channel. Replaces the W8A16 call of cuda_fp8.matmul
  * (engine/kernels/cuda_fp8.py:1316-1330) for the north-star per-channel format. */
@@ -154,9 +160,10 @@ int qlx_linear_fp8wo(const void* w, const void* w_scale, const void* x, void* y,
 
 /* cuda_int8.matmul_quantized (engine/kernels/cuda_int8.py:251-276): int8 weights and
  * activations in fragment order, fp16 weight scales [n][k/64], fp32 activation scales
- * [m][k/64]. */
+ * [m][k/64]; xq2/x_scale2 (or NULL) the optional residual component. */
 int qlx_linear_int8(const void* w, const void* w_scale, const void* xq, const float* x_scale,
-                    void* y, int m, int n, int k, const qlx_plan* plan, void* stream);
+                    const void* xq2, const float* x_scale2, void* y, int m, int n, int k,
+                    const qlx_plan* plan, void* stream);
 
 /* ---- split-K plane consumers and epilogues ----------------------------------------- */
 

@@ -392,12 +392,13 @@ def residual_partials(x_bits, planes):
 def rms_norm(x_bits, w_bits, eps):
     """bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w) (reference.py:13-16).
 
-    The sum of squares is accumulated in fp64 here; implementations that sum in
-    another order agree to within one bf16 ulp (the reference's own bar,
-    gpu_checks.py:451-492)."""
+    The squares of bf16 values and their sum over a row are exact in fp64, so the mean is
+    taken exactly, rounded to fp32, then eps is added and 1/sqrt taken in fp32 as torch's
+    rsqrt(mean + eps) does. An fp32 sum in another order agrees to within one bf16 ulp (the
+    reference's own bar, gpu_checks.py:451-492); the device kernel sums in fp64 too."""
     x = bf16_to_f32(x_bits)
-    ms = (x.astype(np.float64) ** 2).mean(axis=-1, keepdims=True)
-    scale = (F32(1.0) / np.sqrt((ms + eps).astype(F32))).astype(F32)
+    ms = (x.astype(np.float64) ** 2).sum(axis=-1, keepdims=True) / x.shape[-1]
+    scale = (F32(1.0) / np.sqrt((ms.astype(F32) + F32(eps)).astype(F32))).astype(F32)
     y = round_bf16((x * scale).astype(F32))
     return f32_to_bf16((y * bf16_to_f32(w_bits)).astype(F32))
 
