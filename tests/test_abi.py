@@ -1,0 +1,113 @@
+"""CPU tests of the boundary: the C-ABI library loads, exports every declared symbol, and
+the host-side logic (planner, contract checks, no-CPU-fallback) behaves -- no GPU calls."""
+
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qlinear.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(qlx_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    from kernels import _lib
+    lib = _lib.lib()
+    names = declared()
+    assert len(names) >= 25
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures cover exactly the header"
+    assert lib.qlx_abi_version() == 1
+
+
+def test_library_is_gfx950_only_and_has_no_torch_dependency():
+    from kernels import _lib
+    import subprocess
+    out = subprocess.run(["readelf", "-d", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    assert "libtorch" not in out and "libc10" not in out
+    assert "libamdhip64" in out
+
+
+def test_planner_defaults_are_valid_and_fit():
+    from kernels import _lib, _linear
+    lib = _lib.lib()
+    for fmt in range(7):
+        for n, k in ((6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728), (151936, 2560)):
+            for m in (1, 8, 16, 32, 64):
+                p = _lib.Plan()
+                assert lib.qlx_plan_linear(fmt, 0, m, n, k, p) == 0, (fmt, n, k, m)
+                assert p.waves in (4, 8) and p.waves % p.kw == 0 and p.rw in (1, 2) and p.splits >= 1
+                again = _linear.make_plan(fmt, 0, m, n, k, (p.waves, p.kw, p.rw, p.splits))
+                assert again.splits == p.splits, "the default plan is already normalised"
+                assert lib.qlx_plan_tickets(p, fmt, m, n, k) >= 1
+
+
+def test_plan_fit_normalises_splits_like_the_reference():
+    """cuda_fp8._plan (engine/kernels/cuda_fp8.py:1255-1276): gps = ceil(groups/splitk),
+    splitk = ceil(groups/gps)."""
+    from kernels import _lib, _linear
+    for groups, splitk in ((20, 3), (20, 7), (76, 16), (32, 5), (10, 10), (10, 40)):
+        k = 128 * groups
+        plan = _linear.make_plan(_lib.FMT_REF8, _lib.MODE_PLANES, 1, 2560, k, (8, 8, 1, splitk))
+        s = max(1, min(splitk, groups))
+        gps = -(-groups // s)
+        assert plan.splits == -(-groups // gps), (groups, splitk, plan.splits)
+
+
+def test_contract_violations_fail_before_any_launch():
+    """Bad shapes and plans return QLX_EINVAL with a message (no GPU needed to reject them)."""
+    from kernels import _lib
+    import ctypes
+    lib = _lib.lib()
+    bad = _lib.Plan()
+    bad.mode, bad.waves, bad.kw, bad.rw, bad.splits = 0, 4, 3, 1, 1
+    rc = lib.qlx_linear_w4a16(None, None, None, None, 1, 256, 512, 0, ctypes.byref(bad), None)
+    assert rc == _lib.QLX_EINVAL and "kw" in _lib.last_error()
+    good = _lib.Plan()
+    assert lib.qlx_plan_linear(_lib.FMT_W4A16, 0, 1, 256, 512, good) == 0
+    assert lib.qlx_linear_w4a16(None, None, None, None, 1, 256, 500, 0, ctypes.byref(good), None) == _lib.QLX_EINVAL
+    assert lib.qlx_linear_w4a16(None, None, None, None, 65, 256, 512, 0, ctypes.byref(good), None) == _lib.QLX_EINVAL
+    assert lib.qlx_quantize_weight(None, None, None, 4, 100, 64, 8, 0, 1, 0, None) == _lib.QLX_EINVAL
+    assert lib.qlx_tile_rows(None, None, 17, 128, None) == _lib.QLX_EINVAL
+
+
+def test_python_ops_refuse_cpu_tensors():
+    """No CPU fallback: the product path raises instead of computing on the host."""
+    from kernels import cuda_fp8, fp8, qlinear
+    w = torch.randn(64, 256).to(torch.bfloat16)
+    for fn in (lambda: cuda_fp8.quantize(w), lambda: fp8.quantize(w), lambda: qlinear.quantize_w4(w),
+               lambda: qlinear.quantize_fp8(w), lambda: qlinear.quantize_w8(w)):
+        with pytest.raises(ValueError, match="GPU"):
+            fn()
+
+
+def test_package_mirrors_reference_names():
+    import kernels
+    from kernels import cuda_fp8, cuda_int8, fp8
+    for name in ("quantize", "dequantize", "prepare", "Prepared", "matmul", "matmul_partials", "splits",
+                 "gate_up_swiglu", "matmul_add_norm", "add_norm_scratch", "ready", "applicable",
+                 "CONFIGS", "SWIGLU_CONFIGS", "ADD_NORM_CONFIGS", "GROUP", "TILED", "_FUSED_ROWS", "_module_for"):
+        assert hasattr(cuda_fp8, name), name
+    for name in ("quantize", "fp8_matmul", "CONFIGS", "bytes_moved"):
+        assert hasattr(fp8, name), name
+    for name in ("quantize_activation", "Prepared", "matmul", "matmul_quantized", "add_norm_quant"):
+        assert hasattr(cuda_int8, name), name
+    for name in ("rms_norm", "add_rms_norm", "add_rms_norm_partials", "swiglu", "swiglu_partials"):
+        assert hasattr(kernels, name), name
+    assert callable(kernels.swiglu)
+
+
+def test_oracle_is_not_imported_by_the_product():
+    pkg = os.path.join(ROOT, "dryft-flash-infer_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f
