@@ -35,6 +35,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(fmt, m):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated; see its header for the commands), or None."""
+    path = os.path.join(ROOT, "profiles", f"{fmt}_gate_up_swiglu_m{m}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 class Stack:
     """Quantized weights of every projection of the model, plus resident activations."""
 
@@ -244,16 +258,16 @@ def main():
         dom = {"us": t * 1e3, "alg_MB": b / 1e6, "GBps": b / (t * 1e-3) / 1e9}
     roofline = {
         "bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-        "frac": round(dom["GBps"] * 1e9 / PEAK_HBM, 4), "traffic": None,
+        "frac": round(dom["GBps"] * 1e9 / PEAK_HBM, 4), "traffic": profiled_traffic(args.workload, args.m),
         "kernel": f"gemm_kernel<{ {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload] }, ..., SwiGLU> "
                   f"(gate_up 2560->2x9728, M={args.m})",
         "us_per_launch": round(dom["us"], 2), "alg_MB_per_launch": round(dom["alg_MB"], 3),
     }
 
     extra = {}
-    if not args.quick:
-        extra["stream_floor_GBps"] = round(stream_floor(), 1)
-        extra["stack_frac_of_stream_floor"] = round(head["alg_GBps"] / extra["stream_floor_GBps"], 4)
+    # the stream read also calibrates rocprofv3's FETCH_SIZE (a known byte count)
+    extra["stream_floor_GBps"] = round(stream_floor(1 << 30 if args.quick else 4 << 30), 1)
+    extra["stack_frac_of_stream_floor"] = round(head["alg_GBps"] / extra["stream_floor_GBps"], 4)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(stack)
