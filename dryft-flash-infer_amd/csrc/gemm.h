@@ -89,6 +89,31 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Publish this workgroup's device-coherent stores before one thread signals another
+// workgroup (ticket or arrival counter). Each wave waits until its own stores are
+// acknowledged (s_waitcnt 0), then the barrier orders every wave before the signal. A
+// workgroup-scope release alone does not wait for outstanding stores on gfx950 (the
+// barrier does not either), and an agent-scope release would also write back the whole L2.
+__device__ __forceinline__ void publish_stores() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+}
+
+// 16 bytes of activation; device-coherent when another workgroup of the same launch wrote
+// them (the decode executor), a plain 128-bit load otherwise.
+template <bool COH>
+__device__ __forceinline__ uint4 load_x16(const void* p) {
+  if (COH) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return uint4{__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+  }
+  return *reinterpret_cast<const uint4*>(p);
+}
+
 // Two exact small-integer floats -> bf16 pair (the high halves are exact: <= 8 significant bits).
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
@@ -134,9 +159,9 @@ struct FmtW4 {
     return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 7) + 2 * step + j]);
   }
   // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword).
+  template <bool COH>
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) +
-                                                    (size_t)mm * a.k + kabs);
+    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
     uint4 o;
     o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
     o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
@@ -209,8 +234,9 @@ struct FmtW8 {
   __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
     return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
   }
+  template <bool COH>
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
+    return load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
   }
   __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
     const uint4 av = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
@@ -347,7 +373,9 @@ struct FmtRef {
     }
     return t4;
   }
+  template <bool COH>
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
+    static_assert(!COH, "coherent staging is implemented for the north-star formats");
     const uint16_t* row = reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k;
     const int blk = kabs & ~63, p0 = kabs & 63;
     uint32_t v[8];
@@ -417,8 +445,9 @@ struct FmtFP8WO {
     return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k / a.group) +
                                                         (step * 128 + j * 64) / a.group]);
   }
+  template <bool COH>
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
+    return load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
   }
   template <bool HI>
   __device__ static uint32_t fp8pair(uint32_t d) {
@@ -510,14 +539,15 @@ struct FmtInt8 {
 // Prologue: stage the workgroup's activation slice (B order), its scales, bias sums.
 // ====================================================================================
 
-template <class F>
+template <class F, bool COH>
 __device__ void stage_bf16(const GemmArgs& a, char* lds, int step0, int nst) {
   constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
   const int cpr = nst * CPS;
   const int total = a.m * cpr;
   for (int q = threadIdx.x; q < total; q += blockDim.x) {
     const int mm = q / cpr, kc = q - mm * cpr;
-    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = F::stage_chunk(a, mm, step0 * F::KSTEP + kc * 8);
+    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) =
+        F::template stage_chunk<COH>(a, mm, step0 * F::KSTEP + kc * 8);
   }
 }
 
@@ -539,6 +569,7 @@ __device__ void stage_bias(const GemmArgs& a, char* lds, int nst) {
 }
 
 // FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice.
+template <bool COH>
 __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) {
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
   uint32_t* amax = reinterpret_cast<uint32_t*>(sx + a.m);
@@ -555,7 +586,7 @@ __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) 
       cur = mm;
       mx = 0.f;
     }
-    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)q * 8);
+    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)q * 8);
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
@@ -567,8 +598,7 @@ __device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) 
   const int cps = nst * 16;  // 8-value chunks per row of the slice
   for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
     const int mm = q / cps, kc = q - mm * cps;
-    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k +
-                                                    step0 * 128 + kc * 8);
+    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + step0 * 128 + kc * 8);
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
     const float s = sx[mm];
     uint32_t c[8];
@@ -625,12 +655,11 @@ __device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, in
 }
 
 // ====================================================================================
-// The kernel.
+// One work item (a row block's K slice): prefetch, then stage + stream + epilogue.
 // ====================================================================================
 
-__device__ __forceinline__ void block_coords(const GemmArgs& a, int& tg, int& s) {
+__device__ __forceinline__ void block_coords(const GemmArgs& a, int b, int& tg, int& s) {
   const int total = a.tile_groups * a.splits;
-  const int b = blockIdx.x;
   int logical = b;
   if (total >= 8) {  // consecutive logical blocks (the splits of a row block) share an XCD
     const int per = total >> 3, rem = total & 7, xcd = b & 7, idx = b >> 3;
@@ -650,40 +679,77 @@ __device__ __forceinline__ void load_chunk(uint4 (&c)[F::LOADS], const GemmArgs&
   }
 }
 
-// SW: the SwiGLU epilogue (a separate instantiation, so profiles tell it apart).
-template <class F, int MT, int RW, int WAVES, bool SW>
-__global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
-  extern __shared__ __align__(16) char lds[];
-  constexpr int PF = RW == 1 ? 4 : 2;  // steps in flight per wave (each 2 KB for RW = 1)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int tg, s;
-  block_coords(a, tg, s);
-  const int step0 = s * a.sps;
-  const int nst = min(a.nsteps, step0 + a.sps) - step0;
+template <int RW>
+struct PipeDepth {
+  static constexpr int PF = RW == 1 ? 4 : 2;  // steps in flight per wave (each 2 KB for RW = 1)
+};
 
-  // ---- first weight loads: they depend on nothing, so they are in flight while the
-  // prologue stages the activation
-  const int wt = wave / a.kw, kwi = wave - wt * a.kw;   // tile slot, k-interleave index
-  const int tile0 = tg * a.rt + wt * RW;
-  const bool active = tile0 < a.ntiles;
+// Per-wave state of one work item, fixed by item_prefetch.
+template <int RW>
+struct Item {
+  int tg, s, step0, nst, wt, kwi, tile0, my, last;
   int wrow[RW];  // a tile past the end streams its neighbour's rows; its output is dropped
+};
+
+// Issue the wave's first PF steps of weight loads for work item (tg, s). They depend on
+// nothing else, so they are in flight while the activation is staged (or, in the decode
+// executor, while the previous projection finishes).
+template <class F, int RW>
+__device__ __forceinline__ void item_prefetch(const GemmArgs& a, int tg, int s, Item<RW>& it,
+                                              uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+  constexpr int PF = PipeDepth<RW>::PF;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  it.tg = tg;
+  it.s = s;
+  it.step0 = s * a.sps;
+  it.nst = min(a.nsteps, it.step0 + a.sps) - it.step0;
+  it.wt = wave / a.kw;
+  it.kwi = wave - it.wt * a.kw;
+  it.tile0 = tg * a.rt + it.wt * RW;
+  const bool active = it.tile0 < a.ntiles;
 #pragma unroll
-  for (int r = 0; r < RW; ++r) wrow[r] = active ? weight_row(a, tile0 + r < a.ntiles ? tile0 + r : tile0, lane & 15) : 0;
-  const int my = active ? (nst - kwi + a.kw - 1) / a.kw : 0;  // this wave's steps: kwi, kwi + kw, ...
-  uint4 buf[PF][RW][F::LOADS];
+  for (int r = 0; r < RW; ++r)
+    it.wrow[r] = active ? weight_row(a, it.tile0 + r < a.ntiles ? it.tile0 + r : it.tile0, lane & 15) : 0;
+  it.my = active ? (it.nst - it.kwi + a.kw - 1) / a.kw : 0;  // this wave's steps: kwi, kwi + kw, ...
+  it.last = it.step0 + it.kwi + (it.my - 1) * a.kw;
 #pragma unroll
   for (int p = 0; p < PF; ++p)
-    if (p < my)
+    if (p < it.my)
 #pragma unroll
-      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], step0 + kwi + p * a.kw, lane);
+      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, it.wrow[r], it.step0 + it.kwi + p * a.kw, lane);
+}
+
+// bf16 pair (rows idx, idx + 1) to y; device-coherent when another workgroup of the same
+// launch reads it (the decode executor).
+template <bool COH>
+__device__ __forceinline__ void store_pair(uint16_t* y, size_t idx, float v0, float v1) {
+  const uint32_t w = (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
+  if (COH)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(y + idx), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *reinterpret_cast<uint32_t*>(y + idx) = w;
+}
+
+// Stage the activation, stream the item's weight steps through the MFMAs, combine the kw
+// waves of each tile, write the output (bf16, SwiGLU or fp32 planes), and for split-K let
+// the last workgroup of the row block reduce the planes in slice order.
+// COH: activation reads and output writes are device-coherent (other workgroups of the
+// same launch produce the input / consume the output).
+template <class F, int MT, int RW, int WAVES, bool SW, bool COH>
+__device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
+                         uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+  constexpr int PF = PipeDepth<RW>::PF;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tg = it.tg, s = it.s, step0 = it.step0, nst = it.nst, wt = it.wt, kwi = it.kwi, my = it.my;
 
   // ---- prologue
   if constexpr (std::is_same<F, FmtFP8>::value) {
-    stage_fp8_act(a, lds, step0, nst);
+    stage_fp8_act<COH>(a, lds, step0, nst);
   } else if constexpr (std::is_same<F, FmtInt8>::value) {
+    static_assert(!COH, "coherent staging is implemented for the north-star formats");
     stage_int8_act(a, lds, step0, nst);
   } else {
-    stage_bf16<F>(a, lds, step0, nst);
+    stage_bf16<F, COH>(a, lds, step0, nst);
   }
   stage_scales<F>(a, lds, tg, step0, nst);
   __syncthreads();
@@ -707,7 +773,6 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   // Steady state: PF steps per trip, every load unconditional. Prefetch addresses past the
   // wave's last step are clamped to it (a cache hit), so the body has no branches and the
   // compiler keeps PF steps of loads in flight instead of draining at every join.
-  const int last = step0 + kwi + (my - 1) * a.kw;
   int j0 = 0;
   for (; j0 + PF <= my; j0 += PF) {
 #pragma unroll
@@ -718,9 +783,9 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
         F::template compute<MT>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
       // Refill the slot just consumed (same registers: no copies across the loop edge),
       // and keep the refill here rather than letting the scheduler sink it to the end.
-      const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, last);
+      const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, it.last);
 #pragma unroll
-      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, wrow[r], nxt, lane);
+      for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, it.wrow[r], nxt, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -754,49 +819,63 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
     for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
     return F::finish(a, lds, v, tl * 16 + nl, mm);
   };
+  auto swiglu = [](float g, float u) -> float {
+    const float gb = round_bf(g), ub = round_bf(u);
+    return round_bf(gb / (1.f + expf(-gb))) * ub;
+  };
 
-  const int rows_out = SW ? 8 : 16;
-  const int per_tile = rows_out * a.m;
+  // Outputs go out in row pairs (one 32-bit store of two bf16).
+  constexpr int rows_out = SW ? 8 : 16;
+  const int per_tile = (rows_out / 2) * a.m;
   const int total = a.rt * per_tile;
   const bool direct = a.splits == 1 || a.mode == QLX_MODE_PLANES;
   uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
   for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
     const int tl = idx / per_tile, rem = idx - tl * per_tile;
-    const int mm = rem / rows_out, nl = rem - mm * rows_out;
+    const int mm = rem / (rows_out / 2), nl = 2 * (rem - mm * (rows_out / 2));
     const int tile = tg * a.rt + tl;
     if (tile >= a.ntiles) continue;
     if (SW) {
-      const float g = combined(tl, nl, mm), u = combined(tl, nl + 8, mm);
+      const float g0 = combined(tl, nl, mm), u0 = combined(tl, nl + 8, mm);
+      const float g1 = combined(tl, nl + 1, mm), u1 = combined(tl, nl + 9, mm);
       if (direct) {
-        const float gb = round_bf(g), ub = round_bf(u);
-        y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
+        store_pair<COH>(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
       } else {
-        float* pl = a.work + ((size_t)s * a.m + mm) * a.n;
-        store_coherent(pl + 8 * tile + nl, g);
-        store_coherent(pl + a.half + 8 * tile + nl, u);
+        float* pl = a.work + ((size_t)s * a.m + mm) * a.n + 8 * tile + nl;
+        store_coherent(pl, g0);
+        store_coherent(pl + 1, g1);
+        store_coherent(pl + a.half, u0);
+        store_coherent(pl + a.half + 1, u1);
       }
     } else {
       const int row = 16 * tile + nl;
       if (row >= a.n) continue;
-      const float v = combined(tl, nl, mm);
-      if (a.mode == QLX_MODE_PLANES)
-        a.work[((size_t)s * a.m + mm) * a.n + row] = v;
-      else if (!direct)
-        store_coherent(a.work + ((size_t)s * a.m + mm) * a.n + row, v);
-      else
-        y[(size_t)mm * a.n + row] = f2bf(v);
+      const bool two = row + 1 < a.n;
+      const float v0 = combined(tl, nl, mm), v1 = two ? combined(tl, nl + 1, mm) : 0.f;
+      float* pl = a.work + ((size_t)s * a.m + mm) * a.n + row;
+      if (a.mode == QLX_MODE_PLANES) {
+        pl[0] = v0;
+        if (two) pl[1] = v1;
+      } else if (!direct) {
+        store_coherent(pl, v0);
+        if (two) store_coherent(pl + 1, v1);
+      } else if (two && (a.n & 1) == 0) {
+        store_pair<COH>(y, (size_t)mm * a.n + row, v0, v1);
+      } else {
+        y[(size_t)mm * a.n + row] = f2bf(v0);
+        if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
+      }
     }
   }
   if (direct) return;
 
   // ---- split-K: the last workgroup of this row block reduces the planes in slice order.
-  // The partials went out with device-coherent stores; a workgroup release waits for them
-  // to complete before the ticket is taken, and the last workgroup reads them with
+  // The partials went out with device-coherent stores; every wave waits for its stores to
+  // complete before the ticket is taken, and the last workgroup reads them with
   // device-coherent loads. No L2 write-back/invalidate of the whole cache is needed (an
   // agent-scope fence would emit one per workgroup).
   __shared__ int s_last;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __syncthreads();
+  publish_stores();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&a.tickets[tg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == a.splits - 1;
@@ -808,27 +887,50 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   const size_t plane = (size_t)a.m * a.n;
   for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
     const int tl = idx / per_tile, rem = idx - tl * per_tile;
-    const int mm = rem / rows_out, nl = rem - mm * rows_out;
+    const int mm = rem / (rows_out / 2), nl = 2 * (rem - mm * (rows_out / 2));
     const int tile = tg * a.rt + tl;
     if (tile >= a.ntiles) continue;
     if (SW) {
       const float* pg = a.work + (size_t)mm * a.n + 8 * tile + nl;
-      float g = 0.f, u = 0.f;
+      float g0 = 0.f, u0 = 0.f, g1 = 0.f, u1 = 0.f;
       for (int sp = 0; sp < a.splits; ++sp) {
-        g += load_coherent(pg + sp * plane);
-        u += load_coherent(pg + sp * plane + a.half);
+        g0 += load_coherent(pg + sp * plane);
+        g1 += load_coherent(pg + sp * plane + 1);
+        u0 += load_coherent(pg + sp * plane + a.half);
+        u1 += load_coherent(pg + sp * plane + a.half + 1);
       }
-      const float gb = round_bf(g), ub = round_bf(u);
-      y[(size_t)mm * a.half + 8 * tile + nl] = f2bf(round_bf(gb / (1.f + expf(-gb))) * ub);
+      store_pair<COH>(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
     } else {
       const int row = 16 * tile + nl;
       if (row >= a.n) continue;
+      const bool two = row + 1 < a.n;
       const float* p = a.work + (size_t)mm * a.n + row;
-      float v = 0.f;
-      for (int sp = 0; sp < a.splits; ++sp) v += load_coherent(p + sp * plane);
-      y[(size_t)mm * a.n + row] = f2bf(v);
+      float v0 = 0.f, v1 = 0.f;
+      for (int sp = 0; sp < a.splits; ++sp) {
+        v0 += load_coherent(p + sp * plane);
+        if (two) v1 += load_coherent(p + sp * plane + 1);
+      }
+      if (two && (a.n & 1) == 0) {
+        store_pair<COH>(y, (size_t)mm * a.n + row, v0, v1);
+      } else {
+        y[(size_t)mm * a.n + row] = f2bf(v0);
+        if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
+      }
     }
   }
+}
+
+// One launch = one linear call. SW: the SwiGLU epilogue (a separate instantiation, so
+// profiles tell it apart).
+template <class F, int MT, int RW, int WAVES, bool SW>
+__global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  int tg, s;
+  block_coords(a, blockIdx.x, tg, s);
+  Item<RW> it;
+  uint4 buf[PipeDepth<RW>::PF][RW][F::LOADS];
+  item_prefetch<F, RW>(a, tg, s, it, buf);
+  item_run<F, MT, RW, WAVES, SW, false>(a, lds, it, buf);
 }
 
 }  // namespace qlx

@@ -31,8 +31,18 @@ class Plan(ctypes.Structure):
     ]
 
 
+class StackCall(ctypes.Structure):
+    """``qlx_stack_call``: one projection of a decode-step chain."""
+
+    _fields_ = [
+        ("w", ctypes.c_void_p), ("w_scale", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("n", ctypes.c_int), ("k", ctypes.c_int), ("mode", ctypes.c_int), ("pad", ctypes.c_int),
+    ]
+
+
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
 _PLAN = ctypes.POINTER(Plan)
+_PI, _PLL = ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_longlong)
 
 #: Every exported entry point and its argument types (the header's declarations).
 SIGNATURES = {
@@ -61,6 +71,9 @@ SIGNATURES = {
     "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
+    "qlx_stack_desc_size": ([], _I),
+    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _P, _PLAN, _P, _P, _PLL, _PI, _PI, _PI], _I),
+    "qlx_stack_run": ([_I, _P, _I, _I, _I, _P, _I, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 

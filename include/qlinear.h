@@ -197,6 +197,42 @@ int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* plane
 int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, int rows, int inter,
                void* stream);
 
+/* ---- decode-step executor ----------------------------------------------------------- */
+
+/* One projection of a decode step: y = x @ deq(w)^T on tiled weights (qlx_tile_rows layout),
+ * mode QLX_MODE_BF16 or QLX_MODE_SWIGLU. x may be the y of an earlier projection. */
+typedef struct qlx_stack_call {
+  const void* w;
+  const void* w_scale;
+  const void* x;
+  void* y;
+  int n, k, mode, pad;
+} qlx_stack_call;
+
+/* Bytes of one device descriptor written by qlx_stack_build. */
+int qlx_stack_desc_size(void);
+
+/* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
+ * for the executor, with `groups_per_cu` resident workgroups per CU (1..4). Writes the
+ * descriptors to host memory `desc` (ncalls * qlx_stack_desc_size() bytes; NULL to only size)
+ * and, if `plans` is not NULL, each projection's plan (a qlx_linear_* call with that plan gives
+ * the same bits), and reports the split-K workspace (fp32 floats) and ticket counters (int32, zeroed once) the
+ * descriptors must point at, the grid and the dynamic LDS per workgroup. The descriptors hold
+ * `workspace` and `tickets` as given: call once with NULLs to size them, then again.
+ * Replaces the reference's per-projection launches chained by programmatic dependent launch
+ * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
+ * engine/kernels/cuda_jit.py:218-262): here the whole chain is one cooperative launch. */
+int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int groups_per_cu, void* desc,
+                    qlx_plan* plans, float* workspace, int* tickets, long long* workspace_floats,
+                    int* tickets_needed, int* grid, int* lds_bytes);
+
+/* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors, `sync` three
+ * int32 in device memory (zero before the first run; each run leaves [0] and [1] zero and sets
+ * [2] to 1 if any wait gave up after `spin_limit` sleeps, which makes that run's outputs
+ * undefined). Runs that share `sync`, the workspace or the tickets must not overlap. */
+int qlx_stack_run(int fmt, const void* desc, int ncalls, int grid, int lds_bytes, int* sync, int spin_limit,
+                  void* stream);
+
 /* ---- measurement ------------------------------------------------------------------- */
 
 /* Read `bytes` (multiple of 16) from p with 16-byte loads over `blocks` workgroups of 256

@@ -111,3 +111,25 @@ def test_oracle_is_not_imported_by_the_product():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
+
+
+def test_decode_stack_contract_on_host():
+    """The executor rejects unsupported formats, batch sizes and empty chains before any
+    device work."""
+    from kernels import _lib
+    from kernels.decode_stack import DecodeStack
+    import ctypes
+    lib = _lib.lib()
+    assert lib.qlx_stack_desc_size() >= 128
+    call = (_lib.StackCall * 1)()
+    out = [ctypes.c_longlong(0), ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)]
+    for fmt, m, n, gpc in ((_lib.FMT_REF8, 1, 1, 1), (_lib.FMT_W4A16, 17, 1, 1), (_lib.FMT_W4A16, 1, 0, 1),
+                           (_lib.FMT_FP8, 1, 1, 5)):
+        rc = lib.qlx_stack_build(fmt, m, call, n, gpc, None, None, None, None, *out)
+        assert rc == _lib.QLX_EINVAL, (fmt, m, n, gpc)
+    for fmt, m in (("int8", 1), ("w4a16", 0), ("fp8", 17)):
+        with pytest.raises(ValueError):
+            DecodeStack(fmt, m)
+    with pytest.raises(ValueError):
+        DecodeStack("w8a16", 1).build()
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, 1, 0, None, 1, None) == _lib.QLX_EINVAL
