@@ -19,6 +19,15 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 
 // ---- bf16 / fp16 -------------------------------------------------------------------
 
+// Global-memory view of a generic pointer to device memory. Accesses through it compile to
+// global_* instead of flat_* instructions; flat accesses also count against the LDS/scalar
+// counter, so a wait for an LDS result would wait for every flat load in flight (pointers
+// read from memory, unlike kernel arguments, are not known to be global).
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
 // fp32 -> bf16 bits, RNE by integer add (cuda_fp8.py:64-68); NaN -> sign | 0x7FC0.

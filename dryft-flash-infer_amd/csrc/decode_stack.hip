@@ -3,123 +3,302 @@
 // The reference runs each projection as its own CUDA launch inside a graph and hides the
 // launch gap with programmatic dependent launch: a GEMM's weight loads start while the
 // previous kernel drains (engine/kernels/cuda_fp8.py:47-50, 150-169, 252;
-// engine/kernels/cuda_jit.py:218-262). HIP has
-// no such launch attribute, and at M = 1 most projections are 10-25 MB, so a separate launch
-// (about 1.6 us) plus first-load latency, activation staging and the epilogue cost as much as
-// the weight stream itself.
+// engine/kernels/cuda_jit.py:218-262). HIP has no such launch attribute, and at M = 1 most
+// projections are 5-25 MB, so per-launch latency (launch, first loads, activation staging,
+// epilogue) costs as much as the weight stream itself.
 //
-// Here one cooperative launch walks the projections in order. Projection c may read what
-// projections < c wrote, so a workgroup starts projection c only after every workgroup has
-// finished c - 1 (a stage counter of arrivals), but it issues c's first weight loads before
-// it waits: weights do not depend on activations. Activations are read and outputs written
-// device-coherently, since other workgroups of the same launch produce and consume them.
-//
-// Every wait is bounded: cooperative launch guarantees all workgroups are resident, and a
-// spin that still exceeds its limit records an error flag and leaves the wait, so the
-// kernel always ends.
+// Here one cooperative launch runs the whole chain on `lanes` sets of workgroups, one
+// workgroup per CU in each; lane l runs projections l, l + lanes, ... so a CU works on
+// several projections at once and their memory latencies overlap.
+//   * Work: a projection's weight is cut into row blocks of rt tiles, each ns K steps long.
+//     Each workgroup gets one contiguous, equal share of the projection's block-steps (or
+//     of its whole row blocks, when cutting K is not worth it). Each row block a share
+//     touches is one work item. A row block cut into several pieces is summed, in piece
+//     order, by the workgroup holding piece 0 (its last item of the projection), so results
+//     do not depend on timing.
+//   * Overlap: a workgroup issues the first weight loads of its next item -- in this
+//     projection or a later one -- before it finishes the current item. Weights never
+//     depend on activations, so they stream while inputs are still being produced.
+//   * Dependencies without barriers: values another workgroup needs (a chained projection's
+//     output, a row block's partial sums) are published as 64-bit words {32-bit value, run
+//     epoch} with one device-coherent store each, and the reader polls exactly the words it
+//     needs until their epoch is the current run's. A dependency costs one store-to-load
+//     trip instead of a store, its acknowledgement, a counter update and a counter poll.
+//     Every run has a new nonzero epoch, so words left by earlier runs never match.
+//   * Every wait is bounded by a per-run deadline on the 100 MHz real-time counter: a wait
+//     past it sets the error flag and moves on (that run's outputs are undefined), so the
+//     kernel always ends. Cooperative launch guarantees that every workgroup is resident.
 #include <vector>
 
 #include "gemm_launch.h"
 
 namespace qlx {
 
-// One projection of the stack, as the executor reads it from device memory.
-struct StackDesc {
-  GemmArgs a;
-  int items;  // work items: tile_groups * splits
-  int sw;     // SwiGLU epilogue
-  int pad[2];
+constexpr int kMaxPieces = 4;  // pieces of one row block (the reducer has all in flight)
+
+// One projection of the chain, as the executor reads it (from LDS when the chain's
+// descriptors fit next to the items' LDS: read once per launch instead of missing the
+// caches, which the weight stream keeps flushing, on every item).
+struct alignas(16) StackDesc {
+  GemmArgs a;      // a.sps: most steps of one item (LDS layout); a.splits: most pieces of a row block
+  uint64_t* xwire;  // the activation as published by an earlier projection, or null (read a.x)
+  uint64_t* ywire;  // publish the output here ([m][n_out/2] words), or null
+  uint64_t* part;   // partial sums of pieces 1.. ([np-1][m][n] words), or null
+  int units;        // work units: block-steps (gran 1) or row blocks (gran ns)
+  int pe;           // workgroups with work: min(P, units)
+  int gran;         // block-steps per unit
+  int sw;           // SwiGLU epilogue
 };
 
-// sync[0]: arrivals (P per projection), sync[1]: exits, sync[2]: error flag. Zero at launch;
-// the last workgroup to exit zeroes [0] and [1] again.
-__device__ __forceinline__ void stage_arrive(int* sync) {
-  publish_stores();  // this workgroup's outputs are device-visible before it is counted
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(&sync[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// ---- shares of a projection ---------------------------------------------------------
+
+// Workgroup p holds units [p*U/pe, (p+1)*U/pe); owner(u) is the workgroup holding unit u.
+// 32-bit arithmetic (64-bit division is a long software sequence on the GPU): the planner
+// keeps (U + 1) * (pe + 1) and U * gran below 2^31.
+__host__ __device__ inline unsigned share_begin(unsigned p, unsigned U, unsigned pe) { return p * U / pe; }
+__host__ __device__ inline unsigned share_owner(unsigned u, unsigned U, unsigned pe) {
+  const unsigned o = ((u + 1) * pe + U - 1) / U - 1;
+  return o < pe - 1 ? o : pe - 1;
 }
 
-__device__ __forceinline__ void stage_wait(int* sync, int target, int spin_limit) {
-  if (threadIdx.x == 0) {
-    int spins = 0;
-    while (__hip_atomic_load(&sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > spin_limit) {
-        __hip_atomic_store(&sync[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
+// Item of workgroup p in row block g: steps [*step0, *step0 + *nst), piece *piece of *np.
+__host__ __device__ inline void share_item(int p, int g, int U, int pe, int gran, int ns, int* step0, int* nst,
+                                           int* piece, int* np) {
+  const unsigned b0 = share_begin(p, U, pe) * gran, b1 = share_begin(p + 1, U, pe) * gran;
+  const unsigned gs = (unsigned)g * ns;
+  const unsigned s0 = b0 > gs ? b0 : gs;
+  const unsigned s1 = b1 < gs + ns ? b1 : gs + ns;
+  *step0 = (int)(s0 - gs);
+  *nst = (int)(s1 - s0);
+  unsigned first, last;
+  if (gran == ns) {  // whole row blocks: unit g
+    first = last = share_owner(g, U, pe);
+  } else {           // gran 1: units are block-steps
+    first = share_owner(gs, U, pe);
+    last = share_owner(gs + ns - 1, U, pe);
   }
-  __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  *np = (int)(last - first + 1);
+  *piece = p - (int)first;
 }
 
-template <class F, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
-stack_kernel(const StackDesc* __restrict__ calls, int ncalls, int* sync, int spin_limit) {
-  extern __shared__ __align__(16) char lds[];
-  constexpr int PF = PipeDepth<1>::PF;
-  const int P = gridDim.x, p = blockIdx.x;
-  Item<1> it;
-  uint4 buf[PF][1][F::LOADS];
-  auto coords = [&](const GemmArgs& a, int item, int& tg, int& s) {
-    tg = item / a.splits;
-    s = item - tg * a.splits;
+// ---- published words -------------------------------------------------------------------
+
+struct Waits {
+  uint32_t epoch;
+  unsigned long long deadline;  // real-time counter value
+  int* err;
+};
+
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
+  return __hip_atomic_load(gmem(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_store(uint64_t* p, uint32_t v, uint32_t epoch) {
+  __hip_atomic_store(gmem(p), ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value of a word first read as v: re-read until it carries this run's epoch (bounded).
+__device__ __forceinline__ uint32_t ll_settle(const uint64_t* p, uint64_t v, const Waits& w) {
+  while ((uint32_t)(v >> 32) != w.epoch) {
+    if (__builtin_amdgcn_s_memrealtime() > w.deadline) {
+      __hip_atomic_store(gmem(w.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    v = ll_load(p);
+  }
+  return (uint32_t)v;
+}
+
+// Activation published by an earlier projection: [m][k/2] words of bf16 pairs.
+struct XWire {
+  const uint64_t* wire;
+  Waits w;
+  struct Raw {
+    uint64_t v[4];
   };
-  // The first item of projection 0 needs no wait.
-  bool prefetched = false;
-  if (p < calls[0].items) {
-    int tg, s;
-    coords(calls[0].a, p, tg, s);
-    item_prefetch<F, 1>(calls[0].a, tg, s, it, buf);
-    prefetched = true;
+  __device__ __forceinline__ void fetch(const GemmArgs& a, int mm, int kabs, Raw& r) const {
+    const uint64_t* p = wire + (size_t)mm * (a.k >> 1) + (kabs >> 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.v[i] = ll_load(p + i);
   }
-  for (int c = 0; c < ncalls; ++c) {
-    const StackDesc& d = calls[c];
-    if (c > 0) stage_wait(sync, P * c, spin_limit);
-    for (int item = p; item < d.items; item += P) {
-      if (!prefetched) {
-        int tg, s;
-        coords(d.a, item, tg, s);
-        item_prefetch<F, 1>(d.a, tg, s, it, buf);
+  __device__ __forceinline__ uint4 settle(const GemmArgs& a, int mm, int kabs, const Raw& r) const {
+    const uint64_t* p = wire + (size_t)mm * (a.k >> 1) + (kabs >> 1);
+    return uint4{ll_settle(p, r.v[0], w), ll_settle(p + 1, r.v[1], w), ll_settle(p + 2, r.v[2], w),
+                 ll_settle(p + 3, r.v[3], w)};
+  }
+};
+
+// ---- epilogue ----------------------------------------------------------------------------
+
+// Combine the item's waves; then, per output pair: write it (np == 1), publish this piece's
+// partial sums (piece > 0), or add the other pieces' partials in piece order and write
+// (piece 0). Outputs go to y and, when a later projection reads them, to ywire.
+template <class F, bool SW>
+__device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const Item<1>& it,
+                                            const f32x4 (&acc)[1][1], const Waits& w) {
+  const GemmArgs& a = d.a;
+  acc_to_lds<1, 1>(lds, acc);
+  constexpr int NV = SW ? 4 : 2;  // values per output pair: (g0, g1, u0, u1) or (v0, v1)
+  constexpr int rows_out = SW ? 8 : 16;
+  const int per_tile = (rows_out / 2) * a.m;
+  const int total = a.rt * per_tile;
+  const int nout = SW ? a.half : a.n;
+  const int piece = it.s, np = it.np;
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int tl = idx / per_tile, rem = idx - tl * per_tile;
+    const int mm = rem / (rows_out / 2), nl = 2 * (rem - mm * (rows_out / 2));
+    const int tile = it.tg * a.rt + tl;
+    if (tile >= a.ntiles) continue;
+    int row[NV];  // weight rows of the values
+    float v[NV];
+    if constexpr (SW) {
+      row[0] = 8 * tile + nl;
+      row[1] = row[0] + 1;
+      row[2] = a.half + row[0];
+      row[3] = row[2] + 1;
+      v[0] = tile_value<F, 1, 1>(a, lds, tl, nl, mm);
+      v[1] = tile_value<F, 1, 1>(a, lds, tl, nl + 1, mm);
+      v[2] = tile_value<F, 1, 1>(a, lds, tl, nl + 8, mm);
+      v[3] = tile_value<F, 1, 1>(a, lds, tl, nl + 9, mm);
+    } else {
+      row[0] = 16 * tile + nl;
+      row[1] = row[0] + 1;
+      v[0] = tile_value<F, 1, 1>(a, lds, tl, nl, mm);
+      v[1] = tile_value<F, 1, 1>(a, lds, tl, nl + 1, mm);
+    }
+    if (np > 1) {
+      if (piece > 0) {
+        uint64_t* part = d.part + ((size_t)(piece - 1) * a.m + mm) * a.n;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) ll_store(part + row[i], __float_as_uint(v[i]), w.epoch);
+        continue;
       }
-      prefetched = false;
-      if (d.sw)
-        item_run<F, 1, 1, WAVES, true, true>(d.a, lds, it, buf);
-      else
-        item_run<F, 1, 1, WAVES, false, true>(d.a, lds, it, buf);
-      __syncthreads();  // LDS is reused by the next item
+      uint64_t raw[kMaxPieces - 1][NV];
+#pragma unroll
+      for (int q = 1; q < kMaxPieces; ++q)
+        if (q < np) {
+          const uint64_t* part = d.part + ((size_t)(q - 1) * a.m + mm) * a.n;
+#pragma unroll
+          for (int i = 0; i < NV; ++i) raw[q - 1][i] = ll_load(part + row[i]);
+        }
+#pragma unroll
+      for (int q = 1; q < kMaxPieces; ++q)
+        if (q < np) {
+          const uint64_t* part = d.part + ((size_t)(q - 1) * a.m + mm) * a.n;
+#pragma unroll
+          for (int i = 0; i < NV; ++i) v[i] += __uint_as_float(ll_settle(part + row[i], raw[q - 1][i], w));
+        }
     }
-    stage_arrive(sync);
-    // Projection c + 1's weights start streaming before its wait.
-    if (c + 1 < ncalls && p < calls[c + 1].items) {
-      int tg, s;
-      coords(calls[c + 1].a, p, tg, s);
-      item_prefetch<F, 1>(calls[c + 1].a, tg, s, it, buf);
-      prefetched = true;
+    float o0 = v[0], o1 = v[1];
+    if constexpr (SW) {
+      o0 = swiglu_bf(v[0], v[2]);
+      o1 = swiglu_bf(v[1], v[3]);
     }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&sync[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == P - 1) {  // everyone has left every wait: reset for the next launch
-      __hip_atomic_store(&sync[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&sync[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    const int oi = row[0];  // first output of the pair (even; for SwiGLU the gate row index)
+    const uint32_t pair = bf16_pair(o0, o1);
+    *gmem(reinterpret_cast<uint32_t*>(y + (size_t)mm * nout + oi)) = pair;
+    if (d.ywire) ll_store(d.ywire + (size_t)mm * (nout >> 1) + (oi >> 1), pair, w.epoch);
   }
 }
 
-constexpr int kStackWaves = 8;
+// ---- the chain ---------------------------------------------------------------------------
+
+// The work item after (c, g) for workgroup p of its lane: (c, g + 1) inside its share, else
+// the first row block of the lane's next projection in which p has work. False when there is
+// none. Lane l runs projections l, l + lanes, l + 2 lanes, ...
+__device__ __forceinline__ bool next_work(const StackDesc* calls, int ncalls, int lanes, int lane, int p, int& c,
+                                          int& g) {
+  if (c >= 0) {
+    const StackDesc& d = calls[c];
+    if ((unsigned)(g + 1) * d.a.nsteps < share_begin(p + 1, d.units, d.pe) * d.gran) {
+      ++g;
+      return true;
+    }
+  }
+  for (c = c < 0 ? lane : c + lanes; c < ncalls; c += lanes) {
+    const StackDesc& d = calls[c];
+    if (p < d.pe) {
+      const unsigned u = share_begin(p, d.units, d.pe);
+      g = d.gran == d.a.nsteps ? (int)u : (int)(u / d.a.nsteps);
+      return true;
+    }
+  }
+  return false;
+}
 
 template <class F>
-const void* stack_fn() {
-  return reinterpret_cast<const void*>(&stack_kernel<F, kStackWaves>);
+__device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, Item<1>& it,
+                                              uint4 (&buf)[PipeDepth<1>::PF][1][F::LOADS]) {
+  int step0, nst, piece, np;
+  share_item(p, g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
+  item_prefetch_range<F, 1>(d.a, g, step0, nst, piece, np, it, buf);
 }
 
-const void* stack_fn_for(int fmt) {
+template <class F, int WAVES, bool DLDS>
+__global__ void __launch_bounds__(WAVES * 64)
+stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
+             int desc_off, int lanes) {
+  extern __shared__ __align__(16) char lds[];
+  const int per_lane = gridDim.x / lanes;
+  const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
+  const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
+  const StackDesc* calls = gcalls;
+  if constexpr (DLDS) {
+    const int n16 = ncalls * (int)(sizeof(StackDesc) / 16);
+    const auto src = gmem(reinterpret_cast<const u32x4*>(gcalls));
+    u32x4* dst = reinterpret_cast<u32x4*>(lds + desc_off);
+    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+    __syncthreads();
+    calls = reinterpret_cast<const StackDesc*>(lds + desc_off);
+  }
+  Item<1> cur, nxt;
+  uint4 buf[PipeDepth<1>::PF][1][F::LOADS];
+  f32x4 acc[1][1];
+  int nc = -1, ng = 0;
+  bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
+  if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+  while (have) {
+    const int c = nc;
+    const StackDesc& d = calls[c];
+    cur = nxt;
+    if (d.xwire)
+      item_main<F, 1, 1, WAVES>(d.a, XWire{d.xwire, w}, lds, cur, buf, acc);
+    else
+      item_main<F, 1, 1, WAVES>(d.a, XPlain{}, lds, cur, buf, acc);
+    // The next item's weights stream during the epilogue -- except when the epilogue waits
+    // for other pieces: its loads would then also wait for the prefetch (memory counters
+    // complete in order), so the reducer prefetches afterwards.
+    const bool reducer = cur.np > 1 && cur.s == 0;
+    if (!reducer) {
+      have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
+      if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+    }
+    if (d.sw)
+      exec_finish<F, true>(d, lds, cur, acc, w);
+    else
+      exec_finish<F, false>(d, lds, cur, acc, w);
+    if (reducer) {
+      have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
+      if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+    }
+    __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+template <class F>
+const void* stack_fn(int waves, bool dlds) {
+  if (waves == 4)
+    return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, 4, true>)
+                : reinterpret_cast<const void*>(&stack_kernel<F, 4, false>);
+  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, 8, true>)
+              : reinterpret_cast<const void*>(&stack_kernel<F, 8, false>);
+}
+
+const void* stack_fn_for(int fmt, int waves, bool dlds) {
   switch (fmt) {
-    case QLX_FMT_W8A16: return stack_fn<FmtW8>();
-    case QLX_FMT_W4A16: return stack_fn<FmtW4>();
-    case QLX_FMT_FP8: return stack_fn<FmtFP8>();
+    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, dlds);
+    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, dlds);
+    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, dlds);
     default: return nullptr;
   }
 }
@@ -132,37 +311,93 @@ FmtInfo stack_info(int fmt) {
   }
 }
 
-// Plan of one projection for P resident workgroups of 8 waves: the (kw, splits) whose busiest
-// workgroup streams the fewest bytes, counting each extra item as 64 KB of overhead; ties go
-// to fewer items.
-qlx_plan stack_plan(const FmtInfo& fi, int mode, int m, int n, int k, int P, int bytes_per_k) {
-  qlx_plan best = {};
-  double best_cost = 1e300;
-  const int nsteps = k / fi.kstep;
+// ---- planning (host) -------------------------------------------------------------------
+
+struct StackPlan {
+  qlx_plan plan;
+  int units, pe, gran, sps, max_np;
+};
+
+// Checks the shares of one candidate: every row block's pieces are consecutive workgroups
+// whose step ranges tile [0, ns) in order, each within sps steps. Returns the most pieces of
+// one row block, or -1.
+int check_shares(int groups, int ns, int U, int pe, int gran, int sps) {
+  int max_np = 1;
+  for (int g = 0; g < groups; ++g) {
+    const unsigned gs = (unsigned)g * ns;
+    const int first = (int)share_owner(gs / gran, U, pe);
+    int step = 0, np0 = -1;
+    for (int q = first; q < pe && share_begin(q, U, pe) * gran < gs + ns; ++q) {
+      int s0, nst, piece, np;
+      share_item(q, g, U, pe, gran, ns, &s0, &nst, &piece, &np);
+      if (s0 != step || nst < 1 || nst > sps || piece != q - first || (np0 >= 0 && np != np0)) return -1;
+      np0 = np;
+      step += nst;
+    }
+    if (step != ns || np0 < 1) return -1;
+    if (np0 > max_np) max_np = np0;
+  }
+  return max_np;
+}
+
+// kw (so rt = 8 / kw tiles per row block) and the unit size (one block-step, or one whole
+// row block). Cost, in bytes of the busiest workgroup: its weight bytes (a tile step is 2 KB
+// in every executor format), a fixed charge per item, and one extra dependency trip when
+// row blocks are cut into pieces.
+bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, int waves, int force_kw,
+                     StackPlan& out) {
+  constexpr double kStepBytes = 2048.0, kItemBytes = 16384.0, kPieceBytes = 49152.0;
+  const int ns = k / fi.kstep;
   const int ntiles = n / 16;
-  for (int kw = 1; kw <= kStackWaves; kw *= 2) {
-    for (int splits = 1; splits <= 8 && splits <= nsteps; ++splits) {
-      qlx_plan p = {};
-      p.mode = mode;
-      p.waves = kStackWaves;
-      p.kw = kw;
-      p.rw = 1;
-      p.splits = splits;
-      GemmArgs a = {};
-      if (layout(fi, p, m, n, k, a) > kLdsTarget) continue;
-      if (a.splits != splits) continue;  // not a normalised split count
-      const int items = a.tile_groups * a.splits;
-      const int per_wg = (items + P - 1) / P;
-      const double item_bytes = (double)a.rt * 16 * (double)a.sps * fi.kstep * bytes_per_k;
-      const double cost = per_wg * (item_bytes + 65536.0) + 1e-3 * items;
-      (void)ntiles;
-      if (cost < best_cost) {
-        best_cost = cost;
-        best = p;
+  double best = 1e300;
+  bool found = false;
+  for (int kw = 1; kw <= waves; kw *= 2) {
+    if (force_kw && kw != force_kw) continue;
+    const int rt = waves / kw;
+    const int groups = (ntiles + rt - 1) / rt;
+    for (int whole = 0; whole < 2; ++whole) {
+      const int gran = whole ? ns : 1;
+      const long long U = (long long)groups * ns / gran;
+      if ((U + 1) * (P + 1) >= (1LL << 31) || U * gran >= (1LL << 31)) continue;  // 32-bit share math
+      // Fewer workgroups than P give bigger shares: fewer pieces per row block, more LDS.
+      for (int div = 1; div <= 8; div *= 2) {
+        const int pe = U < P / div ? (int)U : P / div;
+        if (pe < 1 || (div > 1 && pe == U)) continue;
+        const long long per = (U + pe - 1) / pe * gran;  // most block-steps of one workgroup
+        const int sps = (int)(per < ns ? per : ns);
+        qlx_plan p = {};
+        p.mode = mode;
+        p.waves = waves;
+        p.kw = kw;
+        p.rw = 1;
+        p.splits = ns / sps;  // layout() then sizes LDS for ceil(ns / splits) >= sps steps
+        GemmArgs a = {};
+        const int lds = layout(fi, p, m, n, k, a);
+        if (a.sps < sps || lds > kLdsLimit) continue;
+        const int max_np = check_shares(groups, ns, (int)U, pe, gran, sps);
+        if (max_np < 1 || max_np > kMaxPieces) continue;
+        const long long items = whole ? per / ns : (per + ns - 1) / ns + 1;
+        const double cost = (double)per * rt * kStepBytes + items * kItemBytes + (max_np > 1 ? kPieceBytes : 0.0);
+        if (cost < best) {
+          best = cost;
+          found = true;
+          out.plan = p;
+          out.units = (int)U;
+          out.pe = pe;
+          out.gran = gran;
+          out.sps = a.sps;
+          out.max_np = max_np;
+        }
       }
     }
   }
-  return best;
+  return found;
+}
+
+bool overlaps(const void* a, long long na, const void* b, long long nb) {
+  const char* x = static_cast<const char*>(a);
+  const char* y = static_cast<const char*>(b);
+  return x < y + nb && y < x + na;
 }
 
 }  // namespace qlx
@@ -173,54 +408,101 @@ extern "C" {
 
 int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 
-int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int groups_per_cu, void* desc,
-                    qlx_plan* plans, float* workspace, int* tickets, long long* workspace_floats,
-                    int* tickets_needed, int* grid, int* lds_bytes) {
-  const void* fn = stack_fn_for(fmt);
-  QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
+int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
+                    void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch) {
+  QLX_REQUIRE(stack_fn_for(fmt, 8, false) != nullptr,
+              "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
+  QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
   QLX_REQUIRE(m >= 1 && m <= 16, "the decode executor serves m = 1..16 (got %d)", m);
   QLX_REQUIRE(calls != nullptr && ncalls >= 1, "no projections");
   QLX_REQUIRE(groups_per_cu >= 1 && groups_per_cu <= 4, "groups_per_cu must be 1..4");
-  int dev = 0, cus = 0, occ = 0;
+  const FmtInfo fi = stack_info(fmt);
+  // Shapes, and which earlier projection (if any) produces each activation. Outputs may not
+  // overlap each other or an activation read from memory: the chain has no ordering between
+  // projections other than these data dependencies.
+  std::vector<int> src(ncalls, -1), published(ncalls, 0);
+  for (int c = 0; c < ncalls; ++c) {
+    const qlx_stack_call& q = calls[c];
+    QLX_REQUIRE(q.kw == 0 || q.kw == 1 || q.kw == 2 || q.kw == 4 || q.kw == 8,
+                "projection %d: kw must be 0 (planner) or 1, 2, 4, 8", c);
+    QLX_REQUIRE(q.n >= 16 && q.n % 16 == 0 && q.k > 0 && q.k % fi.kstep == 0,
+                "projection %d: n=%d k=%d do not fit the tiled format", c, q.n, q.k);
+    QLX_REQUIRE(q.mode == QLX_MODE_BF16 || q.mode == QLX_MODE_SWIGLU, "projection %d: mode %d", c, q.mode);
+    QLX_REQUIRE(q.w && q.w_scale && q.x && q.y, "projection %d: NULL pointer", c);
+  }
+  auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };
+  for (int c = 0; c < ncalls; ++c) {
+    const long long ybytes = 2LL * m * nout(c);
+    for (int j = 0; j < ncalls; ++j) {
+      if (j != c) QLX_REQUIRE(!overlaps(calls[c].y, ybytes, calls[j].y, 2LL * m * nout(j)),
+                              "outputs of projections %d and %d overlap", c, j);
+    }
+    const long long xbytes = 2LL * m * calls[c].k;
+    for (int j = 0; j < ncalls; ++j) {
+      if (calls[c].x == calls[j].y && j < c && nout(j) == calls[c].k) {
+        src[c] = j;
+        published[j] = 1;
+        break;
+      }
+    }
+    if (src[c] < 0)
+      for (int j = 0; j < ncalls; ++j)
+        QLX_REQUIRE(!overlaps(calls[c].x, xbytes, calls[j].y, 2LL * m * nout(j)),
+                    "projection %d reads memory that projection %d writes (only the whole output of an "
+                    "earlier projection can be an input)", c, j);
+  }
+  int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return hip_status(e, "stack_build");
-  const FmtInfo fi = stack_info(fmt);
-  const int bytes_num = fmt == QLX_FMT_W4A16 ? 1 : 2;  // bytes per 2 k values
-  // LDS of the widest projection decides occupancy.
-  int lds = 0;
-  std::vector<qlx_plan> plans_v;  // per projection, for the final P
-  int P = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    if (pass == 1) {
-      if (lds > 64 * 1024) {
-        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e != hipSuccess) return hip_status(e, "stack_build");
-      }
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kStackWaves * 64, lds);
-      if (e != hipSuccess) return hip_status(e, "stack_build");
-      QLX_REQUIRE(occ >= 1, "the executor does not fit a CU with %d bytes of LDS", lds);
-      P = cus * (occ < groups_per_cu ? occ : groups_per_cu);
-    }
-    const int Pp = pass == 0 ? cus * groups_per_cu : P;
-    plans_v.clear();
-    lds = 0;
+  std::vector<StackPlan> sp(ncalls);
+  int lds = 0, lanes = groups_per_cu, desc_lds = -1;
+  const int P = cus;  // workgroups per lane
+  const long long desc_bytes = (long long)ncalls * sizeof(StackDesc);
+  // Plan for P workgroups, then shrink P to what fits the CUs with that LDS; repeat until
+  // plan and grid agree.
+  for (int round = 0;; ++round) {
+    QLX_REQUIRE(round < 4, "no stable executor grid");
+    int items_lds = 0;
     for (int c = 0; c < ncalls; ++c) {
       const qlx_stack_call& q = calls[c];
-      QLX_REQUIRE(q.n >= 16 && q.n % 16 == 0 && q.k % fi.kstep == 0 && q.k > 0,
-                  "projection %d: n=%d k=%d do not fit the tiled format", c, q.n, q.k);
-      QLX_REQUIRE(q.mode == QLX_MODE_BF16 || q.mode == QLX_MODE_SWIGLU, "projection %d: mode %d", c, q.mode);
-      qlx_plan p = stack_plan(fi, q.mode, m, q.n, q.k, Pp, bytes_num);
-      QLX_REQUIRE(p.waves == kStackWaves, "projection %d: no plan fits", c);
+      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, sp[c]),
+                  "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
       GemmArgs a = {};
-      const int l = layout(fi, p, m, q.n, q.k, a);
-      if (l > lds) lds = l;
-      plans_v.push_back(p);
+      const int l = layout(fi, sp[c].plan, m, q.n, q.k, a);
+      if (l > items_lds) items_lds = l;
+    }
+    items_lds = (items_lds + 15) & ~15;
+    desc_lds = items_lds + desc_bytes <= kLdsLimit ? items_lds : -1;
+    lds = desc_lds >= 0 ? (int)(items_lds + desc_bytes) : items_lds;
+    const void* fn = stack_fn_for(fmt, waves, desc_lds >= 0);
+    if (lds > 64 * 1024) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      if (e != hipSuccess) return hip_status(e, "stack_build");
+    }
+    int occ = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * 64, lds);
+    if (e != hipSuccess) return hip_status(e, "stack_build");
+    QLX_REQUIRE(occ >= 1, "the executor does not fit a CU with %d bytes of LDS", lds);
+    if (occ >= lanes) break;
+    lanes = occ;
+  }
+  // Arena: published outputs and partial sums, 256-byte aligned regions.
+  long long off = 0;
+  std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1);
+  for (int c = 0; c < ncalls; ++c) {
+    if (published[c]) {
+      wire_off[c] = off;
+      off += ((8LL * m * (nout(c) / 2)) + 255) & ~255LL;
+    }
+    if (sp[c].max_np > 1) {
+      part_off[c] = off;
+      off += ((8LL * (sp[c].max_np - 1) * m * calls[c].n) + 255) & ~255LL;
     }
   }
-  long long ws = 0;
-  int tk = 0;
   StackDesc* out = reinterpret_cast<StackDesc*>(desc);
+  if (out) QLX_REQUIRE(arena != nullptr || off == 0, "the chain needs an arena of %lld bytes", off);
+  char* base = static_cast<char*>(arena);
   for (int c = 0; c < ncalls; ++c) {
     const qlx_stack_call& q = calls[c];
     StackDesc d = {};
@@ -229,39 +511,55 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     d.a.x = q.x;
     d.a.y = q.y;
     d.a.tiled = 1;
-    layout(fi, plans_v[c], m, q.n, q.k, d.a);
-    d.a.work = workspace;
-    d.a.tickets = tickets;
-    d.items = d.a.tile_groups * d.a.splits;
-    d.sw = q.mode == QLX_MODE_SWIGLU;
-    if (d.a.splits > 1) {
-      const long long need = (long long)d.a.splits * m * q.n;
-      if (need > ws) ws = need;
-      if (d.a.tile_groups > tk) tk = d.a.tile_groups;
+    layout(fi, sp[c].plan, m, q.n, q.k, d.a);
+    d.a.splits = sp[c].max_np;
+    if (base) {
+      d.ywire = wire_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[c]) : nullptr;
+      d.part = part_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + part_off[c]) : nullptr;
+      d.xwire = src[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[src[c]]) : nullptr;
     }
+    d.units = sp[c].units;
+    d.pe = sp[c].pe;
+    d.gran = sp[c].gran;
+    d.sw = q.mode == QLX_MODE_SWIGLU;
     if (out) out[c] = d;
     if (plans) {
-      plans[c] = plans_v[c];
-      plans[c].splits = d.a.splits;
-      plans[c].workspace = d.a.splits > 1 ? workspace : nullptr;
-      plans[c].tickets = d.a.splits > 1 ? tickets : nullptr;
+      plans[c] = sp[c].plan;
+      plans[c].splits = sp[c].max_np;
+      plans[c].workspace = nullptr;
+      plans[c].tickets = nullptr;
     }
   }
-  if (workspace_floats) *workspace_floats = ws;
-  if (tickets_needed) *tickets_needed = tk;
-  if (grid) *grid = P;
-  if (lds_bytes) *lds_bytes = lds;
+  if (arena_bytes) *arena_bytes = off;
+  if (launch) {
+    launch->grid = P * lanes;
+    launch->lanes = lanes;
+    launch->lds_bytes = lds;
+    launch->waves = waves;
+    launch->desc_lds = desc_lds;
+  }
   return QLX_OK;
 }
 
-int qlx_stack_run(int fmt, const void* desc, int ncalls, int grid, int lds_bytes, int* sync, int spin_limit,
-                  void* stream) {
-  const void* fn = stack_fn_for(fmt);
+int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
+                  int* error, long long budget_us, void* stream) {
+  QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1,
+              "bad executor launch configuration");
+  const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
-  QLX_REQUIRE(desc && sync && ncalls >= 1 && grid >= 1 && spin_limit >= 1, "bad executor arguments");
-  void* args[] = {(void*)&desc, (void*)&ncalls, (void*)&sync, (void*)&spin_limit};
-  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kStackWaves * 64), args, (unsigned)lds_bytes,
-                                            (hipStream_t)stream);
+  QLX_REQUIRE(desc && error && ncalls >= 1, "bad executor arguments");
+  QLX_REQUIRE(launch->desc_lds < 0 || launch->desc_lds + (long long)ncalls * (long long)sizeof(StackDesc) <=
+                                          launch->lds_bytes,
+              "descriptor copy does not fit the launch's LDS");
+  QLX_REQUIRE(epoch != 0, "epoch 0 is reserved (a zeroed arena carries it)");
+  QLX_REQUIRE(budget_us >= 0 && budget_us <= 600000000LL, "budget_us must be 0..600e6");
+  long long ticks = budget_us * 100;  // the real-time counter runs at 100 MHz
+  int desc_off = launch->desc_lds, lanes = launch->lanes;
+  QLX_REQUIRE(lanes >= 1 && launch->grid % lanes == 0, "bad executor lanes");
+  void* args[] = {(void*)&desc, (void*)&ncalls, (void*)&epoch, (void*)&error, (void*)&ticks, (void*)&desc_off,
+                  (void*)&lanes};
+  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3(launch->waves * 64), args,
+                                            (unsigned)launch->lds_bytes, (hipStream_t)stream);
   return hip_status(e, "stack_run");
 }
 

@@ -100,19 +100,19 @@ __device__ __forceinline__ void publish_stores() {
   __syncthreads();
 }
 
-// 16 bytes of activation; device-coherent when another workgroup of the same launch wrote
-// them (the decode executor), a plain 128-bit load otherwise.
-template <bool COH>
-__device__ __forceinline__ uint4 load_x16(const void* p) {
-  if (COH) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    return uint4{__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+// Where a work item's bf16 activation comes from. Staging reads it 8 values (16 bytes) at
+// a time in two phases, fetch (issue the loads) and settle (the values), so a thread can
+// have several chunks in flight. The single-call kernels read x from device memory.
+struct XPlain {
+  struct Raw {
+    uint4 v;
+  };
+  __device__ __forceinline__ void fetch(const GemmArgs& a, int mm, int kabs, Raw& r) const {
+    const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs));
+    r.v = uint4{v[0], v[1], v[2], v[3]};
   }
-  return *reinterpret_cast<const uint4*>(p);
-}
+  __device__ __forceinline__ uint4 settle(const GemmArgs&, int, int, const Raw& r) const { return r.v; }
+};
 
 // Two exact small-integer floats -> bf16 pair (the high halves are exact: <= 8 significant bits).
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
@@ -156,12 +156,12 @@ struct FmtW4 {
                                           (size_t)wrow * (a.k >> 3) + step * 32 + j * 16 + (lane >> 4) * 4);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 7) + 2 * step + j]);
+    return bf2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 7) + 2 * step + j]);
   }
-  // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword).
-  template <bool COH>
-  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
+  // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword);
+  // the staged activation chunk (8 values in k order) is permuted to match.
+  static constexpr bool GATHER = false;
+  __device__ static uint4 order(uint4 v) {
     uint4 o;
     o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
     o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
@@ -232,12 +232,10 @@ struct FmtW8 {
                                           step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
+    return bf2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[wrow]);
   }
-  template <bool COH>
-  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    return load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
-  }
+  static constexpr bool GATHER = false;
+  __device__ static uint4 order(uint4 v) { return v; }
   __device__ static f32x4 bias_chain(const char* lds, int srel, int, int lane, int xoff) {
     const uint4 av = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
     f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
@@ -300,7 +298,7 @@ struct FmtFP8 {
                                           step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int, int) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[wrow]);
+    return bf2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[wrow]);
   }
   template <int MT>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
@@ -357,7 +355,7 @@ struct FmtRef {
     return reinterpret_cast<const uint4*>(w + (size_t)wrow * a.k + step * 128 + j * 64 + c * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
-    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
+    return h2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
   }
   // B position e (0..7) of chunk (c, u) of a 64-block holds permuted position 16c + 8u + sw(e):
   // 8-bit codes unpack in byte order, 4-bit codes as bytes (0,2),(1,3) per dword.
@@ -373,9 +371,8 @@ struct FmtRef {
     }
     return t4;
   }
-  template <bool COH>
+  static constexpr bool GATHER = true;  // staged from permuted positions (stage_chunk)
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    static_assert(!COH, "coherent staging is implemented for the north-star formats");
     const uint16_t* row = reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k;
     const int blk = kabs & ~63, p0 = kabs & 63;
     uint32_t v[8];
@@ -442,13 +439,11 @@ struct FmtFP8WO {
                                           step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
-    return bf2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k / a.group) +
+    return bf2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k / a.group) +
                                                         (step * 128 + j * 64) / a.group]);
   }
-  template <bool COH>
-  __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    return load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs);
-  }
+  static constexpr bool GATHER = false;
+  __device__ static uint4 order(uint4 v) { return v; }
   template <bool HI>
   __device__ static uint32_t fp8pair(uint32_t d) {
     typedef __attribute__((ext_vector_type(2))) float f2;
@@ -500,7 +495,7 @@ struct FmtInt8 {
                                           step * 128 + j * 64 + (lane >> 4) * 16);
   }
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
-    return h2f(reinterpret_cast<const uint16_t*>(a.ws)[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
+    return h2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
   }
   template <int MT>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
@@ -539,15 +534,41 @@ struct FmtInt8 {
 // Prologue: stage the workgroup's activation slice (B order), its scales, bias sums.
 // ====================================================================================
 
-template <class F, bool COH>
-__device__ void stage_bf16(const GemmArgs& a, char* lds, int step0, int nst) {
+// Chunks each thread keeps in flight while staging.
+constexpr int kStageUnroll = 4;
+
+template <class F, class XS>
+__device__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst) {
   constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
   const int cpr = nst * CPS;
   const int total = a.m * cpr;
-  for (int q = threadIdx.x; q < total; q += blockDim.x) {
-    const int mm = q / cpr, kc = q - mm * cpr;
-    *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) =
-        F::template stage_chunk<COH>(a, mm, step0 * F::KSTEP + kc * 8);
+  if constexpr (F::GATHER) {
+    static_assert(std::is_same<XS, XPlain>::value, "gathered staging reads x from device memory");
+    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+      const int mm = q / cpr, kc = q - mm * cpr;
+      *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = F::stage_chunk(a, mm, step0 * F::KSTEP + kc * 8);
+    }
+  } else {
+    for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
+      typename XS::Raw r[kStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int q = q0 + u * blockDim.x;
+        if (q < total) {
+          const int mm = q / cpr, kc = q - mm * cpr;
+          xs.fetch(a, mm, step0 * F::KSTEP + kc * 8, r[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int q = q0 + u * blockDim.x;
+        if (q < total) {
+          const int mm = q / cpr, kc = q - mm * cpr;
+          *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) =
+              F::order(xs.settle(a, mm, step0 * F::KSTEP + kc * 8, r[u]));
+        }
+      }
+    }
   }
 }
 
@@ -569,48 +590,64 @@ __device__ void stage_bias(const GemmArgs& a, char* lds, int nst) {
 }
 
 // FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice.
-template <bool COH>
-__device__ void stage_fp8_act(const GemmArgs& a, char* lds, int step0, int nst) {
+template <class XS>
+__device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst) {
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
   uint32_t* amax = reinterpret_cast<uint32_t*>(sx + a.m);
   for (int i = threadIdx.x; i < a.m; i += blockDim.x) amax[i] = 0u;
   __syncthreads();
   const int cpr = a.k >> 3;
   const int total = a.m * cpr;
-  int cur = -1;
-  float mx = 0.f;
-  for (int q = threadIdx.x; q < total; q += blockDim.x) {
-    const int mm = q / cpr;
-    if (mm != cur) {
-      if (cur >= 0) atomicMax(&amax[cur], __float_as_uint(mx));
-      cur = mm;
-      mx = 0.f;
-    }
-    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)q * 8);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
+    typename XS::Raw r[kStageUnroll];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int q = q0 + u * blockDim.x;
+      if (q < total) xs.fetch(a, q / cpr, (q % cpr) * 8, r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int q = q0 + u * blockDim.x;
+      if (q < total) {
+        const uint4 v = xs.settle(a, q / cpr, (q % cpr) * 8, r[u]);
+        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
+        atomicMax(&amax[q / cpr], __float_as_uint(mx));
+      }
+    }
   }
-  if (cur >= 0) atomicMax(&amax[cur], __float_as_uint(mx));
   __syncthreads();
   for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = fmaxf(__uint_as_float(amax[i]) / 448.f, 1e-12f);
   __syncthreads();
   const int cps = nst * 16;  // 8-value chunks per row of the slice
-  for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
-    const int mm = q / cps, kc = q - mm * cps;
-    const uint4 v = load_x16<COH>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + step0 * 128 + kc * 8);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-    const float s = sx[mm];
-    uint32_t c[8];
+  for (int q0 = threadIdx.x; q0 < a.m * cps; q0 += kStageUnroll * blockDim.x) {
+    typename XS::Raw r[kStageUnroll];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
-      c[e] = f32_to_e4m3(clamp_keep_nan(xv / s, 448.f));
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int q = q0 + u * blockDim.x;
+      if (q < a.m * cps) xs.fetch(a, q / cps, step0 * 128 + (q % cps) * 8, r[u]);
     }
-    uint2 o;
-    o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    *reinterpret_cast<uint2*>(lds + mm * a.xstride + kc * 8) = o;
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int q = q0 + u * blockDim.x;
+      if (q >= a.m * cps) continue;
+      const int mm = q / cps, kc = q - mm * cps;
+      const uint4 v = xs.settle(a, mm, step0 * 128 + kc * 8, r[u]);
+      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+      const float sc = sx[mm];
+      uint32_t c[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
+        c[e] = f32_to_e4m3(clamp_keep_nan(xv / sc, 448.f));
+      }
+      uint2 o;
+      o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+      o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+      *reinterpret_cast<uint2*>(lds + mm * a.xstride + kc * 8) = o;
+    }
   }
 }
 
@@ -638,19 +675,19 @@ template <class F>
 __device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, int nst) {
   float* sc = reinterpret_cast<float*>(lds + a.off_sc);
   const int rows = 16 * a.rt;
-  if (F::NSC == 0) {
+  if constexpr (F::NSC == 0) {
     for (int rl = threadIdx.x; rl < rows; rl += blockDim.x) {
       const int tile = tg * a.rt + (rl >> 4);
       sc[rl] = tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), 0, 0) : 0.f;
     }
-    return;
-  }
-  const int total = nst * F::NSC * rows;
-  for (int q = threadIdx.x; q < total; q += blockDim.x) {
-    const int sj = q / rows, rl = q - sj * rows;
-    const int tile = tg * a.rt + (rl >> 4);
-    sc[sj * a.sc_stride + rl] =
-        tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), step0 + sj / F::NSC, sj % F::NSC) : 0.f;
+  } else {
+    const int total = nst * F::NSC * rows;
+    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+      const int sj = q / rows, rl = q - sj * rows;
+      const int tile = tg * a.rt + (rl >> 4);
+      sc[sj * a.sc_stride + rl] =
+          tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), step0 + sj / F::NSC, sj % F::NSC) : 0.f;
+    }
   }
 }
 
@@ -674,7 +711,7 @@ __device__ __forceinline__ void load_chunk(uint4 (&c)[F::LOADS], const GemmArgs&
                                            int lane) {
 #pragma unroll
   for (int j = 0; j < F::LOADS; ++j) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(F::chunk_ptr(a, wrow, step, lane, j)));
+    const u32x4 v = __builtin_nontemporal_load(gmem(reinterpret_cast<const u32x4*>(F::chunk_ptr(a, wrow, step, lane, j))));
     c[j] = uint4{v[0], v[1], v[2], v[3]};
   }
 }
@@ -684,25 +721,28 @@ struct PipeDepth {
   static constexpr int PF = RW == 1 ? 4 : 2;  // steps in flight per wave (each 2 KB for RW = 1)
 };
 
-// Per-wave state of one work item, fixed by item_prefetch.
+// Per-wave state of one work item, fixed by item_prefetch: row block tg, steps
+// [step0, step0 + nst), K piece s of the np pieces the row block is cut into.
 template <int RW>
 struct Item {
-  int tg, s, step0, nst, wt, kwi, tile0, my, last;
+  int tg, s, np, step0, nst, wt, kwi, tile0, my, last;
   int wrow[RW];  // a tile past the end streams its neighbour's rows; its output is dropped
 };
 
-// Issue the wave's first PF steps of weight loads for work item (tg, s). They depend on
-// nothing else, so they are in flight while the activation is staged (or, in the decode
-// executor, while the previous projection finishes).
+// Issue the wave's first PF steps of weight loads for a work item. They depend on nothing
+// else, so they are in flight while the activation is staged (or, in the decode executor,
+// while the previous item finishes or the previous projection completes).
 template <class F, int RW>
-__device__ __forceinline__ void item_prefetch(const GemmArgs& a, int tg, int s, Item<RW>& it,
-                                              uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+__device__ __forceinline__ void item_prefetch_range(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
+                                                    Item<RW>& it,
+                                                    uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
   constexpr int PF = PipeDepth<RW>::PF;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   it.tg = tg;
   it.s = s;
-  it.step0 = s * a.sps;
-  it.nst = min(a.nsteps, it.step0 + a.sps) - it.step0;
+  it.np = np;
+  it.step0 = step0;
+  it.nst = nst;
   it.wt = wave / a.kw;
   it.kwi = wave - it.wt * a.kw;
   it.tile0 = tg * a.rt + it.wt * RW;
@@ -719,37 +759,46 @@ __device__ __forceinline__ void item_prefetch(const GemmArgs& a, int tg, int s, 
       for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, it.wrow[r], it.step0 + it.kwi + p * a.kw, lane);
 }
 
-// bf16 pair (rows idx, idx + 1) to y; device-coherent when another workgroup of the same
-// launch reads it (the decode executor).
-template <bool COH>
-__device__ __forceinline__ void store_pair(uint16_t* y, size_t idx, float v0, float v1) {
-  const uint32_t w = (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
-  if (COH)
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(y + idx), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else
-    *reinterpret_cast<uint32_t*>(y + idx) = w;
+// Work item (tg, s) of a launch whose row blocks are cut into a.splits equal K slices.
+template <class F, int RW>
+__device__ __forceinline__ void item_prefetch(const GemmArgs& a, int tg, int s, Item<RW>& it,
+                                              uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+  const int step0 = s * a.sps;
+  item_prefetch_range<F, RW>(a, tg, step0, min(a.nsteps, step0 + a.sps) - step0, s, a.splits, it, buf);
 }
 
-// Stage the activation, stream the item's weight steps through the MFMAs, combine the kw
-// waves of each tile, write the output (bf16, SwiGLU or fp32 planes), and for split-K let
-// the last workgroup of the row block reduce the planes in slice order.
-// COH: activation reads and output writes are device-coherent (other workgroups of the
-// same launch produce the input / consume the output).
-template <class F, int MT, int RW, int WAVES, bool SW, bool COH>
-__device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
-                         uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+// bf16 pair (rows idx, idx + 1) as one 32-bit word, and its store.
+__device__ __forceinline__ uint32_t bf16_pair(float v0, float v1) {
+  return (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
+}
+__device__ __forceinline__ void store_pair(uint16_t* y, size_t idx, float v0, float v1) {
+  *gmem(reinterpret_cast<uint32_t*>(y + idx)) = bf16_pair(v0, v1);
+}
+
+// y = bf16(bf16(silu(g)) * u) with g and u rounded to bf16 first (swiglu.py:12-30).
+__device__ __forceinline__ float swiglu_bf(float g, float u) {
+  const float gb = round_bf(g), ub = round_bf(u);
+  return round_bf(gb / (1.f + expf(-gb))) * ub;
+}
+
+// Stage the activation (from xs), then stream the item's weight steps through the MFMAs into
+// acc. On return the weight buffer is free (the next item may be prefetched into it) and LDS
+// still holds what the epilogue needs.
+template <class F, int MT, int RW, int WAVES, class XS>
+__device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char* lds, const Item<RW>& it,
+                                          uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS], f32x4 (&acc)[RW][MT]) {
   constexpr int PF = PipeDepth<RW>::PF;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tg = it.tg, s = it.s, step0 = it.step0, nst = it.nst, wt = it.wt, kwi = it.kwi, my = it.my;
+  const int lane = threadIdx.x & 63;
+  const int tg = it.tg, step0 = it.step0, nst = it.nst, wt = it.wt, kwi = it.kwi, my = it.my;
 
   // ---- prologue
   if constexpr (std::is_same<F, FmtFP8>::value) {
-    stage_fp8_act<COH>(a, lds, step0, nst);
+    stage_fp8_act(a, xs, lds, step0, nst);
   } else if constexpr (std::is_same<F, FmtInt8>::value) {
-    static_assert(!COH, "coherent staging is implemented for the north-star formats");
+    static_assert(std::is_same<XS, XPlain>::value, "int8 activations are read from device memory");
     stage_int8_act(a, lds, step0, nst);
   } else {
-    stage_bf16<F, COH>(a, lds, step0, nst);
+    stage_bf16<F>(a, xs, lds, step0, nst);
   }
   stage_scales<F>(a, lds, tg, step0, nst);
   __syncthreads();
@@ -759,7 +808,6 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
   }
 
   // ---- main loop
-  f32x4 acc[RW][MT];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
 #pragma unroll
@@ -800,9 +848,14 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
     }
   }
 
-  // ---- epilogue: combine the kw waves of each tile through LDS
+}
+
+// Epilogue, first half: every wave's accumulators to LDS ([wave][RW][16 rows][16*MT]).
+template <int MT, int RW>
+__device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();
-  float* red = reinterpret_cast<float*>(lds);  // [wave][RW][16 rows][16*MT]
+  float* red = reinterpret_cast<float*>(lds);
   constexpr int RC = 16 * MT;
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -812,23 +865,36 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
       for (int i = 0; i < 4; ++i)
         red[((wave * RW + r) * 16 + 4 * (lane >> 4) + i) * RC + 16 * mt + (lane & 15)] = acc[r][mt][i];
   __syncthreads();
+}
 
-  auto combined = [&](int tl, int nl, int mm) -> float {
-    const int slot = tl / RW, r = tl - slot * RW;  // tile tl of the block = slot's r-th tile
-    float v = 0.f;
-    for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
-    return F::finish(a, lds, v, tl * 16 + nl, mm);
-  };
-  auto swiglu = [](float g, float u) -> float {
-    const float gb = round_bf(g), ub = round_bf(u);
-    return round_bf(gb / (1.f + expf(-gb))) * ub;
-  };
+// Output (tile tl of the block, tile row nl, token mm): the kw waves' sums added in wave
+// order, then the format's scales.
+template <class F, int MT, int RW>
+__device__ __forceinline__ float tile_value(const GemmArgs& a, const char* lds, int tl, int nl, int mm) {
+  constexpr int RC = 16 * MT;
+  const float* red = reinterpret_cast<const float*>(lds);
+  const int slot = tl / RW, r = tl - slot * RW;  // tile tl of the block = slot's r-th tile
+  float v = 0.f;
+  for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
+  return F::finish(a, lds, v, tl * 16 + nl, mm);
+}
+
+// Combine the kw waves of each tile, write the output (bf16, SwiGLU or fp32 planes), and
+// when the row block is cut into pieces let the last workgroup to finish reduce the
+// planes in piece order.
+template <class F, int MT, int RW, int WAVES, bool SW>
+__device__ __forceinline__ void item_finish(const GemmArgs& a, char* lds, const Item<RW>& it,
+                                            const f32x4 (&acc)[RW][MT]) {
+  const int tg = it.tg, s = it.s, np = it.np;
+  acc_to_lds<MT, RW>(lds, acc);
+  auto combined = [&](int tl, int nl, int mm) -> float { return tile_value<F, MT, RW>(a, lds, tl, nl, mm); };
+  auto swiglu = [](float g, float u) -> float { return swiglu_bf(g, u); };
 
   // Outputs go out in row pairs (one 32-bit store of two bf16).
   constexpr int rows_out = SW ? 8 : 16;
   const int per_tile = (rows_out / 2) * a.m;
   const int total = a.rt * per_tile;
-  const bool direct = a.splits == 1 || a.mode == QLX_MODE_PLANES;
+  const bool direct = np == 1 || a.mode == QLX_MODE_PLANES;
   uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
   for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
     const int tl = idx / per_tile, rem = idx - tl * per_tile;
@@ -839,7 +905,7 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
       const float g0 = combined(tl, nl, mm), u0 = combined(tl, nl + 8, mm);
       const float g1 = combined(tl, nl + 1, mm), u1 = combined(tl, nl + 9, mm);
       if (direct) {
-        store_pair<COH>(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
+        store_pair(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
       } else {
         float* pl = a.work + ((size_t)s * a.m + mm) * a.n + 8 * tile + nl;
         store_coherent(pl, g0);
@@ -860,7 +926,7 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
         store_coherent(pl, v0);
         if (two) store_coherent(pl + 1, v1);
       } else if (two && (a.n & 1) == 0) {
-        store_pair<COH>(y, (size_t)mm * a.n + row, v0, v1);
+        store_pair(y, (size_t)mm * a.n + row, v0, v1);
       } else {
         y[(size_t)mm * a.n + row] = f2bf(v0);
         if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
@@ -878,7 +944,7 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
   publish_stores();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&a.tickets[tg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == a.splits - 1;
+    s_last = prev == np - 1;
     if (s_last) __hip_atomic_store(&a.tickets[tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
@@ -893,25 +959,25 @@ __device__ void item_run(const GemmArgs& a, char* lds, Item<RW>& it,
     if (SW) {
       const float* pg = a.work + (size_t)mm * a.n + 8 * tile + nl;
       float g0 = 0.f, u0 = 0.f, g1 = 0.f, u1 = 0.f;
-      for (int sp = 0; sp < a.splits; ++sp) {
+      for (int sp = 0; sp < np; ++sp) {
         g0 += load_coherent(pg + sp * plane);
         g1 += load_coherent(pg + sp * plane + 1);
         u0 += load_coherent(pg + sp * plane + a.half);
         u1 += load_coherent(pg + sp * plane + a.half + 1);
       }
-      store_pair<COH>(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
+      store_pair(y, (size_t)mm * a.half + 8 * tile + nl, swiglu(g0, u0), swiglu(g1, u1));
     } else {
       const int row = 16 * tile + nl;
       if (row >= a.n) continue;
       const bool two = row + 1 < a.n;
       const float* p = a.work + (size_t)mm * a.n + row;
       float v0 = 0.f, v1 = 0.f;
-      for (int sp = 0; sp < a.splits; ++sp) {
+      for (int sp = 0; sp < np; ++sp) {
         v0 += load_coherent(p + sp * plane);
         if (two) v1 += load_coherent(p + sp * plane + 1);
       }
       if (two && (a.n & 1) == 0) {
-        store_pair<COH>(y, (size_t)mm * a.n + row, v0, v1);
+        store_pair(y, (size_t)mm * a.n + row, v0, v1);
       } else {
         y[(size_t)mm * a.n + row] = f2bf(v0);
         if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
@@ -930,7 +996,9 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   Item<RW> it;
   uint4 buf[PipeDepth<RW>::PF][RW][F::LOADS];
   item_prefetch<F, RW>(a, tg, s, it, buf);
-  item_run<F, MT, RW, WAVES, SW, false>(a, lds, it, buf);
+  f32x4 acc[RW][MT];
+  item_main<F, MT, RW, WAVES>(a, XPlain{}, lds, it, buf, acc);
+  item_finish<F, MT, RW, WAVES, SW>(a, lds, it, acc);
 }
 
 }  // namespace qlx

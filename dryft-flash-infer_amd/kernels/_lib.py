@@ -36,8 +36,15 @@ class StackCall(ctypes.Structure):
 
     _fields_ = [
         ("w", ctypes.c_void_p), ("w_scale", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
-        ("n", ctypes.c_int), ("k", ctypes.c_int), ("mode", ctypes.c_int), ("pad", ctypes.c_int),
+        ("n", ctypes.c_int), ("k", ctypes.c_int), ("mode", ctypes.c_int), ("kw", ctypes.c_int),
     ]
+
+
+class StackLaunch(ctypes.Structure):
+    """``qlx_stack_launch``: grid, LDS bytes, waves, descriptor LDS offset, lanes."""
+
+    _fields_ = [("grid", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("waves", ctypes.c_int),
+                ("desc_lds", ctypes.c_int), ("lanes", ctypes.c_int), ("pad", ctypes.c_int)]
 
 
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
@@ -72,8 +79,9 @@ SIGNATURES = {
     "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
     "qlx_stack_desc_size": ([], _I),
-    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _P, _PLAN, _P, _P, _PLL, _PI, _PI, _PI], _I),
-    "qlx_stack_run": ([_I, _P, _I, _I, _I, _P, _I, _P], _I),
+    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _P, _PLAN, _P, _PLL,
+                         ctypes.POINTER(StackLaunch)], _I),
+    "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 

@@ -3,18 +3,20 @@
 The reference replays a captured graph of per-projection launches whose weight loads
 overlap the previous kernel through programmatic dependent launch
 (engine/kernels/cuda_fp8.py:47-50, 150-169; engine/kernels/cuda_jit.py:218-262). On MI355X
-the chain runs inside one launch (``qlx_stack_run``): each workgroup issues its first
-weight loads for the next projection before waiting for the previous one to finish.
+the chain runs inside one launch (``qlx_stack_run``): workgroups stream each projection's
+weights while its input is still being produced, and wait only for the words they need.
 
     chain = DecodeStack("fp8", m=1)
     chain.add(tiled_qkv, x_hidden, y_qkv)
     chain.add(tiled_gate_up, x_normed, y_act, swiglu=True)
-    chain.add(tiled_down, y_act, y_out)            # reads what gate_up wrote
+    chain.add(tiled_down, y_act, y_out)            # reads what gate_up writes
     chain.build()
     chain.run()                                     # on torch.cuda.current_stream()
 
 Inputs and outputs are caller-owned bf16 tensors that stay in place between runs (the
-descriptors hold their addresses), like the static buffers of a captured decode graph.
+descriptors hold their addresses), like the static buffers of a captured decode graph. An
+input is either memory no projection of the chain writes, or exactly the output tensor of an
+earlier projection.
 """
 
 import ctypes
@@ -26,25 +28,27 @@ from .qlinear import Tiled
 
 _FMTS = {"w8a16": _lib.FMT_W8A16, "w4a16": _lib.FMT_W4A16, "fp8": _lib.FMT_FP8}
 
-#: Sleeps (about 50 ns each) a workgroup waits for the previous projection before giving up
-#: and flagging the run as failed; far above any real projection's time.
-SPIN_LIMIT = 1 << 20
+#: Microseconds a run may wait in total before its waits give up and flag it as failed; far
+#: above any real chain's time.
+BUDGET_US = 2_000_000
 
 
 class DecodeStack:
     """An ordered chain of projections of one format, for m = 1..16 tokens."""
 
-    def __init__(self, fmt, m, groups_per_cu=2):
+    def __init__(self, fmt, m, waves=8, groups_per_cu=1):
         if fmt not in _FMTS:
             raise ValueError(f"the decode executor serves {sorted(_FMTS)}, not {fmt!r}")
         if not 1 <= m <= 16:
             raise ValueError(f"the decode executor serves m = 1..16 (got {m})")
-        self.fmt, self.m, self.groups_per_cu = fmt, m, groups_per_cu
+        self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
         self.calls, self._keep = [], []
         self.desc = None
+        self.epoch = 0
 
-    def add(self, weight, x, y, swiglu=False):
-        """Append y = x @ W^T (or the SwiGLU of [gate; up] rows) to the chain."""
+    def add(self, weight, x, y, swiglu=False, kw=0):
+        """Append y = x @ W^T (or the SwiGLU of [gate; up] rows) to the chain. ``kw`` forces
+        the waves per 16-row tile (1, 2, 4, 8; 0 lets the planner choose)."""
         if not isinstance(weight, Tiled) or weight.fmt != self.fmt:
             raise ValueError(f"the chain takes {self.fmt} weights in tile layout (qlinear.prepare)")
         _lib.require_device(weight.weight, weight.scale, x, y)
@@ -56,7 +60,7 @@ class DecodeStack:
                              f"{tuple(x.shape)} and {tuple(y.shape)}")
         self.calls.append(_lib.StackCall(weight.weight.data_ptr(), weight.scale.data_ptr(), x.data_ptr(),
                                          y.data_ptr(), weight.rows, weight.k,
-                                         _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, 0))
+                                         _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, int(kw)))
         self._keep += [weight, x, y]
         self.desc = None
         return self
@@ -69,44 +73,42 @@ class DecodeStack:
         lib = _lib.lib()
         arr = (_lib.StackCall * len(self.calls))(*self.calls)
         fmt = _FMTS[self.fmt]
-        ws, tk = ctypes.c_longlong(0), ctypes.c_int(0)
-        grid, lds = ctypes.c_int(0), ctypes.c_int(0)
+        arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.groups_per_cu, None, None, None,
-                                           None, ws, tk, grid, lds), "qlx_stack_build")
-            self.workspace = torch.empty(max(ws.value, 1), dtype=torch.float32, device=device)
-            self.tickets = torch.zeros(max(tk.value, 1), dtype=torch.int32, device=device)
-            self.sync = torch.zeros(4, dtype=torch.int32, device=device)
-            size = lib.qlx_stack_desc_size()
-            host = torch.empty(size * len(self.calls), dtype=torch.uint8)
+            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.waves, self.groups_per_cu, None,
+                                           None, None, arena_bytes, launch), "qlx_stack_build")
+            self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
+            self.error = torch.zeros(1, dtype=torch.int32, device=device)
+            host = torch.empty(lib.qlx_stack_desc_size() * len(self.calls), dtype=torch.uint8)
             plans = (_lib.Plan * len(self.calls))()
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.groups_per_cu,
-                                           ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.workspace),
-                                           _lib.ptr(self.tickets), ws, tk, grid, lds), "qlx_stack_build")
+            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.waves, self.groups_per_cu,
+                                           ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.arena),
+                                           arena_bytes, launch), "qlx_stack_build")
             self.desc = host.to(device)
-        #: (waves, kw, rw, splits) per projection: qlinear's linears with this config give the same bits
+        #: (waves, kw, rw, most K pieces of one row block) per projection
         self.configs = [(p.waves, p.kw, p.rw, p.splits) for p in plans]
-        self.grid, self.lds = grid.value, lds.value
+        self.launch = launch
+        self.grid, self.lds = launch.grid, launch.lds_bytes
         self.device = device
+        self.epoch = 0
         return self
 
-    def run(self, spin_limit=SPIN_LIMIT):
+    def run(self, budget_us=BUDGET_US):
         """Run the whole chain once on the current stream."""
         if self.desc is None:
             self.build()
-        _lib.call("qlx_stack_run", _FMTS[self.fmt], _lib.ptr(self.desc), len(self.calls), self.grid, self.lds,
-                  _lib.ptr(self.sync), int(spin_limit), _lib.stream(self.device))
+        self.epoch = self.epoch % 0xFFFFFFFF + 1  # nonzero, new every run
+        _lib.call("qlx_stack_run", _FMTS[self.fmt], _lib.ptr(self.desc), len(self.calls), ctypes.byref(self.launch),
+                  self.epoch, _lib.ptr(self.error), int(budget_us), _lib.stream(self.device))
 
     def failed(self):
-        """True if a wait of any run so far gave up (outputs of that run are undefined).
+        """True if a wait of any run so far gave up (that run's outputs are undefined).
         Synchronizes with the device."""
-        return bool(self.sync[2].item())
+        return bool(self.error.item())
 
     def reset(self):
-        """Clear the error flag and the split-K tickets (a run whose wait gave up may leave
-        tickets counted; a normal run leaves everything zero)."""
-        self.sync.zero_()
-        self.tickets.zero_()
+        """Clear the error flag (nothing else outlives a failed run)."""
+        self.error.zero_()
 
     def bytes_moved(self):
         return sum(w.bytes_moved() for w in self._keep[0::3])

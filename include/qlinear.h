@@ -200,38 +200,54 @@ int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, 
 /* ---- decode-step executor ----------------------------------------------------------- */
 
 /* One projection of a decode step: y = x @ deq(w)^T on tiled weights (qlx_tile_rows layout),
- * mode QLX_MODE_BF16 or QLX_MODE_SWIGLU. x may be the y of an earlier projection. */
+ * mode QLX_MODE_BF16 or QLX_MODE_SWIGLU. x is either memory that no projection of the chain
+ * writes, or exactly the y of an earlier projection (then it is read as that projection
+ * produces it). kw: waves sharing one 16-row tile (1, 2, 4 or 8), or 0 for the planner. */
 typedef struct qlx_stack_call {
   const void* w;
   const void* w_scale;
   const void* x;
   void* y;
-  int n, k, mode, pad;
+  int n, k, mode, kw;
 } qlx_stack_call;
 
 /* Bytes of one device descriptor written by qlx_stack_build. */
 int qlx_stack_desc_size(void);
 
-/* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
- * for the executor, with `groups_per_cu` resident workgroups per CU (1..4). Writes the
- * descriptors to host memory `desc` (ncalls * qlx_stack_desc_size() bytes; NULL to only size)
- * and, if `plans` is not NULL, each projection's plan (a qlx_linear_* call with that plan gives
- * the same bits), and reports the split-K workspace (fp32 floats) and ticket counters (int32, zeroed once) the
- * descriptors must point at, the grid and the dynamic LDS per workgroup. The descriptors hold
- * `workspace` and `tickets` as given: call once with NULLs to size them, then again.
- * Replaces the reference's per-projection launches chained by programmatic dependent launch
- * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
- * engine/kernels/cuda_jit.py:218-262): here the whole chain is one cooperative launch. */
-int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int groups_per_cu, void* desc,
-                    qlx_plan* plans, float* workspace, int* tickets, long long* workspace_floats,
-                    int* tickets_needed, int* grid, int* lds_bytes);
+/* Launch configuration of a chain, filled by qlx_stack_build, passed to qlx_stack_run. */
+typedef struct qlx_stack_launch {
+  int grid;      /* workgroups (all resident: cooperative launch) */
+  int lds_bytes; /* dynamic LDS per workgroup */
+  int waves;     /* waves per workgroup */
+  int desc_lds;  /* byte offset of the descriptors' LDS copy, or -1 (read from memory) */
+  int lanes;     /* workgroup sets: lane l runs projections l, l + lanes, ... */
+  int pad;
+} qlx_stack_launch;
 
-/* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors, `sync` three
- * int32 in device memory (zero before the first run; each run leaves [0] and [1] zero and sets
- * [2] to 1 if any wait gave up after `spin_limit` sleeps, which makes that run's outputs
- * undefined). Runs that share `sync`, the workspace or the tickets must not overlap. */
-int qlx_stack_run(int fmt, const void* desc, int ncalls, int grid, int lds_bytes, int* sync, int spin_limit,
-                  void* stream);
+/* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
+ * for the executor: workgroups of `waves` (4 or 8) waves, `groups_per_cu` lanes of one
+ * workgroup per CU (1..4; fewer if registers or LDS do not allow), lane l running projections
+ * l, l + lanes, ... concurrently with the other lanes. Writes the
+ * descriptors to host memory `desc` (ncalls * qlx_stack_desc_size() bytes; NULL to only size)
+ * and, if `plans` is not NULL, each projection's plan (waves, kw; splits = the most K pieces
+ * of one row block). The chain keeps published outputs and partial sums in `arena`
+ * (*arena_bytes of device memory, zeroed once before the first run): call once with desc and
+ * arena NULL to size it, then again with both. Outputs must not overlap each other or an
+ * input read from memory (EINVAL otherwise). Replaces the reference's per-projection launches
+ * chained by programmatic dependent launch inside a captured graph
+ * (engine/kernels/cuda_fp8.py:47-50, 150-169; engine/kernels/cuda_jit.py:218-262): here the
+ * whole chain is one cooperative launch. */
+int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
+                    void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch);
+
+/* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors and `launch` its
+ * launch configuration. `epoch` must be
+ * nonzero and differ from the previous run's on the same arena (a counter). `error` is one
+ * int32 in device memory, set to 1 if a wait inside the run passed `budget_us` microseconds
+ * from the run's start; that run's outputs are then undefined. Runs sharing an arena must not
+ * overlap. */
+int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
+                  int* error, long long budget_us, void* stream);
 
 /* ---- measurement ------------------------------------------------------------------- */
 

@@ -114,22 +114,43 @@ def test_oracle_is_not_imported_by_the_product():
 
 
 def test_decode_stack_contract_on_host():
-    """The executor rejects unsupported formats, batch sizes and empty chains before any
-    device work."""
+    """The executor rejects unsupported formats, batch sizes, shapes, overlapping outputs and
+    empty chains before any device work."""
     from kernels import _lib
     from kernels.decode_stack import DecodeStack
     import ctypes
     lib = _lib.lib()
     assert lib.qlx_stack_desc_size() >= 128
-    call = (_lib.StackCall * 1)()
-    out = [ctypes.c_longlong(0), ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)]
-    for fmt, m, n, gpc in ((_lib.FMT_REF8, 1, 1, 1), (_lib.FMT_W4A16, 17, 1, 1), (_lib.FMT_W4A16, 1, 0, 1),
-                           (_lib.FMT_FP8, 1, 1, 5)):
-        rc = lib.qlx_stack_build(fmt, m, call, n, gpc, None, None, None, None, *out)
-        assert rc == _lib.QLX_EINVAL, (fmt, m, n, gpc)
+    out = [ctypes.c_longlong(0), ctypes.byref(_lib.StackLaunch())]
+
+    def build(fmt, m, calls, gpc=1, waves=8):
+        arr = (_lib.StackCall * max(len(calls), 1))(*calls)
+        return lib.qlx_stack_build(fmt, m, arr, len(calls), waves, gpc, None, None, None, *out)
+
+    ok = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 0)
+    assert build(_lib.FMT_REF8, 1, [ok]) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_W4A16, 17, [ok]) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_W4A16, 1, []) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_FP8, 1, [ok], gpc=5) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_FP8, 1, [ok], waves=6) == _lib.QLX_EINVAL
+    bad_k = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 500, _lib.MODE_BF16, 0)
+    assert build(_lib.FMT_W8A16, 1, [bad_k]) == _lib.QLX_EINVAL
+    bad_kw = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 3)
+    assert build(_lib.FMT_W8A16, 1, [bad_kw]) == _lib.QLX_EINVAL
+    # two outputs in the same bytes; an input overlapping a later output
+    a = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 0)
+    b = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, (1 << 23) + 64, 256, 512, _lib.MODE_BF16, 0)
+    assert build(_lib.FMT_W8A16, 1, [a, b]) == _lib.QLX_EINVAL and "overlap" in _lib.last_error()
+    c = _lib.StackCall(1 << 20, 1 << 21, (1 << 23) + 16, 1 << 24, 256, 512, _lib.MODE_BF16, 0)
+    assert build(_lib.FMT_W8A16, 1, [a, c]) == _lib.QLX_EINVAL and "writes" in _lib.last_error()
     for fmt, m in (("int8", 1), ("w4a16", 0), ("fp8", 17)):
         with pytest.raises(ValueError):
             DecodeStack(fmt, m)
     with pytest.raises(ValueError):
         DecodeStack("w8a16", 1).build()
-    assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, 1, 0, None, 1, None) == _lib.QLX_EINVAL
+    launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0)
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, launch, 1, None, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, 0, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0)  # descriptor copy past the LDS
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
