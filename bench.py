@@ -4,8 +4,14 @@
 One step is the quantized linear stream of one decode step at batch M: 36 layers x
 (qkv 2560->6144, o 4096->2560, gate_up 2560->2x9728 with the fused SwiGLU epilogue,
 down 9728->2560) plus the lm_head 2560->151936, each layer with its own synthetic
-weights (4.03 GB in FP8, so the 256 MB Infinity Cache cannot serve repeats). The step is
-captured once in a HIP graph and replayed; activations are resident in HBM.
+weights (4.03 GB in FP8, so the 256 MB Infinity Cache cannot serve repeats). The
+projections form one dependent chain, as in a decode step: each layer's qkv reads the
+previous layer's down output, o reads the query part (first 4096 columns) of qkv's output
+(standing in for attention), gate_up reads o's output, down reads gate_up's, and the
+lm_head reads the last down output. Activations are resident in HBM.
+
+Two product paths run the chain: the single-call linears captured once in a HIP graph and
+replayed, and the decode-step executor (one cooperative launch for the whole chain).
 
 Prints one JSON line (the driver's contract). ``value`` is microseconds per step for
 the default workload, FP8 e4m3 W8A8 at M=1.
@@ -35,10 +41,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def profiled_traffic(fmt, m):
+def profiled_traffic(fmt, m, kernel="gate_up_swiglu"):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, calibrated; see its header for the commands), or None."""
-    path = os.path.join(ROOT, "profiles", f"{fmt}_gate_up_swiglu_m{m}_hbm_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"{fmt}_{kernel}_m{m}_hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
@@ -75,9 +81,40 @@ class Stack:
         return qlinear.prepare(packed, self.fmt)  # load-time relayout into MI355X tiles
 
     def run(self, which=None):
+        """``which`` = None: the whole chain, each projection reading its producer's output.
+        A projection name: every instance of it, on resident inputs (per-projection timing)."""
+        if which is not None:
+            for name, packed, k, sw in self.calls:
+                if name == which:
+                    self.linear(self.x[k], packed, swiglu=sw)
+            return
+        h = self.x[2560]
         for name, packed, k, sw in self.calls:
-            if which is None or name == which:
-                self.linear(self.x[k], packed, swiglu=sw)
+            if name == "qkv":
+                q = self.linear(h, packed)
+            elif name == "o":
+                q = self.linear(q[:, :4096].contiguous(), packed)
+            elif name == "gate_up":
+                q = self.linear(q, packed, swiglu=True)
+            else:  # down, lm_head
+                q = h = self.linear(h if name == "lm_head" else q, packed)
+
+    def executor(self, waves=8, lanes=1):
+        """The same chain as one decode-step executor launch (outputs preallocated)."""
+        from kernels.decode_stack import DecodeStack
+        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes)
+        self.outs = []
+        h = self.x[2560]
+        q = None
+        for name, packed, k, sw in self.calls:
+            y = torch.empty((self.m, packed.rows // 2 if sw else packed.rows), dtype=torch.bfloat16, device="cuda")
+            x = {"qkv": h, "o": None if q is None else q[:, :4096], "gate_up": q, "down": q, "lm_head": h}[name]
+            chain.add(packed, x, y, swiglu=sw)
+            self.outs.append(y)
+            q = y
+            if name == "down":
+                h = y
+        return chain.build()
 
     def bytes_alg(self, which=None):
         """Algorithmic bytes: weight codes + scales + M*K*2 (x in) + M*N_out*2 (y out)."""
@@ -195,15 +232,43 @@ def cpu_baseline(stack, reps=3):
     }
 
 
+def time_fn(fn, reps, warmup, trials=5):
+    """Median over trials of ms per call, `reps` calls between events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    res = []
+    for _ in range(trials):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        res.append(start.elapsed_time(end) / reps)
+    return statistics.median(res)
+
+
 def measure_stack(fmt, m, steps, warmup, breakdown=True):
     stack = Stack(fmt, m)
     g = graph_of(stack.run)
-    ms = median_graph_ms(g, steps, warmup)
-    out = {
+    ms_graph = median_graph_ms(g, steps, warmup)
+    del g
+    out = {"graph_us": ms_graph * 1e3}
+    if m <= 16:
+        chain = stack.executor()
+        ms_exec = time_fn(chain.run, steps, warmup)
+        if chain.failed():
+            raise RuntimeError("decode executor: a wait gave up")
+        out.update(executor_us=ms_exec * 1e3, executor_grid=chain.grid, executor_lds=chain.lds)
+        del chain
+    ms = min(ms_graph, out.get("executor_us", 1e30) / 1e3)
+    out["path"] = "executor" if ms < ms_graph else "graph"
+    out.update({
         "us": ms * 1e3,
         "weight_GB": stack.weight_bytes() / 1e9,
         "alg_GB": stack.bytes_alg() / 1e9,
-    }
+    })
     out["effective_weight_GBps"] = stack.weight_bytes() / (ms * 1e-3) / 1e9
     out["alg_GBps"] = stack.bytes_alg() / (ms * 1e-3) / 1e9
     out["hbm_frac"] = out["alg_GBps"] * 1e9 / PEAK_HBM
@@ -219,7 +284,6 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
                          "GBps": round(b / (t * 1e-3) / 1e9, 1)}
             del gp
         out["per_projection"] = per
-    del g
     return stack, out
 
 
@@ -245,24 +309,34 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
-    log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step, "
+    log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
+        f"executor {head.get('executor_us', float('nan')):.1f}), "
         f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
 
-    # Roofline of the dominant kernel: the fused gate_up+SwiGLU projection (the largest
-    # share of the step's bytes), averaged over its 36 launches in one graph.
-    dom = head.get("per_projection", {}).get("gate_up")
-    if dom is None:
-        gp = graph_of(lambda: stack.run("gate_up"))
-        t = median_graph_ms(gp, max(3, args.steps // 2), 2, trials=3) / stack.count("gate_up")
-        b = stack.bytes_alg("gate_up") / stack.count("gate_up")
-        dom = {"us": t * 1e3, "alg_MB": b / 1e6, "GBps": b / (t * 1e-3) / 1e9}
-    roofline = {
-        "bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-        "frac": round(dom["GBps"] * 1e9 / PEAK_HBM, 4), "traffic": profiled_traffic(args.workload, args.m),
-        "kernel": f"gemm_kernel<{ {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload] }, ..., SwiGLU> "
-                  f"(gate_up 2560->2x9728, M={args.m})",
-        "us_per_launch": round(dom["us"], 2), "alg_MB_per_launch": round(dom["alg_MB"], 3),
-    }
+    fmt_name = {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload]
+    if head["path"] == "executor":
+        # The whole step is one launch of the executor: its algorithmic bytes over its time.
+        roofline = {
+            "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(head["hbm_frac"], 4), "traffic": profiled_traffic(args.workload, args.m, "stack"),
+            "kernel": f"stack_kernel<{fmt_name}, 8, true> (the whole chain, M={args.m})",
+            "us_per_launch": round(head["us"], 2), "alg_MB_per_launch": round(head["alg_GB"] * 1e3, 3),
+        }
+    else:
+        # The fused gate_up+SwiGLU projection (the largest share of the step's bytes),
+        # averaged over its 36 launches in one graph.
+        dom = head.get("per_projection", {}).get("gate_up")
+        if dom is None:
+            gp = graph_of(lambda: stack.run("gate_up"))
+            t = median_graph_ms(gp, max(3, args.steps // 2), 2, trials=3) / stack.count("gate_up")
+            b = stack.bytes_alg("gate_up") / stack.count("gate_up")
+            dom = {"us": t * 1e3, "alg_MB": b / 1e6, "GBps": b / (t * 1e-3) / 1e9}
+        roofline = {
+            "bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(dom["GBps"] * 1e9 / PEAK_HBM, 4), "traffic": profiled_traffic(args.workload, args.m),
+            "kernel": f"gemm_kernel<{fmt_name}, ..., SwiGLU> (gate_up 2560->2x9728, M={args.m})",
+            "us_per_launch": round(dom["us"], 2), "alg_MB_per_launch": round(dom["alg_MB"], 3),
+        }
 
     extra = {}
     # the stream read also calibrates rocprofv3's FETCH_SIZE (a known byte count)
@@ -278,7 +352,8 @@ def main():
             if (fmt, m) == (args.workload, args.m):
                 continue
             st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=False)
-            extra[f"{fmt}_M{m}_stack"] = {k: round(v, 4 if k == "hbm_frac" else 2) for k, v in res.items()}
+            extra[f"{fmt}_M{m}_stack"] = {k: (round(v, 4 if k == "hbm_frac" else 2) if isinstance(v, float) else v)
+                                          for k, v in res.items()}
             log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s")
             del st
             torch.cuda.empty_cache()
@@ -298,10 +373,13 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) activations)",
         "config": {
             "workload": f"Qwen3-4B decode-step linear stack, {args.workload}, 36 layers x "
-                        f"(qkv, o, gate_up+SwiGLU, down) + lm_head",
+                        f"(qkv, o, gate_up+SwiGLU, down) + lm_head, one dependent chain",
             "m": args.m, "hidden": 2560, "intermediate": 9728, "vocab": 151936, "layers": LAYERS,
             "weight_GB": round(head["weight_GB"], 4), "alg_GB": round(head["alg_GB"], 4),
+            "path": head["path"],
         },
+        "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
+                     "executor": round(head["executor_us"], 2) if "executor_us" in head else None},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),
         "roofline": roofline,

@@ -48,6 +48,9 @@ struct alignas(16) StackDesc {
   int pe;           // workgroups with work: min(P, units)
   int gran;         // block-steps per unit
   int sw;           // SwiGLU epilogue
+  int xpitch;       // words per token row of xwire (the producer's n_out / 2)
+  int off_red;      // LDS byte offset of the waves' partial sums (apart from the staged x)
+  int pad[2];
 };
 
 // ---- shares of a projection ---------------------------------------------------------
@@ -108,24 +111,124 @@ __device__ __forceinline__ uint32_t ll_settle(const uint64_t* p, uint64_t v, con
   return (uint32_t)v;
 }
 
-// Activation published by an earlier projection: [m][k/2] words of bf16 pairs.
+// Activation published by an earlier projection: bf16 pairs, `pitch` words per token row
+// (the activation may be the first k columns of a wider output).
 struct XWire {
   const uint64_t* wire;
+  int pitch;
   Waits w;
   struct Raw {
     uint64_t v[4];
   };
-  __device__ __forceinline__ void fetch(const GemmArgs& a, int mm, int kabs, Raw& r) const {
-    const uint64_t* p = wire + (size_t)mm * (a.k >> 1) + (kabs >> 1);
+  __device__ __forceinline__ void fetch(const GemmArgs&, int mm, int kabs, Raw& r) const {
+    const uint64_t* p = wire + (size_t)mm * pitch + (kabs >> 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.v[i] = ll_load(p + i);
   }
-  __device__ __forceinline__ uint4 settle(const GemmArgs& a, int mm, int kabs, const Raw& r) const {
-    const uint64_t* p = wire + (size_t)mm * (a.k >> 1) + (kabs >> 1);
+  __device__ __forceinline__ uint4 settle(const GemmArgs&, int mm, int kabs, const Raw& r) const {
+    const uint64_t* p = wire + (size_t)mm * pitch + (kabs >> 1);
     return uint4{ll_settle(p, r.v[0], w), ll_settle(p + 1, r.v[1], w), ll_settle(p + 2, r.v[2], w),
                  ll_settle(p + 3, r.v[3], w)};
   }
 };
+
+// ---- work items --------------------------------------------------------------------------
+
+// Weight steps in flight per wave: most workgroups' whole share of a decode projection
+// (fewer for 4-bit weights, whose dequantization needs more registers).
+template <class F>
+struct ExecDepth {
+  static constexpr int PF = 8;
+};
+template <>
+struct ExecDepth<FmtW4> {
+  static constexpr int PF = 4;
+};
+
+// Per-wave state of one executor work item: row block tg, steps [step0, step0 + nst), K
+// piece s of np; the wave streams tile row wrow at steps step0 + kwi + j * kw, j < my, the
+// last being `last`; plus the item's per-row scale for formats with one scale per row.
+struct ExecItem {
+  int tg, s, np, step0, nst, wt, kwi, my, last, wrow;
+  float sc;
+};
+
+// Issue the wave's first ExecDepth<F>::PF weight steps (and the per-row scale) of a work
+// item. A wave without steps in the item (my == 0) loads nothing.
+template <class F>
+__device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
+                                              ExecItem& it, uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  it.tg = tg;
+  it.s = s;
+  it.np = np;
+  it.step0 = step0;
+  it.nst = nst;
+  it.wt = wave / a.kw;
+  it.kwi = wave - it.wt * a.kw;
+  const int tile0 = tg * a.rt + it.wt;
+  const bool active = tile0 < a.ntiles;
+  it.wrow = active ? weight_row(a, tile0, lane & 15) : 0;
+  it.my = active ? (nst - it.kwi + a.kw - 1) / a.kw : 0;  // this wave's steps: kwi, kwi + kw, ...
+  it.last = step0 + it.kwi + (it.my - 1) * a.kw;
+  // The scale first: memory counters complete in order, so reading it then waits for no
+  // weight load.
+  it.sc = 0.f;
+  if constexpr (F::NSC == 0) {
+    const int rl = threadIdx.x, tile = tg * a.rt + (rl >> 4);
+    if (rl < 16 * a.rt && tile < a.ntiles) it.sc = F::scale(a, weight_row(a, tile, rl & 15), 0, 0);
+  }
+#pragma unroll
+  for (int p = 0; p < ExecDepth<F>::PF; ++p)
+    if (p < it.my) load_chunk<F>(buf[p], a, it.wrow, step0 + it.kwi + p * a.kw, lane);
+}
+
+// Stage what the item needs in LDS and stream its weight steps through the MFMAs. With
+// `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
+// projection, same steps -- is still in place.
+template <class F, int WAVES, class XS>
+__device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
+                                          uint4 (&buf)[ExecDepth<F>::PF][F::LOADS], f32x4 (&acc)[1][1]) {
+  constexpr int PF = ExecDepth<F>::PF;
+  const int lane = threadIdx.x & 63;
+  const int step0 = it.step0, nst = it.nst, kwi = it.kwi, my = it.my;
+  if (!reuse) {
+    if constexpr (std::is_same<F, FmtFP8>::value)
+      stage_fp8_act(a, xs, lds, step0, nst);
+    else
+      stage_bf16<F>(a, xs, lds, step0, nst);
+  }
+  if constexpr (F::NSC == 0) {
+    if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = it.sc;
+  } else {
+    stage_scales<F>(a, lds, it.tg, step0, nst);
+  }
+  __syncthreads();
+  if constexpr (F::BIAS != 0.f) {
+    if (!reuse) {
+      stage_bias<F, WAVES>(a, lds, nst);
+      __syncthreads();
+    }
+  }
+  acc[0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int xoff[1], mrow[1];
+  mrow[0] = min(lane & 15, a.m - 1);
+  xoff[0] = mrow[0] * a.xstride;
+  const int rowl = it.wt * 16 + 4 * (lane >> 4);
+  int j0 = 0;
+  for (; j0 + PF <= my; j0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      F::template compute<1>(acc[0], buf[p], lds, a, kwi + (j0 + p) * a.kw, lane, xoff, mrow, rowl);
+      const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, it.last);
+      load_chunk<F>(buf[p], a, it.wrow, nxt, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (j0 + p < my) F::template compute<1>(acc[0], buf[p], lds, a, kwi + (j0 + p) * a.kw, lane, xoff, mrow, rowl);
+}
 
 // ---- epilogue ----------------------------------------------------------------------------
 
@@ -133,10 +236,11 @@ struct XWire {
 // partial sums (piece > 0), or add the other pieces' partials in piece order and write
 // (piece 0). Outputs go to y and, when a later projection reads them, to ywire.
 template <class F, bool SW>
-__device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const Item<1>& it,
+__device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const ExecItem& it,
                                             const f32x4 (&acc)[1][1], const Waits& w) {
   const GemmArgs& a = d.a;
-  acc_to_lds<1, 1>(lds, acc);
+  char* red = lds + d.off_red;
+  acc_to_lds<1, 1>(red, acc);
   constexpr int NV = SW ? 4 : 2;  // values per output pair: (g0, g1, u0, u1) or (v0, v1)
   constexpr int rows_out = SW ? 8 : 16;
   const int per_tile = (rows_out / 2) * a.m;
@@ -156,15 +260,15 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
       row[1] = row[0] + 1;
       row[2] = a.half + row[0];
       row[3] = row[2] + 1;
-      v[0] = tile_value<F, 1, 1>(a, lds, tl, nl, mm);
-      v[1] = tile_value<F, 1, 1>(a, lds, tl, nl + 1, mm);
-      v[2] = tile_value<F, 1, 1>(a, lds, tl, nl + 8, mm);
-      v[3] = tile_value<F, 1, 1>(a, lds, tl, nl + 9, mm);
+      v[0] = tile_value<F, 1, 1>(a, red, lds, tl, nl, mm);
+      v[1] = tile_value<F, 1, 1>(a, red, lds, tl, nl + 1, mm);
+      v[2] = tile_value<F, 1, 1>(a, red, lds, tl, nl + 8, mm);
+      v[3] = tile_value<F, 1, 1>(a, red, lds, tl, nl + 9, mm);
     } else {
       row[0] = 16 * tile + nl;
       row[1] = row[0] + 1;
-      v[0] = tile_value<F, 1, 1>(a, lds, tl, nl, mm);
-      v[1] = tile_value<F, 1, 1>(a, lds, tl, nl + 1, mm);
+      v[0] = tile_value<F, 1, 1>(a, red, lds, tl, nl, mm);
+      v[1] = tile_value<F, 1, 1>(a, red, lds, tl, nl + 1, mm);
     }
     if (np > 1) {
       if (piece > 0) {
@@ -227,11 +331,11 @@ __device__ __forceinline__ bool next_work(const StackDesc* calls, int ncalls, in
 }
 
 template <class F>
-__device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, Item<1>& it,
-                                              uint4 (&buf)[PipeDepth<1>::PF][1][F::LOADS]) {
+__device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, ExecItem& it,
+                                              uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
   int step0, nst, piece, np;
   share_item(p, g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
-  item_prefetch_range<F, 1>(d.a, g, step0, nst, piece, np, it, buf);
+  exec_prefetch<F>(d.a, g, step0, nst, piece, np, it, buf);
 }
 
 template <class F, int WAVES, bool DLDS>
@@ -251,36 +355,33 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     __syncthreads();
     calls = reinterpret_cast<const StackDesc*>(lds + desc_off);
   }
-  Item<1> cur, nxt;
-  uint4 buf[PipeDepth<1>::PF][1][F::LOADS];
+  ExecItem cur, nxt;
+  uint4 buf[ExecDepth<F>::PF][F::LOADS];
   f32x4 acc[1][1];
   int nc = -1, ng = 0;
+  int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
   if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
   while (have) {
     const int c = nc;
     const StackDesc& d = calls[c];
     cur = nxt;
+    const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire)
-      item_main<F, 1, 1, WAVES>(d.a, XWire{d.xwire, w}, lds, cur, buf, acc);
+      exec_main<F, WAVES>(d.a, XWire{d.xwire, d.xpitch, w}, lds, cur, reuse, buf, acc);
     else
-      item_main<F, 1, 1, WAVES>(d.a, XPlain{}, lds, cur, buf, acc);
-    // The next item's weights stream during the epilogue -- except when the epilogue waits
-    // for other pieces: its loads would then also wait for the prefetch (memory counters
-    // complete in order), so the reducer prefetches afterwards.
-    const bool reducer = cur.np > 1 && cur.s == 0;
-    if (!reducer) {
-      have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-      if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
-    }
+      exec_main<F, WAVES>(d.a, XPlain{}, lds, cur, reuse, buf, acc);
+    staged_c = c;
+    staged_step0 = cur.step0;
+    staged_nst = cur.nst;
+    // Outputs first: later projections wait for them, and issuing the next item's loads
+    // can stall on a full memory pipeline (a reducer's loads would also wait behind them).
     if (d.sw)
       exec_finish<F, true>(d, lds, cur, acc, w);
     else
       exec_finish<F, false>(d, lds, cur, acc, w);
-    if (reducer) {
-      have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-      if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
-    }
+    have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
+    if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
     __syncthreads();  // LDS is reused by the next item
   }
 }
@@ -313,6 +414,13 @@ FmtInfo stack_info(int fmt) {
 
 // ---- planning (host) -------------------------------------------------------------------
 
+// LDS of one executor item: the single-call layout plus the waves' partial sums kept apart
+// from the staged activation (which later items of the same projection reuse).
+int exec_lds(const FmtInfo& fi, const qlx_plan& p, int m, int n, int k, GemmArgs& a) {
+  const int base = (layout(fi, p, m, n, k, a) + 15) & ~15;
+  return base + p.waves * 16 * 16 * 4;  // [wave][16 rows][16 tokens] floats (rw = 1, mt = 1)
+}
+
 struct StackPlan {
   qlx_plan plan;
   int units, pe, gran, sps, max_np;
@@ -340,13 +448,15 @@ int check_shares(int groups, int ns, int U, int pe, int gran, int sps) {
   return max_np;
 }
 
-// kw (so rt = 8 / kw tiles per row block) and the unit size (one block-step, or one whole
-// row block). Cost, in bytes of the busiest workgroup: its weight bytes (a tile step is 2 KB
-// in every executor format), a fixed charge per item, and one extra dependency trip when
-// row blocks are cut into pieces.
+// kw (so rt = waves / kw tiles per row block) and the unit size (one block-step, or one
+// whole row block). Cost, in bytes of the busiest workgroup: its weight bytes (a tile step is
+// 2 KB in every executor format), a fixed charge per item, and one extra dependency trip
+// when row blocks are cut into pieces.
 bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, int waves, int force_kw,
                      StackPlan& out) {
-  constexpr double kStepBytes = 2048.0, kItemBytes = 16384.0, kPieceBytes = 49152.0;
+  // An item costs about one memory round trip more than its bytes (staging, epilogue), and a
+  // cut row block one more dependency trip: ~4 us, ~128 KB of one workgroup's stream.
+  constexpr double kStepBytes = 2048.0, kItemBytes = 131072.0, kPieceBytes = 98304.0;
   const int ns = k / fi.kstep;
   const int ntiles = n / 16;
   double best = 1e300;
@@ -372,7 +482,7 @@ bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, in
         p.rw = 1;
         p.splits = ns / sps;  // layout() then sizes LDS for ceil(ns / splits) >= sps steps
         GemmArgs a = {};
-        const int lds = layout(fi, p, m, n, k, a);
+        const int lds = exec_lds(fi, p, m, n, k, a);
         if (a.sps < sps || lds > kLdsLimit) continue;
         const int max_np = check_shares(groups, ns, (int)U, pe, gran, sps);
         if (max_np < 1 || max_np > kMaxPieces) continue;
@@ -439,7 +549,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     }
     const long long xbytes = 2LL * m * calls[c].k;
     for (int j = 0; j < ncalls; ++j) {
-      if (calls[c].x == calls[j].y && j < c && nout(j) == calls[c].k) {
+      if (calls[c].x == calls[j].y && j < c && calls[c].k <= nout(j)) {
         src[c] = j;
         published[j] = 1;
         break;
@@ -469,7 +579,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, sp[c]),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
       GemmArgs a = {};
-      const int l = layout(fi, sp[c].plan, m, q.n, q.k, a);
+      const int l = exec_lds(fi, sp[c].plan, m, q.n, q.k, a);
       if (l > items_lds) items_lds = l;
     }
     items_lds = (items_lds + 15) & ~15;
@@ -511,12 +621,13 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     d.a.x = q.x;
     d.a.y = q.y;
     d.a.tiled = 1;
-    layout(fi, sp[c].plan, m, q.n, q.k, d.a);
+    d.off_red = (layout(fi, sp[c].plan, m, q.n, q.k, d.a) + 15) & ~15;
     d.a.splits = sp[c].max_np;
     if (base) {
       d.ywire = wire_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[c]) : nullptr;
       d.part = part_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + part_off[c]) : nullptr;
       d.xwire = src[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[src[c]]) : nullptr;
+      d.xpitch = src[c] >= 0 ? nout(src[c]) / 2 : 0;
     }
     d.units = sp[c].units;
     d.pe = sp[c].pe;

@@ -589,7 +589,24 @@ __device__ void stage_bias(const GemmArgs& a, char* lds, int nst) {
   }
 }
 
-// FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice.
+// e4m3 codes of 8 activation values (bf16 pairs in v) at per-token scale sc, to LDS.
+__device__ __forceinline__ void store_e4m3_chunk(char* dst, uint4 v, float sc) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  uint32_t c[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
+    c[e] = f32_to_e4m3(clamp_keep_nan(xv / sc, 448.f));
+  }
+  uint2 o;
+  o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+  o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  *reinterpret_cast<uint2*>(dst) = o;
+}
+
+// FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice. When
+// one batch of loads covers the rows, the values stay in registers for the codes (one pass
+// over x); otherwise the slice is read again.
 template <class XS>
 __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst) {
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
@@ -598,6 +615,8 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
   __syncthreads();
   const int cpr = a.k >> 3;
   const int total = a.m * cpr;
+  const bool one_pass = total <= kStageUnroll * (int)blockDim.x;
+  uint4 kept[kStageUnroll];
   for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
     typename XS::Raw r[kStageUnroll];
 #pragma unroll
@@ -610,6 +629,7 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
       const int q = q0 + u * blockDim.x;
       if (q < total) {
         const uint4 v = xs.settle(a, q / cpr, (q % cpr) * 8, r[u]);
+        kept[u] = v;
         const uint32_t d[4] = {v.x, v.y, v.z, v.w};
         float mx = 0.f;
 #pragma unroll
@@ -621,6 +641,18 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
   __syncthreads();
   for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = fmaxf(__uint_as_float(amax[i]) / 448.f, 1e-12f);
   __syncthreads();
+  const int c0 = step0 * 16, c1 = c0 + nst * 16;  // the slice's 8-value chunks within a row
+  if (one_pass) {
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int q = threadIdx.x + u * blockDim.x;
+      if (q < total) {
+        const int mm = q / cpr, kc = q - mm * cpr;
+        if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, kept[u], sx[mm]);
+      }
+    }
+    return;
+  }
   const int cps = nst * 16;  // 8-value chunks per row of the slice
   for (int q0 = threadIdx.x; q0 < a.m * cps; q0 += kStageUnroll * blockDim.x) {
     typename XS::Raw r[kStageUnroll];
@@ -634,19 +666,7 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
       const int q = q0 + u * blockDim.x;
       if (q >= a.m * cps) continue;
       const int mm = q / cps, kc = q - mm * cps;
-      const uint4 v = xs.settle(a, mm, step0 * 128 + kc * 8, r[u]);
-      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-      const float sc = sx[mm];
-      uint32_t c[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
-        c[e] = f32_to_e4m3(clamp_keep_nan(xv / sc, 448.f));
-      }
-      uint2 o;
-      o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-      *reinterpret_cast<uint2*>(lds + mm * a.xstride + kc * 8) = o;
+      store_e4m3_chunk(lds + mm * a.xstride + kc * 8, xs.settle(a, mm, step0 * 128 + kc * 8, r[u]), sx[mm]);
     }
   }
 }
@@ -867,12 +887,13 @@ __device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT]
   __syncthreads();
 }
 
-// Output (tile tl of the block, tile row nl, token mm): the kw waves' sums added in wave
-// order, then the format's scales.
+// Output (tile tl of the block, tile row nl, token mm): the kw waves' sums (acc_to_lds at
+// `redp`) added in wave order, then the format's scales (staged in `lds`).
 template <class F, int MT, int RW>
-__device__ __forceinline__ float tile_value(const GemmArgs& a, const char* lds, int tl, int nl, int mm) {
+__device__ __forceinline__ float tile_value(const GemmArgs& a, const char* redp, const char* lds, int tl, int nl,
+                                            int mm) {
   constexpr int RC = 16 * MT;
-  const float* red = reinterpret_cast<const float*>(lds);
+  const float* red = reinterpret_cast<const float*>(redp);
   const int slot = tl / RW, r = tl - slot * RW;  // tile tl of the block = slot's r-th tile
   float v = 0.f;
   for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
@@ -887,7 +908,7 @@ __device__ __forceinline__ void item_finish(const GemmArgs& a, char* lds, const 
                                             const f32x4 (&acc)[RW][MT]) {
   const int tg = it.tg, s = it.s, np = it.np;
   acc_to_lds<MT, RW>(lds, acc);
-  auto combined = [&](int tl, int nl, int mm) -> float { return tile_value<F, MT, RW>(a, lds, tl, nl, mm); };
+  auto combined = [&](int tl, int nl, int mm) -> float { return tile_value<F, MT, RW>(a, lds, lds, tl, nl, mm); };
   auto swiglu = [](float g, float u) -> float { return swiglu_bf(g, u); };
 
   // Outputs go out in row pairs (one 32-bit store of two bf16).

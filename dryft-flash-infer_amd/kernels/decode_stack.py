@@ -15,8 +15,8 @@ weights while its input is still being produced, and wait only for the words the
 
 Inputs and outputs are caller-owned bf16 tensors that stay in place between runs (the
 descriptors hold their addresses), like the static buffers of a captured decode graph. An
-input is either memory no projection of the chain writes, or exactly the output tensor of an
-earlier projection.
+input is either memory no projection of the chain writes, or an earlier projection's output
+tensor -- whole, or its first columns (``y_qkv[:, :4096]``, the attention's query part).
 """
 
 import ctypes
@@ -51,7 +51,13 @@ class DecodeStack:
         the waves per 16-row tile (1, 2, 4, 8; 0 lets the planner choose)."""
         if not isinstance(weight, Tiled) or weight.fmt != self.fmt:
             raise ValueError(f"the chain takes {self.fmt} weights in tile layout (qlinear.prepare)")
-        _lib.require_device(weight.weight, weight.scale, x, y)
+        _lib.require_device(weight.weight, weight.scale, y)
+        if x.device.type != "cuda":
+            raise ValueError("quantized linear ops need tensors on a ROCm GPU (no CPU path)")
+        if not x.is_contiguous():  # only the first columns of an earlier output, rows n_out apart
+            earlier = [t for t in self._keep[2::3] if t.data_ptr() == x.data_ptr()]
+            if not earlier or x.stride() != (earlier[0].shape[1], 1):
+                raise ValueError("a strided input must be the first columns of an earlier output of the chain")
         out_n = weight.rows // 2 if swiglu else weight.rows
         if x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16:
             raise ValueError("activations and outputs are bf16")

@@ -201,8 +201,9 @@ int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, 
 
 /* One projection of a decode step: y = x @ deq(w)^T on tiled weights (qlx_tile_rows layout),
  * mode QLX_MODE_BF16 or QLX_MODE_SWIGLU. x is either memory that no projection of the chain
- * writes, or exactly the y of an earlier projection (then it is read as that projection
- * produces it). kw: waves sharing one 16-row tile (1, 2, 4 or 8), or 0 for the planner. */
+ * writes ([m][k], dense), or the y of an earlier projection -- all of it, or its first k
+ * columns (x == that y, rows n_out apart) -- and is then read as that projection produces it.
+ * kw: waves sharing one 16-row tile (1, 2, 4 or 8), or 0 for the planner. */
 typedef struct qlx_stack_call {
   const void* w;
   const void* w_scale;
