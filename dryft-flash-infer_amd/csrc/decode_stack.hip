@@ -98,22 +98,17 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
 __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t v, uint32_t epoch) {
   __hip_atomic_store(gmem(p), ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// The value of a word first read as v: re-read until it carries this run's epoch (bounded).
-__device__ __forceinline__ uint32_t ll_settle(const uint64_t* p, uint64_t v, const Waits& w) {
-  while ((uint32_t)(v >> 32) != w.epoch) {
-    if (__builtin_amdgcn_s_memrealtime() > w.deadline) {
-      __hip_atomic_store(gmem(w.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-    v = ll_load(p);
-  }
-  return (uint32_t)v;
+// True (and the run flagged as failed) once the run's deadline has passed: waits stop there.
+__device__ __forceinline__ bool ll_expired(const Waits& w) {
+  if (__builtin_amdgcn_s_memrealtime() <= w.deadline) return false;
+  __hip_atomic_store(gmem(w.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
 }
 
 // Activation published by an earlier projection: bf16 pairs, `pitch` words per token row
 // (the activation may be the first k columns of a wider output).
 struct XWire {
+  static constexpr bool POLLS = true;
   const uint64_t* wire;
   int pitch;
   Waits w;
@@ -125,10 +120,21 @@ struct XWire {
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.v[i] = ll_load(p + i);
   }
-  __device__ __forceinline__ uint4 settle(const GemmArgs&, int mm, int kabs, const Raw& r) const {
+  __device__ __forceinline__ bool ready(const Raw& r) const {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ok &= (uint32_t)(r.v[i] >> 32) == w.epoch;
+    return ok;
+  }
+  __device__ __forceinline__ void refetch(const GemmArgs&, int mm, int kabs, Raw& r) const {
     const uint64_t* p = wire + (size_t)mm * pitch + (kabs >> 1);
-    return uint4{ll_settle(p, r.v[0], w), ll_settle(p + 1, r.v[1], w), ll_settle(p + 2, r.v[2], w),
-                 ll_settle(p + 3, r.v[3], w)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if ((uint32_t)(r.v[i] >> 32) != w.epoch) r.v[i] = ll_load(p + i);
+  }
+  __device__ __forceinline__ bool expired() const { return ll_expired(w); }
+  __device__ __forceinline__ uint4 value(const Raw& r) const {
+    return uint4{(uint32_t)r.v[0], (uint32_t)r.v[1], (uint32_t)r.v[2], (uint32_t)r.v[3]};
   }
 };
 
@@ -138,7 +144,7 @@ struct XWire {
 // (fewer for 4-bit weights, whose dequantization needs more registers).
 template <class F>
 struct ExecDepth {
-  static constexpr int PF = 8;
+  static constexpr int PF = 6;
 };
 template <>
 struct ExecDepth<FmtW4> {
@@ -285,13 +291,30 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
 #pragma unroll
           for (int i = 0; i < NV; ++i) raw[q - 1][i] = ll_load(part + row[i]);
         }
+      // Re-poll every stale word together until all pieces are in (bounded).
+      while (true) {
+        bool all = true;
+#pragma unroll
+        for (int q = 1; q < kMaxPieces; ++q)
+#pragma unroll
+          for (int i = 0; i < NV; ++i)
+            if (q < np && (uint32_t)(raw[q - 1][i] >> 32) != w.epoch) all = false;
+        if (all || ll_expired(w)) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 1; q < kMaxPieces; ++q)
+          if (q < np) {
+            const uint64_t* part = d.part + ((size_t)(q - 1) * a.m + mm) * a.n;
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+              if ((uint32_t)(raw[q - 1][i] >> 32) != w.epoch) raw[q - 1][i] = ll_load(part + row[i]);
+          }
+      }
 #pragma unroll
       for (int q = 1; q < kMaxPieces; ++q)
-        if (q < np) {
-          const uint64_t* part = d.part + ((size_t)(q - 1) * a.m + mm) * a.n;
+        if (q < np)
 #pragma unroll
-          for (int i = 0; i < NV; ++i) v[i] += __uint_as_float(ll_settle(part + row[i], raw[q - 1][i], w));
-        }
+          for (int i = 0; i < NV; ++i) v[i] += __uint_as_float((uint32_t)raw[q - 1][i]);
     }
     float o0 = v[0], o1 = v[1];
     if constexpr (SW) {

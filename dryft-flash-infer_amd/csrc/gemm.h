@@ -101,9 +101,12 @@ __device__ __forceinline__ void publish_stores() {
 }
 
 // Where a work item's bf16 activation comes from. Staging reads it 8 values (16 bytes) at
-// a time in two phases, fetch (issue the loads) and settle (the values), so a thread can
-// have several chunks in flight. The single-call kernels read x from device memory.
+// a time: fetch issues the loads of a chunk, so a thread has several chunks in flight;
+// sources whose data may not have arrived yet (POLLS) also say whether a fetched chunk is
+// ready and re-fetch its stale parts; value gives the 8 values. The single-call kernels read
+// x from device memory.
 struct XPlain {
+  static constexpr bool POLLS = false;
   struct Raw {
     uint4 v;
   };
@@ -111,8 +114,38 @@ struct XPlain {
     const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k + kabs));
     r.v = uint4{v[0], v[1], v[2], v[3]};
   }
-  __device__ __forceinline__ uint4 settle(const GemmArgs&, int, int, const Raw& r) const { return r.v; }
+  __device__ __forceinline__ bool ready(const Raw&) const { return true; }
+  __device__ __forceinline__ void refetch(const GemmArgs&, int, int, Raw&) const {}
+  __device__ __forceinline__ bool expired() const { return false; }
+  __device__ __forceinline__ uint4 value(const Raw& r) const { return r.v; }
 };
+
+// Settle a batch of fetched chunks of a source whose data may not have arrived: wait for the
+// first chunk alone, then re-fetch every other stale chunk together (when the first is in,
+// the rest usually is: one round trip for all, not one per chunk), then settle each, until
+// ready or the source's deadline has passed. chunk(u, mm, kabs) says whether slot u holds a
+// chunk and where it is.
+template <class XS, int U, class Chunk>
+__device__ __forceinline__ void settle_batch(const GemmArgs& a, const XS& xs, typename XS::Raw (&r)[U], Chunk chunk) {
+  if constexpr (XS::POLLS) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int mm, kabs;
+      if (!chunk(u, mm, kabs)) continue;
+      while (!xs.ready(r[u]) && !xs.expired()) {
+        __builtin_amdgcn_s_sleep(1);
+        xs.refetch(a, mm, kabs, r[u]);
+      }
+      if (u == 0) {
+#pragma unroll
+        for (int v = 1; v < U; ++v) {
+          int mv, kv;
+          if (chunk(v, mv, kv) && !xs.ready(r[v])) xs.refetch(a, mv, kv, r[v]);
+        }
+      }
+    }
+  }
+}
 
 // Two exact small-integer floats -> bf16 pair (the high halves are exact: <= 8 significant bits).
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
@@ -551,22 +584,23 @@ __device__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0
   } else {
     for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
       typename XS::Raw r[kStageUnroll];
+      auto chunk = [&](int u, int& mm, int& kabs) {
+        const int q = q0 + u * blockDim.x;
+        mm = q / cpr;
+        kabs = step0 * F::KSTEP + (q - mm * cpr) * 8;
+        return q < total;
+      };
 #pragma unroll
       for (int u = 0; u < kStageUnroll; ++u) {
-        const int q = q0 + u * blockDim.x;
-        if (q < total) {
-          const int mm = q / cpr, kc = q - mm * cpr;
-          xs.fetch(a, mm, step0 * F::KSTEP + kc * 8, r[u]);
-        }
+        int mm, kabs;
+        if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
       }
+      settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
 #pragma unroll
       for (int u = 0; u < kStageUnroll; ++u) {
-        const int q = q0 + u * blockDim.x;
-        if (q < total) {
-          const int mm = q / cpr, kc = q - mm * cpr;
-          *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) =
-              F::order(xs.settle(a, mm, step0 * F::KSTEP + kc * 8, r[u]));
-        }
+        int mm, kabs;
+        if (chunk(u, mm, kabs))
+          *reinterpret_cast<uint4*>(lds + mm * a.xstride + (kabs - step0 * F::KSTEP) * 2) = F::order(xs.value(r[u]));
       }
     }
   }
@@ -619,16 +653,23 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
   uint4 kept[kStageUnroll];
   for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
     typename XS::Raw r[kStageUnroll];
+    auto chunk = [&](int u, int& mm, int& kabs) {
+      const int q = q0 + u * blockDim.x;
+      mm = q / cpr;
+      kabs = (q - mm * cpr) * 8;
+      return q < total;
+    };
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const int q = q0 + u * blockDim.x;
-      if (q < total) xs.fetch(a, q / cpr, (q % cpr) * 8, r[u]);
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
     }
+    settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
       const int q = q0 + u * blockDim.x;
       if (q < total) {
-        const uint4 v = xs.settle(a, q / cpr, (q % cpr) * 8, r[u]);
+        const uint4 v = xs.value(r[u]);
         kept[u] = v;
         const uint32_t d[4] = {v.x, v.y, v.z, v.w};
         float mx = 0.f;
@@ -656,17 +697,22 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
   const int cps = nst * 16;  // 8-value chunks per row of the slice
   for (int q0 = threadIdx.x; q0 < a.m * cps; q0 += kStageUnroll * blockDim.x) {
     typename XS::Raw r[kStageUnroll];
+    auto chunk = [&](int u, int& mm, int& kabs) {
+      const int q = q0 + u * blockDim.x;
+      mm = q / cps;
+      kabs = step0 * 128 + (q - mm * cps) * 8;
+      return q < a.m * cps;
+    };
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const int q = q0 + u * blockDim.x;
-      if (q < a.m * cps) xs.fetch(a, q / cps, step0 * 128 + (q % cps) * 8, r[u]);
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
     }
+    settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const int q = q0 + u * blockDim.x;
-      if (q >= a.m * cps) continue;
-      const int mm = q / cps, kc = q - mm * cps;
-      store_e4m3_chunk(lds + mm * a.xstride + kc * 8, xs.settle(a, mm, step0 * 128 + kc * 8, r[u]), sx[mm]);
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), sx[mm]);
     }
   }
 }
