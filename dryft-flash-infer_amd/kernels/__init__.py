@@ -2,13 +2,14 @@
 
 Mirrors the module surface of the reference's ``engine/kernels`` package for the
 quantized linear path (engine/kernels/__init__.py:11-75): ``cuda_fp8``, ``fp8``,
-``cuda_int8``, ``cuda_small``, ``swiglu`` and ``norm`` keep their names and signatures,
-and ``qlinear`` adds the north-star formats. Every op runs in the hand-written HIP
+``cuda_int8``, ``cuda_small``, ``swiglu``, ``norm``, ``gemm`` (the per-shape race) and
+``timing`` keep their names and signatures; ``qlinear`` adds the north-star formats and
+``decode_stack`` the one-launch decode-step executor. Every op runs in the hand-written HIP
 library ``libqlinear.so``; there is no CPU or Triton fallback, and ops raise if the
 library is missing or the tensors are not on the GPU.
 """
 
-from . import _lib, cuda_fp8, cuda_int8, cuda_small, fp8, norm, qlinear, swiglu  # noqa: F401
+from . import _lib, cuda_fp8, cuda_int8, cuda_small, fp8, gemm, norm, qlinear, swiglu, timing  # noqa: F401
 from .norm import (  # noqa: F401
     add_rms_norm, add_rms_norm_partials, add_rms_norm_partials_separate, add_rms_norm_separate, rms_norm,
 )
@@ -19,7 +20,7 @@ from .swiglu import swiglu, swiglu_partials  # noqa: F401,E402
 HAVE_TRITON = False  # the reference's flag (kernels/__init__.py:13): these ops never use Triton
 
 __all__ = [
-    "HAVE_TRITON", "cuda_fp8", "fp8", "cuda_int8", "cuda_small", "qlinear", "norm", "swiglu",
+    "HAVE_TRITON", "cuda_fp8", "fp8", "cuda_int8", "cuda_small", "qlinear", "norm", "swiglu", "gemm", "timing",
     "add_rms_norm", "add_rms_norm_partials", "add_rms_norm_separate", "add_rms_norm_partials_separate",
     "rms_norm", "swiglu_partials",
 ]

@@ -154,3 +154,19 @@ def test_decode_stack_contract_on_host():
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
     bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0)  # descriptor copy past the LDS
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+
+
+def test_selection_api_mirrors_the_reference():
+    """gemm.pick_matmul and timing.time_calls keep the reference's signatures
+    (engine/kernels/gemm.py:134-135, timing.py:9) and contract checks."""
+    import inspect
+    from kernels import gemm, timing
+    params = list(inspect.signature(gemm.pick_matmul).parameters)
+    assert params == ["batch", "every", "reps", "trials", "packed", "use_graph", "family", "quick"]
+    sig = inspect.signature(timing.time_calls)
+    assert list(sig.parameters) == ["fn", "operands", "reps", "trials", "use_graph"]
+    assert sig.parameters["reps"].default == 3 and sig.parameters["trials"].default == 5
+    for bad in (dict(operands=[]), dict(operands=[1], reps=0), dict(operands=[1], trials=0)):
+        ops = bad.pop("operands")
+        with pytest.raises(ValueError):
+            timing.time_calls(lambda w: None, ops, **bad)
