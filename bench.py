@@ -99,10 +99,11 @@ class Stack:
             else:  # down, lm_head
                 q = h = self.linear(h if name == "lm_head" else q, packed)
 
-    def executor(self, waves=8, lanes=1):
+    def executor(self, waves=8, lanes=1, loaders=0, ring_chunks=0):
         """The same chain as one decode-step executor launch (outputs preallocated)."""
         from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes)
+        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, loaders=loaders,
+                            ring_chunks=ring_chunks)
         self.outs = []
         h = self.x[2560]
         q = None
@@ -256,14 +257,23 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
     del g
     out = {"graph_us": ms_graph * 1e3}
     if m <= 16:
-        chain = stack.executor()
-        ms_exec = time_fn(chain.run, steps, warmup)
-        if chain.failed():
-            raise RuntimeError("decode executor: a wait gave up")
-        out.update(executor_us=ms_exec * 1e3, executor_grid=chain.grid, executor_lds=chain.lds)
-        del chain
-    ms = min(ms_graph, out.get("executor_us", 1e30) / 1e3)
-    out["path"] = "executor" if ms < ms_graph else "graph"
+        # Two executors: every wave loads its own weights (stack_kernel), or loader waves feed
+        # the compute waves through an LDS ring (ring_kernel; best of its shapes).
+        for key, waves, loaders in (("executor_us", 8, 0), ("ring_us", 4, 6), ("ring_us", 4, 4), ("ring_us", 8, 4)):
+            chain = stack.executor(waves=waves, loaders=loaders)
+            ms_exec = time_fn(chain.run, steps, warmup)
+            if chain.failed():
+                raise RuntimeError(f"decode executor (loaders={loaders}): a wait gave up")
+            out.setdefault("shapes_us", {})[f"{waves}c{loaders}l"] = round(ms_exec * 1e3, 2)
+            if ms_exec * 1e3 < out.get(key, 1e30):
+                out[key] = ms_exec * 1e3
+                out[key.replace("_us", "_launch")] = {"grid": chain.grid, "lds": chain.lds, "waves": waves,
+                                                      "loaders": loaders, "ring_chunks": chain.launch.ring_chunks,
+                                                      "desc_lds": chain.launch.desc_lds >= 0}
+            del chain
+    cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30), "ring": out.get("ring_us", 1e30)}
+    out["path"] = min(cands, key=cands.get)
+    ms = cands[out["path"]] / 1e3
     out.update({
         "us": ms * 1e3,
         "weight_GB": stack.weight_bytes() / 1e9,
@@ -310,16 +320,21 @@ def main():
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
     log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
-        f"executor {head.get('executor_us', float('nan')):.1f}), "
+        f"executor {head.get('executor_us', float('nan')):.1f}, ring {head.get('ring_us', float('nan')):.1f}), "
         f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
 
     fmt_name = {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload]
-    if head["path"] == "executor":
+    if head["path"] in ("executor", "ring"):
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
+        rl = head.get("ring_launch", {})
+        kname = (f"stack_kernel<{fmt_name}, 8, true>" if head["path"] == "executor"
+                 else f"ring_kernel<{fmt_name}, {rl.get('waves')}, {rl.get('loaders')}, "
+                      f"{str(rl.get('desc_lds')).lower()}>")
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(head["hbm_frac"], 4), "traffic": profiled_traffic(args.workload, args.m, "stack"),
-            "kernel": f"stack_kernel<{fmt_name}, 8, true> (the whole chain, M={args.m})",
+            "frac": round(head["hbm_frac"], 4),
+            "traffic": profiled_traffic(args.workload, args.m, "stack" if head["path"] == "executor" else "ring"),
+            "kernel": f"{kname} (the whole chain, M={args.m})",
             "us_per_launch": round(head["us"], 2), "alg_MB_per_launch": round(head["alg_GB"] * 1e3, 3),
         }
     else:
@@ -379,7 +394,9 @@ def main():
             "path": head["path"],
         },
         "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
-                     "executor": round(head["executor_us"], 2) if "executor_us" in head else None},
+                     "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
+                     "ring_executor": round(head["ring_us"], 2) if "ring_us" in head else None,
+                     "executor_shapes": head.get("shapes_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),
         "roofline": roofline,

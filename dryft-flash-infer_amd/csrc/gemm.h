@@ -570,22 +570,32 @@ struct FmtInt8 {
 // Chunks each thread keeps in flight while staging.
 constexpr int kStageUnroll = 4;
 
-template <class F, class XS>
-__device__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst) {
+// The threads that stage and finish a work item, and how they wait for each other: the
+// whole workgroup and its barrier here; the decode executor's compute waves (without its
+// weight-loading waves) bring their own.
+struct BlockTeam {
+  __device__ int tid() const { return threadIdx.x; }
+  __device__ int size() const { return blockDim.x; }
+  __device__ void sync() const { __syncthreads(); }
+};
+
+template <class F, class XS, class Team = BlockTeam>
+__device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {}) {
+  const int tid = team.tid(), nthr = team.size();
   constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
   const int cpr = nst * CPS;
   const int total = a.m * cpr;
   if constexpr (F::GATHER) {
     static_assert(std::is_same<XS, XPlain>::value, "gathered staging reads x from device memory");
-    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+    for (int q = tid; q < total; q += nthr) {
       const int mm = q / cpr, kc = q - mm * cpr;
       *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = F::stage_chunk(a, mm, step0 * F::KSTEP + kc * 8);
     }
   } else {
-    for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
+    for (int q0 = tid; q0 < total; q0 += kStageUnroll * nthr) {
       typename XS::Raw r[kStageUnroll];
       auto chunk = [&](int u, int& mm, int& kabs) {
-        const int q = q0 + u * blockDim.x;
+        const int q = q0 + u * nthr;
         mm = q / cpr;
         kabs = step0 * F::KSTEP + (q - mm * cpr) * 8;
         return q < total;
@@ -638,23 +648,33 @@ __device__ __forceinline__ void store_e4m3_chunk(char* dst, uint4 v, float sc) {
   *reinterpret_cast<uint2*>(dst) = o;
 }
 
+// The per-token bf16 maxima (as uint bits) of the FP8 prologue, after the token scales.
+__device__ __forceinline__ uint32_t* fp8_amax(const GemmArgs& a, char* lds) {
+  return reinterpret_cast<uint32_t*>(lds + a.off_sx) + a.m;
+}
+
 // FP8 W8A8 prologue: per-token scale over the whole row, then e4m3 codes of the slice. When
 // one batch of loads covers the rows, the values stay in registers for the codes (one pass
-// over x); otherwise the slice is read again.
-template <class XS>
-__device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst) {
+// over x); otherwise the slice is read again. With `zeroed_amax`, the per-token maxima live
+// there, already cleared and visible to the team.
+template <class XS, class Team = BlockTeam>
+__device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {},
+                              uint32_t* zeroed_amax = nullptr) {
+  const int tid = team.tid(), nthr = team.size();
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
-  uint32_t* amax = reinterpret_cast<uint32_t*>(sx + a.m);
-  for (int i = threadIdx.x; i < a.m; i += blockDim.x) amax[i] = 0u;
-  __syncthreads();
+  uint32_t* amax = zeroed_amax ? zeroed_amax : fp8_amax(a, lds);
+  if (!zeroed_amax) {
+    for (int i = tid; i < a.m; i += nthr) amax[i] = 0u;
+    team.sync();
+  }
   const int cpr = a.k >> 3;
   const int total = a.m * cpr;
-  const bool one_pass = total <= kStageUnroll * (int)blockDim.x;
+  const bool one_pass = total <= kStageUnroll * nthr;
   uint4 kept[kStageUnroll];
-  for (int q0 = threadIdx.x; q0 < total; q0 += kStageUnroll * blockDim.x) {
+  for (int q0 = tid; q0 < total; q0 += kStageUnroll * nthr) {
     typename XS::Raw r[kStageUnroll];
     auto chunk = [&](int u, int& mm, int& kabs) {
-      const int q = q0 + u * blockDim.x;
+      const int q = q0 + u * nthr;
       mm = q / cpr;
       kabs = (q - mm * cpr) * 8;
       return q < total;
@@ -667,7 +687,7 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
     settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const int q = q0 + u * blockDim.x;
+      const int q = q0 + u * nthr;
       if (q < total) {
         const uint4 v = xs.value(r[u]);
         kept[u] = v;
@@ -679,26 +699,28 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
       }
     }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = fmaxf(__uint_as_float(amax[i]) / 448.f, 1e-12f);
-  __syncthreads();
+  team.sync();
+  // Every thread derives the token scales it needs from the maxima (no second barrier); the
+  // epilogue reads sx after later barriers.
+  auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
+  for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
   const int c0 = step0 * 16, c1 = c0 + nst * 16;  // the slice's 8-value chunks within a row
   if (one_pass) {
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const int q = threadIdx.x + u * blockDim.x;
+      const int q = tid + u * nthr;
       if (q < total) {
         const int mm = q / cpr, kc = q - mm * cpr;
-        if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, kept[u], sx[mm]);
+        if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, kept[u], token_scale(mm));
       }
     }
     return;
   }
   const int cps = nst * 16;  // 8-value chunks per row of the slice
-  for (int q0 = threadIdx.x; q0 < a.m * cps; q0 += kStageUnroll * blockDim.x) {
+  for (int q0 = tid; q0 < a.m * cps; q0 += kStageUnroll * nthr) {
     typename XS::Raw r[kStageUnroll];
     auto chunk = [&](int u, int& mm, int& kabs) {
-      const int q = q0 + u * blockDim.x;
+      const int q = q0 + u * nthr;
       mm = q / cps;
       kabs = step0 * 128 + (q - mm * cps) * 8;
       return q < a.m * cps;
@@ -712,7 +734,8 @@ __device__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int st
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
       int mm, kabs;
-      if (chunk(u, mm, kabs)) store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), sx[mm]);
+      if (chunk(u, mm, kabs))
+        store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), token_scale(mm));
     }
   }
 }
@@ -737,18 +760,19 @@ __device__ void stage_int8_act(const GemmArgs& a, char* lds, int step0, int nst)
   }
 }
 
-template <class F>
-__device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, int nst) {
+template <class F, class Team = BlockTeam>
+__device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, int nst, const Team& team = {}) {
+  const int tid = team.tid(), nthr = team.size();
   float* sc = reinterpret_cast<float*>(lds + a.off_sc);
   const int rows = 16 * a.rt;
   if constexpr (F::NSC == 0) {
-    for (int rl = threadIdx.x; rl < rows; rl += blockDim.x) {
+    for (int rl = tid; rl < rows; rl += nthr) {
       const int tile = tg * a.rt + (rl >> 4);
       sc[rl] = tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), 0, 0) : 0.f;
     }
   } else {
     const int total = nst * F::NSC * rows;
-    for (int q = threadIdx.x; q < total; q += blockDim.x) {
+    for (int q = tid; q < total; q += nthr) {
       const int sj = q / rows, rl = q - sj * rows;
       const int tile = tg * a.rt + (rl >> 4);
       sc[sj * a.sc_stride + rl] =
@@ -916,11 +940,13 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
 
 }
 
-// Epilogue, first half: every wave's accumulators to LDS ([wave][RW][16 rows][16*MT]).
-template <int MT, int RW>
-__device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT]) {
+// Epilogue, first half: every wave's accumulators to LDS ([wave][RW][16 rows][16*MT]). With
+// `guard`, first wait until every wave is done with what was there.
+template <int MT, int RW, class Team = BlockTeam>
+__device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT], const Team& team = {},
+                                           bool guard = true) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
+  if (guard) team.sync();
   float* red = reinterpret_cast<float*>(lds);
   constexpr int RC = 16 * MT;
 #pragma unroll
@@ -930,7 +956,7 @@ __device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT]
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         red[((wave * RW + r) * 16 + 4 * (lane >> 4) + i) * RC + 16 * mt + (lane & 15)] = acc[r][mt][i];
-  __syncthreads();
+  team.sync();
 }
 
 // Output (tile tl of the block, tile row nl, token mm): the kw waves' sums (acc_to_lds at

@@ -34,14 +34,19 @@ BUDGET_US = 2_000_000
 
 
 class DecodeStack:
-    """An ordered chain of projections of one format, for m = 1..16 tokens."""
+    """An ordered chain of projections of one format, for m = 1..16 tokens.
 
-    def __init__(self, fmt, m, waves=8, groups_per_cu=1):
+    ``loaders`` (4 or 6 beside 4 compute waves, 4 beside 8) adds waves per workgroup that only copy weights into an LDS ring of
+    ``ring_chunks`` 1 KB slots (0: the most that fits), so the weight stream never waits for
+    an activation; 0 lets every compute wave load its own weights."""
+
+    def __init__(self, fmt, m, waves=8, groups_per_cu=1, loaders=0, ring_chunks=0):
         if fmt not in _FMTS:
             raise ValueError(f"the decode executor serves {sorted(_FMTS)}, not {fmt!r}")
         if not 1 <= m <= 16:
             raise ValueError(f"the decode executor serves m = 1..16 (got {m})")
         self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
+        self.loaders, self.ring_chunks = loaders, ring_chunks
         self.calls, self._keep = [], []
         self.desc = None
         self.epoch = 0
@@ -81,15 +86,15 @@ class DecodeStack:
         fmt = _FMTS[self.fmt]
         arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.waves, self.groups_per_cu, None,
-                                           None, None, arena_bytes, launch), "qlx_stack_build")
+            opts = (self.waves, self.groups_per_cu, self.loaders, self.ring_chunks)
+            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), *opts, None, None, None, arena_bytes,
+                                           launch), "qlx_stack_build")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
             self.error = torch.zeros(1, dtype=torch.int32, device=device)
             host = torch.empty(lib.qlx_stack_desc_size() * len(self.calls), dtype=torch.uint8)
             plans = (_lib.Plan * len(self.calls))()
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), self.waves, self.groups_per_cu,
-                                           ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.arena),
-                                           arena_bytes, launch), "qlx_stack_build")
+            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), *opts, ctypes.c_void_p(host.data_ptr()),
+                                           plans, _lib.ptr(self.arena), arena_bytes, launch), "qlx_stack_build")
             self.desc = host.to(device)
         #: (waves, kw, rw, most K pieces of one row block) per projection
         self.configs = [(p.waves, p.kw, p.rw, p.splits) for p in plans]
@@ -111,6 +116,15 @@ class DecodeStack:
         """True if a wait of any run so far gave up (that run's outputs are undefined).
         Synchronizes with the device."""
         return bool(self.error.item())
+
+    #: The kinds of wait, by bit of the error word: an activation from an earlier projection, a
+    #: piece's partial sums, the compute waves' barrier, a weight chunk in the ring, a free ring slot.
+    WAIT_SITES = ("input", "partial", "team", "chunk", "slot")
+
+    def failed_waits(self):
+        """The kind of the first wait that gave up (a list; empty if none did)."""
+        e = int(self.error.item())
+        return [name for i, name in enumerate(self.WAIT_SITES) if e >> i & 1]
 
     def reset(self):
         """Clear the error flag (nothing else outlives a failed run)."""

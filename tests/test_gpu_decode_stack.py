@@ -53,11 +53,11 @@ def source(bufs, src):
     return bufs[src]
 
 
-def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1):
+def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, loaders=0, ring_chunks=0):
     quant = qlinear.FORMATS[fmt][0]
     bufs = {"x": rand((m, 1024), seed).to(DEV), "g": rand((m, 9728), seed + 1).to(DEV)}
     weights, raw = {}, {}
-    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes)
+    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes, loaders=loaders, ring_chunks=ring_chunks)
     for idx, (name, n, k, src, sw) in enumerate(CHAIN):
         w = rand((n, k), seed + 10 + idx, std=0.02).to(DEV)
         packed = quant(w)
@@ -100,19 +100,16 @@ def oracle_check(fmt, x_bits, packed, y):
     return O.rel_l2(y.float().cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
-@pytest.mark.parametrize("m", [1, 5, 16])
-def test_chain_matches_single_calls_and_oracle(fmt, m):
-    print(f"decode stack {fmt} m={m}", flush=True)
-    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m)
-    assert chain.grid >= 256 and chain.lds > 0
+def run_chain_checks(fmt, m, waves=8, loaders=0, ring_chunks=0):
+    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m, waves=waves, loaders=loaders, ring_chunks=ring_chunks)
+    assert chain.grid >= 256 and chain.lds > 0 and chain.launch.loaders == loaders
     for run in range(3):
         if run:
             bufs["x"].copy_(rand((m, 1024), 7 * run + m).to(DEV))
             bufs["g"].copy_(rand((m, 9728), 9 * run + m).to(DEV))
         chain.run()
         torch.cuda.synchronize()
-        assert not chain.failed()
+        assert not chain.failed(), chain.failed_waits()
         first = {name: bufs[name].clone() for name, *_ in CHAIN}
         chain.run()
         torch.cuda.synchronize()
@@ -124,15 +121,35 @@ def test_chain_matches_single_calls_and_oracle(fmt, m):
         assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name]) < 1e-2, name
 
 
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_chain_matches_single_calls_and_oracle(fmt, m):
+    print(f"decode stack {fmt} m={m}", flush=True)
+    run_chain_checks(fmt, m)
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+@pytest.mark.parametrize("m,waves,loaders,ring", [(1, 4, 6, 0), (5, 4, 4, 0), (16, 8, 4, 0), (1, 4, 6, 32),
+                                                  (2, 8, 4, 32)])
+def test_ring_chain_matches_single_calls_and_oracle(fmt, m, waves, loaders, ring):
+    """Loader waves feeding the compute waves through the LDS weight ring (32 slots, the
+    least allowed: the ring wraps many times per item) give the same results as the
+    single-call linears."""
+    print(f"decode stack ring {fmt} m={m} waves={waves} loaders={loaders} ring={ring}", flush=True)
+    run_chain_checks(fmt, m, waves=waves, loaders=loaders, ring_chunks=ring)
+
+
 @pytest.mark.parametrize("kw", [1, 2, 4, 8])
-def test_every_tile_split_is_exact(kw):
+@pytest.mark.parametrize("loaders", [0, 4])
+def test_every_tile_split_is_exact(kw, loaders):
     """Forced waves-per-tile settings change the pieces, not the results' bound."""
-    chain, bufs, weights, _ = build_chain("w4a16", 3, 77, kw=kw)
+    print(f"decode stack kw={kw} loaders={loaders}", flush=True)
+    chain, bufs, weights, _ = build_chain("fp8" if loaders else "w4a16", 3, 77, kw=kw, loaders=loaders)
     assert all(c[1] == kw for c in chain.configs)
     chain.run()
     torch.cuda.synchronize()
     assert not chain.failed()
-    check_against_single_calls("w4a16", bufs, weights, ("kw", kw))
+    check_against_single_calls("fp8" if loaders else "w4a16", bufs, weights, ("kw", kw, loaders))
 
 
 @pytest.mark.parametrize("fmt,waves,lanes", [("fp8", 4, 3), ("w4a16", 4, 2), ("w8a16", 8, 2)])
@@ -151,11 +168,13 @@ def test_lanes_and_small_workgroups(fmt, waves, lanes):
         check_against_single_calls(fmt, bufs, weights, (fmt, waves, lanes, run))
 
 
-def test_bounded_wait_gives_up_and_recovers():
+@pytest.mark.parametrize("waves,loaders", [(8, 0), (4, 6)])
+def test_bounded_wait_gives_up_and_recovers(waves, loaders):
     """A zero wait budget makes the waits give up (forced from the host): the kernel still
     ends, flags the run, and after reset() a normal run is right again."""
     m = 2
-    chain, bufs, weights, _ = build_chain("fp8", m, 55)
+    print(f"decode stack bounded wait waves={waves} loaders={loaders}", flush=True)
+    chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves, loaders=loaders)
     chain.run(budget_us=0)
     torch.cuda.synchronize()
     assert chain.failed()
