@@ -170,7 +170,7 @@ struct ExecDepth<FmtW4> {
 // last being `last`; plus the item's per-row scale for formats with one scale per row.
 struct ExecItem {
   int tg, s, np, step0, nst, wt, kwi, my, last, wrow;
-  float sc;
+  uint32_t scb;  // the per-row scale's bf16 bits, converted only when staged
 };
 
 // Issue the wave's first ExecDepth<F>::PF weight steps (and the per-row scale) of a work
@@ -192,11 +192,13 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
   it.my = active ? (nst - it.kwi + a.kw - 1) / a.kw : 0;  // this wave's steps: kwi, kwi + kw, ...
   it.last = step0 + it.kwi + (it.my - 1) * a.kw;
   // The scale first: memory counters complete in order, so reading it then waits for no
-  // weight load.
-  it.sc = 0.f;
+  // weight load. It stays raw bits here: converting it now would wait for every memory
+  // operation still in flight (the previous item's output stores among them).
+  it.scb = 0u;
   if constexpr (F::NSC == 0) {
     const int rl = threadIdx.x, tile = tg * a.rt + (rl >> 4);
-    if (rl < 16 * a.rt && tile < a.ntiles) it.sc = F::scale(a, weight_row(a, tile, rl & 15), 0, 0);
+    if (rl < 16 * a.rt && tile < a.ntiles)
+      it.scb = gmem(reinterpret_cast<const uint16_t*>(a.ws))[weight_row(a, tile, rl & 15)];
   }
 #pragma unroll
   for (int p = 0; p < ExecDepth<F>::PF; ++p)
@@ -219,7 +221,9 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
       stage_bf16<F>(a, xs, lds, step0, nst);
   }
   if constexpr (F::NSC == 0) {
-    if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = it.sc;
+    // Read on every path, so the register is not left pending for the next item's prefetch.
+    const float scv = bf2f(it.scb);
+    if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
   } else {
     stage_scales<F>(a, lds, it.tg, step0, nst);
   }
@@ -235,15 +239,26 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   mrow[0] = min(lane & 15, a.m - 1);
   xoff[0] = mrow[0] * a.xstride;
   const int rowl = it.wt * 16 + 4 * (lane >> 4);
+  // Steps j0 .. j0 + PF - 1 are in buf. Every load issued is consumed: a load nobody reads
+  // leaves its register pending, and the next item's first use of that register would wait for
+  // every memory operation in flight.
   int j0 = 0;
-  for (; j0 + PF <= my; j0 += PF) {
+  for (; j0 + 2 * PF <= my; j0 += PF) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
       F::template compute<1>(acc[0], buf[p], lds, a, kwi + (j0 + p) * a.kw, lane, xoff, mrow, rowl);
-      const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, it.last);
-      load_chunk<F>(buf[p], a, it.wrow, nxt, lane);
+      load_chunk<F>(buf[p], a, it.wrow, step0 + kwi + (j0 + p + PF) * a.kw, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
+  if (j0 + PF <= my) {  // the last block that still refills some buffers
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      F::template compute<1>(acc[0], buf[p], lds, a, kwi + (j0 + p) * a.kw, lane, xoff, mrow, rowl);
+      if (j0 + p + PF < my) load_chunk<F>(buf[p], a, it.wrow, step0 + kwi + (j0 + p + PF) * a.kw, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    j0 += PF;
   }
 #pragma unroll
   for (int p = 0; p < PF; ++p)
@@ -377,6 +392,26 @@ __device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, 
   exec_prefetch<F>(d.a, g, step0, nst, piece, np, it, buf);
 }
 
+// A workgroup's next work item, found ahead of time: finding it is arithmetic, and arithmetic
+// that runs after the item's output stores may wait for them (a register it reuses can still
+// be the target of a load), which would delay the next item's weight loads.
+struct NextItem {
+  bool have;
+  int c, g, step0, nst, piece, np;
+};
+__device__ __forceinline__ NextItem find_next(const StackDesc* calls, int ncalls, int lanes, int lane, int p, int c,
+                                              int g) {
+  NextItem n;
+  n.c = c;
+  n.g = g;
+  n.have = next_work(calls, ncalls, lanes, lane, p, n.c, n.g);
+  if (n.have) {
+    const StackDesc& d = calls[n.c];
+    share_item(share_slot(d, p), n.g, d.units, d.pe, d.gran, d.a.nsteps, &n.step0, &n.nst, &n.piece, &n.np);
+  }
+  return n;
+}
+
 template <class F, int WAVES, bool DLDS>
 __global__ void __launch_bounds__(WAVES * 64)
 stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
@@ -413,14 +448,18 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     staged_c = c;
     staged_step0 = cur.step0;
     staged_nst = cur.nst;
-    // Outputs first: later projections wait for them, and issuing the next item's loads
-    // can stall on a full memory pipeline (a reducer's loads would also wait behind them).
+    // Outputs first: later projections wait for them. Anything before them -- finding the
+    // next item, issuing its loads (the stores would queue behind them) -- delays the chain
+    // (measured: 60-160 us per decode step).
     if (d.sw)
       exec_finish<F, true>(d, lds, cur, acc, w);
     else
       exec_finish<F, false>(d, lds, cur, acc, w);
-    have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-    if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+    const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
+    have = after.have;
+    nc = after.c;
+    ng = after.g;
+    if (have) exec_prefetch<F>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     __syncthreads();  // LDS is reused by the next item
   }
 }
