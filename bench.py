@@ -35,6 +35,7 @@ LAYERS = 36
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
+EXECUTOR_SHAPES = ((8, 0), (4, 0), (4, 2), (4, 4))  # (compute waves, poller waves)
 
 
 def log(*a):
@@ -99,11 +100,10 @@ class Stack:
             else:  # down, lm_head
                 q = h = self.linear(h if name == "lm_head" else q, packed)
 
-    def executor(self, waves=8, lanes=1, loaders=0, ring_chunks=0):
+    def executor(self, waves=8, lanes=1, pollers=0):
         """The same chain as one decode-step executor launch (outputs preallocated)."""
         from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, loaders=loaders,
-                            ring_chunks=ring_chunks)
+        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, pollers=pollers)
         self.outs = []
         h = self.x[2560]
         q = None
@@ -257,21 +257,20 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
     del g
     out = {"graph_us": ms_graph * 1e3}
     if m <= 16:
-        # Two executors: every wave loads its own weights (stack_kernel), or loader waves feed
-        # the compute waves through an LDS ring (ring_kernel; best of its shapes).
-        for key, waves, loaders in (("executor_us", 8, 0), ("ring_us", 4, 6), ("ring_us", 4, 4), ("ring_us", 8, 4)):
-            chain = stack.executor(waves=waves, loaders=loaders)
+        # The executor in each workgroup shape: 8 compute waves, or 4 with 0, 2 or 4 poller waves
+        # (waves that only read and stage the published activations).
+        for waves, pollers in EXECUTOR_SHAPES:
+            chain = stack.executor(waves=waves, pollers=pollers)
             ms_exec = time_fn(chain.run, steps, warmup)
             if chain.failed():
-                raise RuntimeError(f"decode executor (loaders={loaders}): a wait gave up")
-            out.setdefault("shapes_us", {})[f"{waves}c{loaders}l"] = round(ms_exec * 1e3, 2)
-            if ms_exec * 1e3 < out.get(key, 1e30):
-                out[key] = ms_exec * 1e3
-                out[key.replace("_us", "_launch")] = {"grid": chain.grid, "lds": chain.lds, "waves": waves,
-                                                      "loaders": loaders, "ring_chunks": chain.launch.ring_chunks,
-                                                      "desc_lds": chain.launch.desc_lds >= 0}
+                raise RuntimeError(f"decode executor ({waves}c{pollers}p): a wait gave up")
+            out.setdefault("shapes_us", {})[f"{waves}c{pollers}p"] = round(ms_exec * 1e3, 2)
+            if ms_exec * 1e3 < out.get("executor_us", 1e30):
+                out["executor_us"] = ms_exec * 1e3
+                out["executor_launch"] = {"grid": chain.grid, "lds": chain.lds, "waves": waves, "pollers": pollers,
+                                          "desc_lds": chain.launch.desc_lds >= 0}
             del chain
-    cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30), "ring": out.get("ring_us", 1e30)}
+    cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
     ms = cands[out["path"]] / 1e3
     out.update({
@@ -320,20 +319,18 @@ def main():
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
     log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
-        f"executor {head.get('executor_us', float('nan')):.1f}, ring {head.get('ring_us', float('nan')):.1f}), "
+        f"executor {head.get('executor_us', float('nan')):.1f} {head.get('shapes_us')}), "
         f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
 
     fmt_name = {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload]
-    if head["path"] in ("executor", "ring"):
+    if head["path"] == "executor":
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
-        rl = head.get("ring_launch", {})
-        kname = (f"stack_kernel<{fmt_name}, 8, true>" if head["path"] == "executor"
-                 else f"ring_kernel<{fmt_name}, {rl.get('waves')}, {rl.get('loaders')}, "
-                      f"{str(rl.get('desc_lds')).lower()}>")
+        el = head["executor_launch"]
+        kname = f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}>"
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
-            "traffic": profiled_traffic(args.workload, args.m, "stack" if head["path"] == "executor" else "ring"),
+            "traffic": profiled_traffic(args.workload, args.m, "stack"),
             "kernel": f"{kname} (the whole chain, M={args.m})",
             "us_per_launch": round(head["us"], 2), "alg_MB_per_launch": round(head["alg_GB"] * 1e3, 3),
         }
@@ -395,7 +392,6 @@ def main():
         },
         "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
                      "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
-                     "ring_executor": round(head["ring_us"], 2) if "ring_us" in head else None,
                      "executor_shapes": head.get("shapes_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),

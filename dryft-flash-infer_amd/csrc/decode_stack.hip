@@ -48,7 +48,7 @@ struct alignas(16) StackDesc {
   int pe;           // workgroups with work: min(P, units)
   int gran;         // block-steps per unit
   int sw;           // SwiGLU epilogue
-  int xpitch;       // words per token row of xwire (the producer's n_out / 2)
+  int xpitch;       // words (values) per token row of xwire (the producer's n_out)
   int off_red;      // LDS byte offset of the waves' partial sums (apart from the staged x)
   int rot;          // workgroup p holds share (p - rot) mod nwg of this projection
   int nwg;          // workgroups per lane
@@ -108,7 +108,7 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t v, uint32_t epoch
   __hip_atomic_store(gmem(p), ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Kinds of wait: the first one of a run to give up leaves (1 << kind) in the error word.
-enum WaitSite { kWaitInput = 0, kWaitPartial = 1, kWaitTeam = 2, kWaitChunk = 3, kWaitSlot = 4 };
+enum WaitSite { kWaitInput = 0, kWaitPartial = 1 };
 
 // True (and the run flagged as failed) once the run's deadline has passed: waits stop there.
 __device__ __forceinline__ bool ll_expired(const Waits& w, WaitSite site) {
@@ -119,36 +119,65 @@ __device__ __forceinline__ bool ll_expired(const Waits& w, WaitSite site) {
   return true;
 }
 
-// Activation published by an earlier projection: bf16 pairs, `pitch` words per token row
-// (the activation may be the first k columns of a wider output).
+// Published activations ("wire"): one 32-bit word per value, {16-bit run tag, bf16}. Every
+// word is single-copy atomic on its own, so a reader can take 16 bytes (4 values) per lane
+// with one device-coherent load and check each value's tag: half the load instructions of
+// 64-bit {value pair, 32-bit tag} words, and each lane's loads are the wave's bottleneck
+// (a wave draws about 1 KB per 110 ns however deep its queue, measured on MI355X).
+__device__ __forceinline__ uint32_t wire_tag(uint32_t epoch) { return epoch & 0xffffu; }
+
+// Both values of an output pair as two tagged words, in one 64-bit device-coherent store.
+__device__ __forceinline__ void wire_store_pair(uint64_t* p, uint32_t pair, uint32_t epoch) {
+  const uint32_t t = wire_tag(epoch) << 16;
+  const uint64_t v = ((uint64_t)(t | (pair >> 16)) << 32) | (t | (pair & 0xffffu));
+  __hip_atomic_store(gmem(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Buffer resource over `bytes` of device memory, in scalar registers (the pointer is the
+// same for every lane: descriptors are read from LDS, which the compiler cannot see).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wire_rsrc(const void* p, unsigned bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)bytes,
+                                           0x00020000);
+}
+// 16 bytes at `off`, read at device scope (sc1: past this XCD's L2, which other XCDs'
+// stores do not update).
+__device__ __forceinline__ u32x4 wire_load16(__amdgpu_buffer_rsrc_t rs, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 16);
+}
+
+// Activation published by an earlier projection: `pitch` words per token row (the
+// activation may be the first k columns of a wider output).
 struct XWire {
   static constexpr bool POLLS = true;
-  const uint64_t* wire;
+  __amdgpu_buffer_rsrc_t rs;
   int pitch;
+  uint32_t tag;
   Waits w;
+  __device__ XWire(const uint64_t* wire, int pitch_, int m, const Waits& w_)
+      : rs(wire_rsrc(wire, (unsigned)m * (unsigned)pitch_ * 4u)), pitch(pitch_), tag(wire_tag(w_.epoch)), w(w_) {}
   struct Raw {
-    uint64_t v[4];
+    u32x4 v[2];
   };
+  __device__ __forceinline__ static bool half_ready(const u32x4& h, uint32_t tag) {
+    return (h[0] >> 16) == tag && (h[1] >> 16) == tag && (h[2] >> 16) == tag && (h[3] >> 16) == tag;
+  }
   __device__ __forceinline__ void fetch(const GemmArgs&, int mm, int kabs, Raw& r) const {
-    const uint64_t* p = wire + (size_t)mm * pitch + (kabs >> 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.v[i] = ll_load(p + i);
+    const unsigned off = ((unsigned)mm * pitch + kabs) * 4u;
+    r.v[0] = wire_load16(rs, off);
+    r.v[1] = wire_load16(rs, off + 16);
   }
-  __device__ __forceinline__ bool ready(const Raw& r) const {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ok &= (uint32_t)(r.v[i] >> 32) == w.epoch;
-    return ok;
-  }
+  __device__ __forceinline__ bool ready(const Raw& r) const { return half_ready(r.v[0], tag) && half_ready(r.v[1], tag); }
   __device__ __forceinline__ void refetch(const GemmArgs&, int mm, int kabs, Raw& r) const {
-    const uint64_t* p = wire + (size_t)mm * pitch + (kabs >> 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if ((uint32_t)(r.v[i] >> 32) != w.epoch) r.v[i] = ll_load(p + i);
+    const unsigned off = ((unsigned)mm * pitch + kabs) * 4u;
+    if (!half_ready(r.v[0], tag)) r.v[0] = wire_load16(rs, off);
+    if (!half_ready(r.v[1], tag)) r.v[1] = wire_load16(rs, off + 16);
   }
   __device__ __forceinline__ bool expired() const { return ll_expired(w, kWaitInput); }
   __device__ __forceinline__ uint4 value(const Raw& r) const {
-    return uint4{(uint32_t)r.v[0], (uint32_t)r.v[1], (uint32_t)r.v[2], (uint32_t)r.v[3]};
+    return uint4{(r.v[0][0] & 0xffffu) | (r.v[0][1] << 16), (r.v[0][2] & 0xffffu) | (r.v[0][3] << 16),
+                 (r.v[1][0] & 0xffffu) | (r.v[1][1] << 16), (r.v[1][2] & 0xffffu) | (r.v[1][3] << 16)};
   }
 };
 
@@ -205,35 +234,143 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
     if (p < it.my) load_chunk<F>(buf[p], a, it.wrow, step0 + it.kwi + p * a.kw, lane);
 }
 
+// The two roles of an executor workgroup: WAVES compute waves (threads 0 .. 64 WAVES - 1)
+// stream weights and run the MFMAs and the epilogue; NP poller waves after them only read
+// published activations and stage them. A wave's memory operations complete in issue order,
+// so a compute wave's poll would wait for every weight load it has in flight (the next
+// item's prefetch: up to 12 KB per wave, 96 KB per CU); a poller has none. Both teams meet
+// at the workgroup's barriers, so they execute the same number of them per item.
+template <int WAVES>
+struct ComputeTeam {
+  __device__ int tid() const { return threadIdx.x; }
+  __device__ int size() const { return WAVES * 64; }
+  __device__ void sync() const { __syncthreads(); }
+};
+template <int WAVES, int NP>
+struct PollTeam {
+  __device__ int tid() const { return threadIdx.x - WAVES * 64; }
+  __device__ int size() const { return NP * 64; }
+  __device__ void sync() const { __syncthreads(); }
+};
+
+// Chunks of 8 values each poller thread keeps in registers between the two halves of the FP8
+// prologue (one pass over x when m * k <= 8 * 64 NP * kPollKeep: k <= 10240 at m = 1, NP = 4).
+constexpr int kPollKeep = 5;
+
+// FP8 prologue of the poller team: the per-token maxima over whole rows (atomicMax into the
+// zeroed `amax`), one workgroup barrier (the compute waves' matching one is in exec_main),
+// then the token scales and the e4m3 codes of the item's slice. Chunks kept from the first
+// pass are quantized from registers; the rest of the slice is read again (already published).
+template <int WAVES, int NP, class XS>
+__device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst,
+                                               uint32_t* amax) {
+  constexpr int U = kPollKeep;
+  const PollTeam<WAVES, NP> team;
+  const int tid = team.tid(), nthr = team.size();
+  const int cpr = a.k >> 3, total = a.m * cpr;
+  uint4 kept[U];
+  for (int q0 = tid; q0 < total; q0 += U * nthr) {
+    typename XS::Raw r[U];
+    auto chunk = [&](int u, int& mm, int& kabs) {
+      const int q = q0 + u * nthr;
+      mm = q / cpr;
+      kabs = (q - mm * cpr) * 8;
+      return q < total;
+    };
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
+    }
+    settle_batch<XS, U>(a, xs, r, chunk);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * nthr;
+      if (q < total) {
+        const uint4 v = xs.value(r[u]);
+        if (q0 == tid) kept[u] = v;
+        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
+        atomicMax(&amax[q / cpr], __float_as_uint(mx));
+      }
+    }
+  }
+  __syncthreads();
+  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+  auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
+  for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
+  const int c0 = step0 * 16, c1 = c0 + nst * 16;  // the slice's 8-value chunks within a row
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int q = tid + u * nthr;
+    if (q < total) {
+      const int mm = q / cpr, kc = q - mm * cpr;
+      if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, kept[u], token_scale(mm));
+    }
+  }
+  const int cps = nst * 16, kept_end = U * nthr;
+  for (int sidx = tid; sidx < a.m * cps; sidx += nthr) {
+    const int mm = sidx / cps, kc = c0 + (sidx - mm * cps);
+    if (mm * cpr + kc < kept_end) continue;
+    typename XS::Raw r[1];
+    auto chunk = [&](int, int& m2, int& kabs) {
+      m2 = mm;
+      kabs = kc * 8;
+      return true;
+    };
+    xs.fetch(a, mm, kc * 8, r[0]);
+    settle_batch<XS, 1>(a, xs, r, chunk);
+    store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, xs.value(r[0]), token_scale(mm));
+  }
+}
+
 // Stage what the item needs in LDS and stream its weight steps through the MFMAs. With
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
-// projection, same steps -- is still in place.
-template <class F, int WAVES, class XS>
+// projection, same steps -- is still in place. With poller waves (NP > 0) they stage the
+// activation and leave after the staging barriers; `amax` is their zeroed FP8 scratch.
+template <class F, int WAVES, int NP, class XS>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
-                                          uint4 (&buf)[ExecDepth<F>::PF][F::LOADS], f32x4 (&acc)[1][1]) {
+                                          uint4 (&buf)[ExecDepth<F>::PF][F::LOADS], f32x4 (&acc)[1][1],
+                                          uint32_t* amax) {
   constexpr int PF = ExecDepth<F>::PF;
+  constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
   const int step0 = it.step0, nst = it.nst, kwi = it.kwi, my = it.my;
+  const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
   if (!reuse) {
-    if constexpr (std::is_same<F, FmtFP8>::value)
-      stage_fp8_act(a, xs, lds, step0, nst);
-    else
-      stage_bf16<F>(a, xs, lds, step0, nst);
+    if constexpr (NP == 0) {
+      if constexpr (FP8)
+        stage_fp8_act(a, xs, lds, step0, nst);
+      else
+        stage_bf16<F>(a, xs, lds, step0, nst);
+    } else if (poller) {
+      if constexpr (FP8)
+        poll_stage_fp8<WAVES, NP>(a, xs, lds, step0, nst, amax);
+      else
+        stage_bf16<F>(a, xs, lds, step0, nst, PollTeam<WAVES, NP>{});
+    } else if constexpr (FP8) {
+      __syncthreads();  // the pollers' barrier between the row maxima and the codes
+    }
   }
-  if constexpr (F::NSC == 0) {
-    // Read on every path, so the register is not left pending for the next item's prefetch.
-    const float scv = bf2f(it.scb);
-    if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
-  } else {
-    stage_scales<F>(a, lds, it.tg, step0, nst);
+  if (!poller) {
+    if constexpr (F::NSC == 0) {
+      // Read on every path, so the register is not left pending for the next item's prefetch.
+      const float scv = bf2f(it.scb);
+      if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
+    } else {
+      stage_scales<F>(a, lds, it.tg, step0, nst, ComputeTeam<WAVES>{});
+    }
   }
   __syncthreads();
   if constexpr (F::BIAS != 0.f) {
     if (!reuse) {
-      stage_bias<F, WAVES>(a, lds, nst);
+      if (!poller) stage_bias<F, WAVES>(a, lds, nst);
       __syncthreads();
     }
   }
+  if (poller) return;
   acc[0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
   int xoff[1], mrow[1];
   mrow[0] = min(lane & 15, a.m - 1);
@@ -354,7 +491,7 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
     const int oi = row[0];  // first output of the pair (even; for SwiGLU the gate row index)
     const uint32_t pair = bf16_pair(o0, o1);
     *gmem(reinterpret_cast<uint32_t*>(y + (size_t)mm * nout + oi)) = pair;
-    if (d.ywire) ll_store(d.ywire + (size_t)mm * (nout >> 1) + (oi >> 1), pair, w.epoch);
+    if (d.ywire) wire_store_pair(d.ywire + (size_t)mm * (nout >> 1) + (oi >> 1), pair, w.epoch);
   }
 }
 
@@ -412,443 +549,112 @@ __device__ __forceinline__ NextItem find_next(const StackDesc* calls, int ncalls
   return n;
 }
 
-template <class F, int WAVES, bool DLDS>
-__global__ void __launch_bounds__(WAVES * 64)
+// A poller wave's copy of a work item: the geometry staging needs, no loads.
+__device__ __forceinline__ void poll_item(const StackDesc& d, int p, int g, ExecItem& it) {
+  int step0, nst, piece, np;
+  share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
+  it.tg = g;
+  it.s = piece;
+  it.np = np;
+  it.step0 = step0;
+  it.nst = nst;
+  it.wt = it.kwi = it.my = it.last = it.wrow = 0;
+  it.scb = 0u;
+}
+
+template <class F, int WAVES, int NP, bool DLDS>
+__global__ void __launch_bounds__((WAVES + NP) * 64)
 stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
-             int desc_off, int lanes) {
+             int desc_off, int lanes, int amax_off) {
   extern __shared__ __align__(16) char lds[];
   const int per_lane = gridDim.x / lanes;
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
+  const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
+  uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 pollers' per-token maxima
+  if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   const StackDesc* calls = gcalls;
   if constexpr (DLDS) {
     const int n16 = ncalls * (int)(sizeof(StackDesc) / 16);
     const auto src = gmem(reinterpret_cast<const u32x4*>(gcalls));
     u32x4* dst = reinterpret_cast<u32x4*>(lds + desc_off);
     for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
-    __syncthreads();
     calls = reinterpret_cast<const StackDesc*>(lds + desc_off);
   }
+  __syncthreads();
   ExecItem cur, nxt;
   uint4 buf[ExecDepth<F>::PF][F::LOADS];
   f32x4 acc[1][1];
   int nc = -1, ng = 0;
   int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-  if (have) prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+  if (have) {
+    if (poller) poll_item(calls[nc], p, ng, nxt);
+    else prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+  }
   while (have) {
     const int c = nc;
     const StackDesc& d = calls[c];
     cur = nxt;
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire)
-      exec_main<F, WAVES>(d.a, XWire{d.xwire, d.xpitch, w}, lds, cur, reuse, buf, acc);
+      exec_main<F, WAVES, NP>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax);
     else
-      exec_main<F, WAVES>(d.a, XPlain{}, lds, cur, reuse, buf, acc);
+      exec_main<F, WAVES, NP>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax);
     staged_c = c;
     staged_step0 = cur.step0;
     staged_nst = cur.nst;
     // Outputs first: later projections wait for them. Anything before them -- finding the
     // next item, issuing its loads (the stores would queue behind them) -- delays the chain
     // (measured: 60-160 us per decode step).
-    if (d.sw)
-      exec_finish<F, true>(d, lds, cur, acc, w);
-    else
-      exec_finish<F, false>(d, lds, cur, acc, w);
+    if (poller) {
+      __syncthreads();  // the two barriers of acc_to_lds in exec_finish
+      __syncthreads();
+      if (threadIdx.x - WAVES * 64 < 16) amax[threadIdx.x - WAVES * 64] = 0u;  // for the next staging
+    } else if (d.sw) {
+      exec_finish<F, true>(d, lds, cur, acc, w, ComputeTeam<WAVES>{});
+    } else {
+      exec_finish<F, false>(d, lds, cur, acc, w, ComputeTeam<WAVES>{});
+    }
     const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
     have = after.have;
     nc = after.c;
     ng = after.g;
-    if (have) exec_prefetch<F>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+    if (have) {
+      if (poller) poll_item(calls[nc], p, ng, nxt);
+      else exec_prefetch<F>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+    }
     __syncthreads();  // LDS is reused by the next item
   }
 }
 
-template <class F>
-const void* stack_fn(int waves, bool dlds) {
-  if (waves == 4)
-    return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, 4, true>)
-                : reinterpret_cast<const void*>(&stack_kernel<F, 4, false>);
-  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, 8, true>)
-              : reinterpret_cast<const void*>(&stack_kernel<F, 8, false>);
+template <class F, int WAVES, int NP>
+const void* stack_fn2(bool dlds) {
+  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true>)
+              : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false>);
 }
 
-// ---- ring executor: weight-loading waves feed the compute waves through LDS -------------
-//
-// In the executor above every wave streams its own weights, so the loads it issues for its
-// next item sit in the same in-order memory queue as the polls of that item's activation:
-// a poll's answer waits for every weight load issued before it, and while a dependency is
-// outstanding the wave can keep only a few steps in flight. Here the workgroup has NC compute
-// waves and NL loader waves. The loaders walk the same work items and copy every weight step
-// (and, for per-row-scale formats, each item's scales) into an LDS ring of 1 KB chunks, as far
-// ahead as the ring allows; they never wait for an activation. The compute waves stage
-// activations, wait only for the words they need and read weights from the ring. Weights
-// never depend on activations, so the HBM stream goes on while the chain waits for a
-// dependency. One wave streams about one 1 KB chunk per 150 ns however many loads it keeps in
-// flight (measured on MI355X, for plain loads and for LDS-direct loads alike), so a CU needs
-// four to six loader waves to draw its share of 7 TB/s; they keep eight plain 16-byte-per-lane
-// loads in flight each and write every chunk to its slot once the slot is free.
-//
-// Stream order of one workgroup: item after item, each [scale chunk], then its steps in
-// order, in each step the rt tiles in order, each tile step as two 1 KB chunks (the two
-// 16-byte loads of every lane). Loader l copies the chunks q with q % NL == l; chunk q lives
-// in ring slot q % R. Counters in LDS: landed[l] = chunks of loader l in place (its chunks
-// in stream order, so chunk q is in place once landed[q % NL] > q / NL); pos[w] = first
-// chunk compute wave w still needs (monotonic). A loader writes chunk q once q < min(pos) + R.
-// Compute waves wait for each other through an LDS counter (the hardware barrier would wait
-// for the loaders too).
-
-constexpr int kCtlBytes = 256;
-constexpr int kCtlBar = 0, kCtlLanded = 4, kCtlAmax = 16, kCtlPos = 32;  // uint32 indices
-constexpr int kLoaderDepth = 8;  // loads each loader wave keeps in flight
-// A compute wave reads its next step (two chunks, NC waves x 2 chunks further on) before it
-// releases the current one, so it needs chunk pos + 2 NC + 1 while holding pos: the ring must
-// hold more than 17 chunks, or the slowest wave could never get its next step.
-constexpr int kRingMinChunks = 32;
-
-template <int NC>
-struct RingTeam {
-  uint32_t* bar;
-  Waits w;
-  __device__ __forceinline__ int tid() const { return threadIdx.x; }
-  __device__ __forceinline__ int size() const { return NC * 64; }
-  // Arrival k (counting from 0) belongs to barrier k / NC: no wave reaches barrier b + 1
-  // before all have reached b, so the counter needs no reset.
-  __device__ __forceinline__ void sync() const {
-    uint32_t old = 0;
-    if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    old = __builtin_amdgcn_readfirstlane(old);
-    const uint32_t target = (old / NC + 1) * NC;
-    while (__hip_atomic_load(bar, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
-      if (ll_expired(w, kWaitTeam)) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-};
-
-// The geometry of a workgroup's item that both roles derive from the descriptor.
-struct RingItem {
-  int tg, step0, nst, piece, np, lrt;
-  uint32_t n;  // chunks
-};
-template <class F>
-__device__ __forceinline__ RingItem ring_item(const StackDesc& d, int p, int g) {
-  RingItem r;
-  r.tg = g;
-  share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &r.step0, &r.nst, &r.piece, &r.np);
-  r.lrt = 31 - __builtin_clz((unsigned)d.a.rt);
-  r.n = (F::NSC == 0 ? 1u : 0u) + ((uint32_t)r.nst << (r.lrt + 1));
-  return r;
-}
-
-// The 16 bytes (8 bf16 per-row scales) that lane `lane` copies for row block tg: rows in
-// block order ([gate rows][up rows] for SwiGLU blocks); lanes past the block copy a valid
-// block that nobody reads.
-__device__ __forceinline__ const u32x4* scale_block(const GemmArgs& a, int tg, int lane) {
-  const u32x4* ws = reinterpret_cast<const u32x4*>(a.ws);
-  const int tile0 = tg * a.rt;
-  int b = 0;
-  if (a.mode == QLX_MODE_SWIGLU) {  // rt blocks of gate rows (8 per tile), then rt of up rows
-    if (lane < a.rt) b = min(tile0 + lane, a.half / 8 - 1);
-    else if (lane < 2 * a.rt) b = min((a.half + 8 * tile0) / 8 + lane - a.rt, a.n / 8 - 1);
-  } else if (lane < 2 * a.rt) {
-    b = min(2 * tile0 + lane, a.n / 8 - 1);
-  }
-  return ws + b;
-}
-
-// Wave-uniform value (kept in scalar registers: the loader's bookkeeping is scalar work).
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// Loader wave l: chunks l, l + NL, l + 2 NL, ... of the workgroup's stream. Loads run
-// kLoaderDepth chunks ahead of the writes (chunk t of this loader is in buf[t % depth]); a
-// chunk is written once its slot is free, then counted in landed[l]. The item's geometry is
-// held in scalar registers; a weight chunk's address is tile_offset() of the tiled layout
-// with the wave-uniform part computed once per chunk.
-template <class F, int NC, int NL>
-__device__ __forceinline__ void ring_loader(const StackDesc* calls, int ncalls, int p, char* lds, uint32_t* ctl,
-                                            int ring_off, uint32_t rmask, const Waits& w) {
-  static_assert(F::LOADS == 2, "one tile step is two 1 KB chunks");
-  constexpr int D = kLoaderDepth;
-  constexpr int nsc = F::NSC == 0 ? 1 : 0;
-  const int l = uni((int)(threadIdx.x >> 6) - NC), lane = threadIdx.x & 63;
-  uint32_t* landed = ctl + kCtlLanded;
-  const uint32_t* pos = ctl + kCtlPos;
-  char* ring = lds + ring_off;
-  int c = -1, g = 0;
-  bool more = next_work(calls, ncalls, 1, 0, p, c, g);
-  if (!more) return;
-  // The current item, as scalars, and this lane's part of its addresses.
-  const char* wb = nullptr;
-  int spr = 0, rt = 1, lrt = 0, ntiles = 1, tile0 = 0, step0 = 0, n = 0, sw = 0, rowsel = 0;
-  const u32x4* sptr = nullptr;
-  auto enter = [&]() {
-    const StackDesc& d = calls[c];
-    const RingItem it = ring_item<F>(d, p, g);
-    wb = reinterpret_cast<const char*>(d.a.w);
-    spr = uni((std::is_same<F, FmtW4>::value ? d.a.k >> 1 : d.a.k) >> 7);  // 128-byte steps per row
-    rt = uni(d.a.rt);
-    lrt = uni(it.lrt);
-    ntiles = uni(d.a.ntiles);
-    tile0 = uni(it.tg * d.a.rt);
-    step0 = uni(it.step0);
-    n = uni((int)it.n);
-    sw = uni(d.a.mode == QLX_MODE_SWIGLU);
-    const int r = lane & 15;
-    rowsel = sw ? (r < 8 ? r : d.a.half + r - 8) : r;  // weight row of tile row r, less 8 * tile
-    if (nsc) sptr = scale_block(d.a, it.tg, lane);
-  };
-  enter();
-  int idx = l;  // this loader's next chunk, within the current item
-  // The next chunk's address for this lane; false once the stream has ended. The flag (not the
-  // per-lane address) steers the loop, so the bookkeeping stays wave-uniform.
-  auto next_chunk = [&](const u32x4*& ptr) -> bool {
-    while (more && idx >= n) {
-      idx -= n;
-      more = next_work(calls, ncalls, 1, 0, p, c, g);
-      if (more) enter();
-    }
-    if (!more) return false;
-    if (nsc && idx == 0) {
-      ptr = sptr;
-    } else {
-      const int e = idx - nsc;
-      const int j = e & 1, t = (e >> 1) & (rt - 1), step = step0 + (e >> (lrt + 1));
-      const int tile = min(tile0 + t, ntiles - 1);
-      size_t off;
-      if (!sw) {  // rows 16 tile .. 16 tile + 15: the chunk is 1 KB of consecutive bytes
-        off = ((size_t)(tile * spr + step) * 2 + j) * 1024 + lane * 16;
-      } else {
-        const int wrow = 8 * tile + rowsel;
-        off = ((size_t)((wrow >> 4) * spr + step) * 2 + j) * 1024 + (lane >> 4) * 256 + (wrow & 15) * 16;
-      }
-      ptr = reinterpret_cast<const u32x4*>(wb + off);
-    }
-    idx += NL;
-    return true;
-  };
-  auto load = [](const u32x4* ptr) { return __builtin_nontemporal_load(gmem(ptr)); };
-  u32x4 buf[D];
-  uint32_t issued = 0;
-  const u32x4* any = nullptr;  // an address already read: where loads past the end go
-#pragma unroll
-  for (int k = 0; k < D; ++k) {
-    if (next_chunk(any)) ++issued;
-    buf[k] = load(any);
-  }
-  uint32_t t = 0, limit = rmask + 1;
-  bool live = true;  // false once the run's deadline has passed: stop waiting for slots
-  while (t < issued) {
-#pragma unroll
-    for (int k = 0; k < D; ++k) {
-      if (t < issued) {
-        const uint32_t q = (uint32_t)l + NL * t;
-        while (q >= limit && live) {  // ring full: wait for the compute waves to free slots
-          uint32_t mn = __hip_atomic_load(&pos[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-          for (int v = 1; v < NC; ++v)
-            mn = min(mn, __hip_atomic_load(&pos[v], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
-          limit = (uint32_t)uni((int)mn) + rmask + 1;
-          if (q < limit) break;
-          if (ll_expired(w, kWaitSlot)) live = false;
-          else __builtin_amdgcn_s_sleep(1);
-        }
-        *reinterpret_cast<u32x4*>(ring + ((q & rmask) << 10) + lane * 16) = buf[k];
-        ++t;
-        __hip_atomic_store(&landed[l], t, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (next_chunk(any)) ++issued;
-      }
-      buf[k] = load(any);
-    }
-  }
-}
-
-// Compute side: wait until chunk q is in its slot (cached counters; bounded by the deadline).
-template <int NL>
-struct Landed {
-  const uint32_t* landed;
-  uint32_t c[NL];  // last value read of each loader's counter
-  __device__ __forceinline__ void wait(uint32_t q, const Waits& w) {
-    const int l = (int)(q % NL);
-    const uint32_t t = q / NL;
-    uint32_t have = 0;
-#pragma unroll
-    for (int i = 0; i < NL; ++i)
-      if (i == l) have = c[i];
-    if (have > t) return;
-    while (true) {
-      have = __hip_atomic_load(&landed[l], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (have > t) break;
-      if (ll_expired(w, kWaitChunk)) {
-        have = 0xffffffffu;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-#pragma unroll
-    for (int i = 0; i < NL; ++i)
-      if (i == l) c[i] = have;
-  }
-};
-
-template <class F, int NC, int NL, bool DLDS>
-__global__ void __launch_bounds__((NC + NL) * 64)
-ring_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
-            int desc_off, int ctl_off, int ring_off, uint32_t rmask) {
-  extern __shared__ __align__(16) char lds[];
-  const int p = blockIdx.x, wave = uni((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
-  uint32_t* ctl = reinterpret_cast<uint32_t*>(lds + ctl_off);
-  if (threadIdx.x < kCtlBytes / 4) ctl[threadIdx.x] = 0u;
-  const StackDesc* calls = gcalls;
-  if constexpr (DLDS) {
-    const int n16 = ncalls * (int)(sizeof(StackDesc) / 16);
-    const auto src = gmem(reinterpret_cast<const u32x4*>(gcalls));
-    u32x4* dst = reinterpret_cast<u32x4*>(lds + desc_off);
-    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
-    calls = reinterpret_cast<const StackDesc*>(lds + desc_off);
-  }
-  __syncthreads();  // the only barrier of all waves
-  if (wave >= NC) {
-    ring_loader<F, NC, NL>(calls, ncalls, p, lds, ctl, ring_off, rmask, w);
-    return;
-  }
-  const RingTeam<NC> team{ctl + kCtlBar, w};
-  uint32_t* pos = ctl + kCtlPos;
-  uint32_t* amax = ctl + kCtlAmax;
-  const char* ring = lds + ring_off;
-  Landed<NL> landed{ctl + kCtlLanded, {}};
-  auto release = [&](uint32_t v) {
-    if (lane == 0) __hip_atomic_store(&pos[wave], v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  };
-  uint32_t q = 0;
-  int c = -1, g = 0;
-  int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
-  while (next_work(calls, ncalls, 1, 0, p, c, g)) {
-    const StackDesc& d = calls[c];
-    const GemmArgs& a = d.a;
-    const RingItem it = ring_item<F>(d, p, g);
-    constexpr uint32_t nsc = F::NSC == 0 ? 1u : 0u;
-    const int lkw = 31 - __builtin_clz((unsigned)a.kw);
-    const int wt = wave >> lkw, kwi = wave & (a.kw - 1);
-    const bool active = it.tg * a.rt + wt < a.ntiles;
-    const int my = active && it.nst > kwi ? (it.nst - kwi + a.kw - 1) >> lkw : 0;
-    const bool reuse = staged_c == c && staged_step0 == it.step0 && staged_nst == it.nst;
-    // Per-row scales: from the item's scale chunk (bf16, rows in block order).
-    if constexpr (F::NSC == 0) {
-      landed.wait(q, w);
-      if (threadIdx.x < 16 * a.rt) {
-        const uint16_t* sl = reinterpret_cast<const uint16_t*>(ring + ((q & rmask) << 10));
-        const int rl = threadIdx.x, t = rl >> 4, r = rl & 15;
-        const int at = a.mode == QLX_MODE_SWIGLU ? (r < 8 ? 8 * t + r : 8 * a.rt + 8 * t + r - 8) : rl;
-        reinterpret_cast<float*>(lds + a.off_sc)[rl] = bf2f(sl[at]);
-      }
-      release(q + nsc);
-    } else {
-      stage_scales<F>(a, lds, it.tg, it.step0, it.nst, team);
-    }
-    if (!reuse) {
-      if constexpr (std::is_same<F, FmtFP8>::value) {
-        if (d.xwire)
-          stage_fp8_act(a, XWire{d.xwire, d.xpitch, w}, lds, it.step0, it.nst, team, amax);
-        else
-          stage_fp8_act(a, XPlain{}, lds, it.step0, it.nst, team, amax);
-      } else {
-        if (d.xwire)
-          stage_bf16<F>(a, XWire{d.xwire, d.xpitch, w}, lds, it.step0, it.nst, team);
-        else
-          stage_bf16<F>(a, XPlain{}, lds, it.step0, it.nst, team);
-      }
-      staged_c = c;
-      staged_step0 = it.step0;
-      staged_nst = it.nst;
-    }
-    if (!reuse || F::NSC != 0) team.sync();
-    if constexpr (F::BIAS != 0.f) {
-      if (!reuse) {
-        stage_bias<F, NC>(a, lds, it.nst);
-        team.sync();
-      }
-    }
-    // Main loop: this wave's steps kwi, kwi + kw, ... of tile wt, two chunks each, the next
-    // step's chunks read while the current one is in the MFMAs.
-    f32x4 acc[1][1];
-    acc[0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int xoff[1], mrow[1];
-    mrow[0] = min(lane & 15, a.m - 1);
-    xoff[0] = mrow[0] * a.xstride;
-    const int rowl = wt * 16 + 4 * (lane >> 4);
-    auto chunk_of = [&](int jj) {
-      return q + nsc + ((uint32_t)(((kwi + (jj << lkw)) << it.lrt) + wt) << 1);
-    };
-    auto fetch = [&](uint4 (&cb)[2], int jj) {
-      const uint32_t cq = chunk_of(jj);
-      landed.wait(cq, w);
-      landed.wait(cq + 1, w);
-      cb[0] = *reinterpret_cast<const uint4*>(ring + ((cq & rmask) << 10) + lane * 16);
-      cb[1] = *reinterpret_cast<const uint4*>(ring + (((cq + 1) & rmask) << 10) + lane * 16);
-    };
-    uint4 ca[2], cb[2];
-    if (my > 0) fetch(ca, 0);
-    for (int jj = 0; jj < my; jj += 2) {
-      if (jj + 1 < my) fetch(cb, jj + 1);
-      F::template compute<1>(acc[0], ca, lds, a, kwi + (jj << lkw), lane, xoff, mrow, rowl);
-      release(jj + 1 < my ? chunk_of(jj + 1) : q + it.n);
-      if (jj + 1 >= my) break;
-      if (jj + 2 < my) fetch(ca, jj + 2);
-      F::template compute<1>(acc[0], cb, lds, a, kwi + ((jj + 1) << lkw), lane, xoff, mrow, rowl);
-      release(jj + 2 < my ? chunk_of(jj + 2) : q + it.n);
-    }
-    release(q + it.n);
-    ExecItem ei;
-    ei.tg = it.tg;
-    ei.s = it.piece;
-    ei.np = it.np;
-    if (d.sw)
-      exec_finish<F, true>(d, lds, ei, acc, w, team, false);
-    else
-      exec_finish<F, false>(d, lds, ei, acc, w, team, false);
-    if constexpr (std::is_same<F, FmtFP8>::value) {
-      if (threadIdx.x < a.m) amax[threadIdx.x] = 0u;  // for the next staging
-    }
-    team.sync();  // the next item overwrites scales, partial sums and maybe the activation
-    q += it.n;
-  }
-}
-
-// Compute and loader waves per workgroup the ring executor is built for: 8, 10 or 12 waves
-// (at most three per SIMD, so each wave keeps 168 registers).
-bool ring_shape_ok(int waves, int loaders) {
-  return (waves == 4 && (loaders == 4 || loaders == 6)) || (waves == 8 && loaders == 4);
-}
-
-template <class F, int NC, int NL>
-const void* ring_fn2(bool dlds) {
-  return dlds ? reinterpret_cast<const void*>(&ring_kernel<F, NC, NL, true>)
-              : reinterpret_cast<const void*>(&ring_kernel<F, NC, NL, false>);
+// Compute and poller waves the executor is built for: 8 compute waves alone, or 4 with 0, 2 or
+// 4 pollers (at most two waves per SIMD: beside 8 compute waves, pollers would leave each
+// wave 168 registers and the compute path spills).
+bool stack_shape_ok(int waves, int pollers) {
+  return (waves == 8 && pollers == 0) || (waves == 4 && (pollers == 0 || pollers == 2 || pollers == 4));
 }
 
 template <class F>
-const void* ring_fn(int waves, int loaders, bool dlds) {
-  if (waves == 8) return ring_fn2<F, 8, 4>(dlds);
-  return loaders == 6 ? ring_fn2<F, 4, 6>(dlds) : ring_fn2<F, 4, 4>(dlds);
+const void* stack_fn(int waves, int pollers, bool dlds) {
+  if (waves == 8) return stack_fn2<F, 8, 0>(dlds);
+  if (pollers == 2) return stack_fn2<F, 4, 2>(dlds);
+  if (pollers == 4) return stack_fn2<F, 4, 4>(dlds);
+  return stack_fn2<F, 4, 0>(dlds);
 }
 
-const void* ring_fn_for(int fmt, int waves, int loaders, bool dlds) {
-  if (!ring_shape_ok(waves, loaders)) return nullptr;
+const void* stack_fn_for(int fmt, int waves, int pollers, bool dlds) {
+  if (!stack_shape_ok(waves, pollers)) return nullptr;
   switch (fmt) {
-    case QLX_FMT_W8A16: return ring_fn<FmtW8>(waves, loaders, dlds);
-    case QLX_FMT_W4A16: return ring_fn<FmtW4>(waves, loaders, dlds);
-    case QLX_FMT_FP8: return ring_fn<FmtFP8>(waves, loaders, dlds);
-    default: return nullptr;
-  }
-}
-
-const void* stack_fn_for(int fmt, int waves, bool dlds) {
-  switch (fmt) {
-    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, dlds);
-    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, dlds);
-    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, dlds);
+    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, pollers, dlds);
+    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, pollers, dlds);
+    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, pollers, dlds);
     default: return nullptr;
   }
 }
@@ -902,14 +708,10 @@ int check_shares(int groups, int ns, int U, int pe, int gran, int sps) {
 // 2 KB in every executor format), a fixed charge per item, and one extra dependency trip
 // when row blocks are cut into pieces.
 bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, int waves, int force_kw,
-                     int lds_limit, bool ring, StackPlan& out) {
-  // Where every wave loads its own weights, an item costs about one memory round trip more
-  // than its bytes (staging, epilogue) and a cut row block one more dependency trip: ~4 us,
-  // ~128 KB of one workgroup's stream. With loader waves the stream does not stop for either:
-  // an item costs its barriers and epilogue (~1 us), a cut row block the reducer's wait; and
-  // every workgroup streams all the time, so a projection is spread over all of them (the
-  // same workgroups would otherwise carry the extra work in every layer).
-  const double kStepBytes = 2048.0, kItemBytes = ring ? 24576.0 : 131072.0, kPieceBytes = ring ? 49152.0 : 98304.0;
+                     int lds_limit, StackPlan& out) {
+  // An item costs about one memory round trip more than its bytes (staging, epilogue) and a
+  // cut row block one more dependency trip: ~4 us, ~128 KB of one workgroup's stream.
+  const double kStepBytes = 2048.0, kItemBytes = 131072.0, kPieceBytes = 98304.0;
   const int ns = k / fi.kstep;
   const int ntiles = n / 16;
   double best = 1e300;
@@ -926,7 +728,7 @@ bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, in
       // with fewer block-steps than workgroups, a few pieces per row block.
       long long cand[8];
       int nc = 0;
-      for (int div = 1; div <= (ring ? 1 : 8); div *= 2) cand[nc++] = U < P / div ? U : P / div;
+      for (int div = 1; div <= 8; div *= 2) cand[nc++] = U < P / div ? U : P / div;
       for (int np = 2; np <= kMaxPieces; ++np) cand[nc++] = !whole && groups * np < U ? (long long)groups * np : 0;
       for (int ci = 0; ci < nc; ++ci) {
         const int pe = (int)cand[ci];
@@ -979,22 +781,19 @@ extern "C" {
 int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
-                    int loaders, int ring_chunks, void* desc, qlx_plan* plans, void* arena,
-                    long long* arena_bytes, qlx_stack_launch* launch) {
-  QLX_REQUIRE(stack_fn_for(fmt, 8, false) != nullptr,
+                    int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
+                    qlx_stack_launch* launch) {
+  QLX_REQUIRE(stack_fn_for(fmt, 8, 0, false) != nullptr,
               "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
   QLX_REQUIRE(m >= 1 && m <= 16, "the decode executor serves m = 1..16 (got %d)", m);
   QLX_REQUIRE(calls != nullptr && ncalls >= 1, "no projections");
   QLX_REQUIRE(groups_per_cu >= 1 && groups_per_cu <= 4, "groups_per_cu must be 1..4");
-  QLX_REQUIRE(loaders == -1 || loaders == 0 || loaders == 4 || loaders == 6, "loaders must be -1, 0, 4 or 6 (got %d)",
-              loaders);
-  QLX_REQUIRE(ring_chunks == 0 || (ring_chunks >= kRingMinChunks && (ring_chunks & (ring_chunks - 1)) == 0),
-              "ring_chunks must be 0 or a power of two >= %d (got %d)", kRingMinChunks, ring_chunks);
-  if (loaders < 0) loaders = groups_per_cu == 1 ? (waves == 4 ? 6 : 4) : 0;
-  QLX_REQUIRE(loaders == 0 || (ring_shape_ok(waves, loaders) && groups_per_cu == 1),
-              "loader waves: 4 compute waves with 4 or 6 loaders, or 8 with 4, and one lane (waves=%d, loaders=%d, "
-              "groups_per_cu=%d)", waves, loaders, groups_per_cu);
+  QLX_REQUIRE(pollers == -1 || pollers == 0 || pollers == 2 || pollers == 4, "pollers must be -1, 0, 2 or 4 (got %d)",
+              pollers);
+  if (pollers < 0) pollers = waves == 4 ? 4 : 0;
+  QLX_REQUIRE(stack_shape_ok(waves, pollers), "poller waves run beside 4 compute waves (waves=%d, pollers=%d)", waves,
+              pollers);
   const FmtInfo fi = stack_info(fmt);
   // Shapes, and which earlier projection (if any) produces each activation. Outputs may not
   // overlap each other or an activation read from memory: the chain has no ordering between
@@ -1035,57 +834,33 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return hip_status(e, "stack_build");
   std::vector<StackPlan> sp(ncalls);
-  int lds = 0, lanes = groups_per_cu, desc_lds = -1;
-  int ctl_off = 0, ring_off = 0, rchunks = 0;
+  int lds = 0, lanes = groups_per_cu, desc_lds = -1, amax_off = 0;
   const int P = cus;  // workgroups per lane
   const long long desc_bytes = (long long)ncalls * sizeof(StackDesc);
   // Plan for P workgroups, then shrink P to what fits the CUs with that LDS; repeat until
-  // plan and grid agree.
-  // Item LDS may take what the weight ring (at least 32 slots, or the requested size) leaves.
-  const int item_limit =
-      loaders ? kLdsLimit - kCtlBytes - 1024 - (ring_chunks ? ring_chunks : kRingMinChunks) * 1024 : kLdsLimit;
+  // plan and grid agree. LDS: [items][64 B of FP8 row maxima][descriptors, if they fit].
   for (int round = 0;; ++round) {
     QLX_REQUIRE(round < 4, "no stable executor grid");
     int items_lds = 0;
     for (int c = 0; c < ncalls; ++c) {
       const qlx_stack_call& q = calls[c];
-      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, item_limit, loaders > 0, sp[c]),
+      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c]),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
       GemmArgs a = {};
       const int l = exec_lds(fi, sp[c].plan, m, q.n, q.k, a);
       if (l > items_lds) items_lds = l;
     }
-    items_lds = (items_lds + 15) & ~15;
-    const void* fn = nullptr;
-    if (loaders == 0) {
-      desc_lds = items_lds + desc_bytes <= kLdsLimit ? items_lds : -1;
-      lds = desc_lds >= 0 ? (int)(items_lds + desc_bytes) : items_lds;
-      fn = stack_fn_for(fmt, waves, desc_lds >= 0);
-    } else {
-      // [items][counters][ring][descriptors, if the ring keeps >= 32 slots beside them]
-      ctl_off = items_lds;
-      ring_off = (ctl_off + kCtlBytes + 1023) & ~1023;
-      auto fit = [&](long long room) {
-        int r = 0;
-        for (int c = kRingMinChunks; (long long)c * 1024 <= room; c *= 2) r = c;
-        return ring_chunks ? (ring_chunks * 1024LL <= room ? ring_chunks : 0) : r;
-      };
-      // Descriptors go to LDS only beside a ring of 128 slots (or the requested size): a
-      // deeper ring hides longer dependency waits than descriptor reads cost.
-      rchunks = fit(kLdsLimit - ring_off - desc_bytes);
-      desc_lds = rchunks >= (ring_chunks ? ring_chunks : 128) ? ring_off + rchunks * 1024 : -1;
-      if (desc_lds < 0) rchunks = fit(kLdsLimit - ring_off);
-      QLX_REQUIRE(rchunks >= kRingMinChunks, "the executor's weight ring does not fit beside %d bytes of item LDS",
-                  items_lds);
-      lds = ring_off + rchunks * 1024 + (desc_lds >= 0 ? (int)desc_bytes : 0);
-      fn = ring_fn_for(fmt, waves, loaders, desc_lds >= 0);
-    }
+    amax_off = (items_lds + 15) & ~15;
+    const int items_end = amax_off + 64;
+    desc_lds = items_end + desc_bytes <= kLdsLimit ? items_end : -1;
+    lds = desc_lds >= 0 ? (int)(items_end + desc_bytes) : items_end;
+    const void* fn = stack_fn_for(fmt, waves, pollers, desc_lds >= 0);
     if (lds > 64 * 1024) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       if (e != hipSuccess) return hip_status(e, "stack_build");
     }
     int occ = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (waves + loaders) * 64, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (waves + pollers) * 64, lds);
     if (e != hipSuccess) return hip_status(e, "stack_build");
     QLX_REQUIRE(occ >= 1, "the executor does not fit a CU with %d bytes of LDS", lds);
     if (occ >= lanes) break;
@@ -1122,7 +897,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       d.ywire = wire_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[c]) : nullptr;
       d.part = part_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + part_off[c]) : nullptr;
       d.xwire = src[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[src[c]]) : nullptr;
-      d.xpitch = src[c] >= 0 ? nout(src[c]) / 2 : 0;
+      d.xpitch = src[c] >= 0 ? nout(src[c]) : 0;
     }
     d.units = sp[c].units;
     d.nwg = P;
@@ -1146,50 +921,33 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     launch->lds_bytes = lds;
     launch->waves = waves;
     launch->desc_lds = desc_lds;
-    launch->loaders = loaders;
-    launch->ring_off = ring_off;
-    launch->ring_chunks = rchunks;
-    launch->ctl_off = ctl_off;
-    launch->inflight = loaders ? kLoaderDepth : 0;
+    launch->pollers = pollers;
+    launch->amax_off = amax_off;
   }
   return QLX_OK;
 }
 
 int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
                   int* error, long long budget_us, void* stream) {
-  QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1,
+  QLX_REQUIRE(launch != nullptr && stack_shape_ok(launch->waves, launch->pollers) && launch->grid >= 1,
               "bad executor launch configuration");
-  const int loaders = launch->loaders;
-  QLX_REQUIRE(loaders == 0 || ring_shape_ok(launch->waves, loaders), "bad executor loaders");
-  const void* fn = loaders ? ring_fn_for(fmt, launch->waves, loaders, launch->desc_lds >= 0)
-                           : stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0);
+  const void* fn = stack_fn_for(fmt, launch->waves, launch->pollers, launch->desc_lds >= 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(desc && error && ncalls >= 1, "bad executor arguments");
   QLX_REQUIRE(launch->desc_lds < 0 || launch->desc_lds + (long long)ncalls * (long long)sizeof(StackDesc) <=
                                           launch->lds_bytes,
               "descriptor copy does not fit the launch's LDS");
-  QLX_REQUIRE(epoch != 0, "epoch 0 is reserved (a zeroed arena carries it)");
+  QLX_REQUIRE(launch->amax_off >= 0 && launch->amax_off % 16 == 0 && launch->amax_off + 64 <= launch->lds_bytes,
+              "bad executor LDS layout");
+  QLX_REQUIRE((epoch & 0xffffu) != 0, "epoch %u: its low 16 bits tag published values and must not be 0 "
+              "(a zeroed arena carries tag 0)", epoch);
   QLX_REQUIRE(budget_us >= 0 && budget_us <= 600000000LL, "budget_us must be 0..600e6");
   long long ticks = budget_us * 100;  // the real-time counter runs at 100 MHz
-  int desc_off = launch->desc_lds, lanes = launch->lanes;
+  int desc_off = launch->desc_lds, lanes = launch->lanes, amax_off = launch->amax_off;
   QLX_REQUIRE(lanes >= 1 && launch->grid % lanes == 0, "bad executor lanes");
-  if (loaders) {
-    const int rc = launch->ring_chunks, ctl = launch->ctl_off, ro = launch->ring_off;
-    QLX_REQUIRE(lanes == 1 && rc >= kRingMinChunks && (rc & (rc - 1)) == 0 && ctl >= 0 && ctl + kCtlBytes <= ro &&
-                    ro % 1024 == 0 && (long long)ro + rc * 1024LL <= launch->lds_bytes &&
-                    (launch->desc_lds < 0 || launch->desc_lds >= ro + rc * 1024),
-                "bad ring executor launch configuration");
-    uint32_t rmask = (uint32_t)rc - 1;
-    int ctl_off = ctl, ring_off = ro;
-    void* args[] = {(void*)&desc,     (void*)&ncalls,  (void*)&epoch,    (void*)&error, (void*)&ticks,
-                    (void*)&desc_off, (void*)&ctl_off, (void*)&ring_off, (void*)&rmask};
-    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3((launch->waves + loaders) * 64), args,
-                                              (unsigned)launch->lds_bytes, (hipStream_t)stream);
-    return hip_status(e, "stack_run");
-  }
-  void* args[] = {(void*)&desc, (void*)&ncalls, (void*)&epoch, (void*)&error, (void*)&ticks, (void*)&desc_off,
-                  (void*)&lanes};
-  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3(launch->waves * 64), args,
+  void* args[] = {(void*)&desc,     (void*)&ncalls, (void*)&epoch,   (void*)&error,
+                  (void*)&ticks,    (void*)&desc_off, (void*)&lanes, (void*)&amax_off};
+  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3((launch->waves + launch->pollers) * 64), args,
                                             (unsigned)launch->lds_bytes, (hipStream_t)stream);
   return hip_status(e, "stack_run");
 }

@@ -41,11 +41,10 @@ class StackCall(ctypes.Structure):
 
 
 class StackLaunch(ctypes.Structure):
-    """``qlx_stack_launch``: grid, LDS bytes, compute waves, descriptor LDS offset, lanes, and the
-    weight ring of the loader waves (loaders, ring offset, slots, counter offset, loads in flight)."""
+    """``qlx_stack_launch``: grid, LDS bytes, compute waves, descriptor LDS offset, lanes, poller
+    waves, and the LDS offset of the pollers' FP8 row maxima."""
 
-    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "loaders",
-                                            "ring_off", "ring_chunks", "ctl_off", "inflight")]
+    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "pollers", "amax_off")]
 
 
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
@@ -80,7 +79,7 @@ SIGNATURES = {
     "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
     "qlx_stack_desc_size": ([], _I),
-    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
+    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
                          ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),

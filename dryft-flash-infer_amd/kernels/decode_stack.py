@@ -36,17 +36,19 @@ BUDGET_US = 2_000_000
 class DecodeStack:
     """An ordered chain of projections of one format, for m = 1..16 tokens.
 
-    ``loaders`` (4 or 6 beside 4 compute waves, 4 beside 8) adds waves per workgroup that only copy weights into an LDS ring of
-    ``ring_chunks`` 1 KB slots (0: the most that fits), so the weight stream never waits for
-    an activation; 0 lets every compute wave load its own weights."""
+    Each workgroup has ``waves`` compute waves and ``pollers`` (0, 2 or 4) waves that only
+    read the activations earlier projections publish: a compute wave's read would wait for the
+    weight loads it keeps in flight."""
 
-    def __init__(self, fmt, m, waves=8, groups_per_cu=1, loaders=0, ring_chunks=0):
+    def __init__(self, fmt, m, waves=8, groups_per_cu=1, pollers=0):
         if fmt not in _FMTS:
             raise ValueError(f"the decode executor serves {sorted(_FMTS)}, not {fmt!r}")
         if not 1 <= m <= 16:
             raise ValueError(f"the decode executor serves m = 1..16 (got {m})")
+        if pollers not in (0, 2, 4):
+            raise ValueError(f"pollers must be 0, 2 or 4 (got {pollers})")
         self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
-        self.loaders, self.ring_chunks = loaders, ring_chunks
+        self.pollers = pollers
         self.calls, self._keep = [], []
         self.desc = None
         self.epoch = 0
@@ -86,7 +88,7 @@ class DecodeStack:
         fmt = _FMTS[self.fmt]
         arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
-            opts = (self.waves, self.groups_per_cu, self.loaders, self.ring_chunks)
+            opts = (self.waves, self.groups_per_cu, self.pollers)
             _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), *opts, None, None, None, arena_bytes,
                                            launch), "qlx_stack_build")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
@@ -108,7 +110,7 @@ class DecodeStack:
         """Run the whole chain once on the current stream."""
         if self.desc is None:
             self.build()
-        self.epoch = self.epoch % 0xFFFFFFFF + 1  # nonzero, new every run
+        self.epoch = self.epoch % 0xFFFF + 1  # its low 16 bits tag published values: 1..65535
         _lib.call("qlx_stack_run", _FMTS[self.fmt], _lib.ptr(self.desc), len(self.calls), ctypes.byref(self.launch),
                   self.epoch, _lib.ptr(self.error), int(budget_us), _lib.stream(self.device))
 
@@ -118,8 +120,8 @@ class DecodeStack:
         return bool(self.error.item())
 
     #: The kinds of wait, by bit of the error word: an activation from an earlier projection, a
-    #: piece's partial sums, the compute waves' barrier, a weight chunk in the ring, a free ring slot.
-    WAIT_SITES = ("input", "partial", "team", "chunk", "slot")
+    #: piece's partial sums.
+    WAIT_SITES = ("input", "partial")
 
     def failed_waits(self):
         """The kind of the first wait that gave up (a list; empty if none did)."""

@@ -222,42 +222,36 @@ typedef struct qlx_stack_launch {
   int waves;       /* compute waves per workgroup */
   int desc_lds;    /* byte offset of the descriptors' LDS copy, or -1 (read from memory) */
   int lanes;       /* workgroup sets: lane l runs projections l, l + lanes, ... */
-  int loaders;     /* weight-loading waves per workgroup (0: every wave loads its own weights) */
-  int ring_off;    /* LDS byte offset of the loaders' weight ring */
-  int ring_chunks; /* 1 KB slots of the ring (a power of two) */
-  int ctl_off;     /* LDS byte offset of the ring's counters */
-  int inflight;    /* loads each loader wave keeps in flight */
+  int pollers;     /* waves per workgroup that only read and stage published activations */
+  int amax_off;    /* LDS byte offset of the pollers' per-token FP8 maxima (64 bytes) */
 } qlx_stack_launch;
 
 /* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
  * for the executor: workgroups of `waves` (4 or 8) compute waves, `groups_per_cu` lanes of one
  * workgroup per CU (1..4; fewer if registers or LDS do not allow), lane l running projections
- * l, l + lanes, ... concurrently with the other lanes. `loaders` (1 or 2; needs waves 8 and
- * one lane) adds that many waves per workgroup that only copy weights into an LDS ring of
- * `ring_chunks` 1 KB slots (a power of two >= 32, or 0 for the most that fits), so the weight
- * stream does not wait for activations; 0 lets every wave load its own weights; -1 lets the
- * library choose. Writes the
- * descriptors to host memory `desc` (ncalls * qlx_stack_desc_size() bytes; NULL to only size)
- * and, if `plans` is not NULL, each projection's plan (waves, kw; splits = the most K pieces
- * of one row block). The chain keeps published outputs and partial sums in `arena`
- * (*arena_bytes of device memory, zeroed once before the first run): call once with desc and
- * arena NULL to size it, then again with both. Outputs must not overlap each other or an
- * input read from memory (EINVAL otherwise). Replaces the reference's per-projection launches
- * chained by programmatic dependent launch inside a captured graph
- * (engine/kernels/cuda_fp8.py:47-50, 150-169; engine/kernels/cuda_jit.py:218-262): here the
- * whole chain is one cooperative launch. */
+ * l, l + lanes, ... concurrently with the other lanes. `pollers` (0, 2 or 4; -1 lets the
+ * library choose) adds that many waves per workgroup that only read the activations earlier
+ * projections publish and stage them, so those reads never wait behind weight loads (0: the
+ * compute waves read them). Writes the descriptors to host memory `desc`
+ * (ncalls * qlx_stack_desc_size() bytes; NULL to only size) and, if `plans` is not NULL, each
+ * projection's plan (waves, kw; splits = the most K pieces of one row block). The chain keeps
+ * published outputs and partial sums in `arena` (*arena_bytes of device memory, zeroed once
+ * before the first run): call once with desc and arena NULL to size it, then again with both.
+ * Outputs must not overlap each other or an input read from memory (EINVAL otherwise).
+ * Replaces the reference's per-projection launches chained by programmatic dependent launch
+ * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
+ * engine/kernels/cuda_jit.py:218-262): here the whole chain is one cooperative launch. */
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
-                    int loaders, int ring_chunks, void* desc, qlx_plan* plans, void* arena,
-                    long long* arena_bytes, qlx_stack_launch* launch);
+                    int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
+                    qlx_stack_launch* launch);
 
 /* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors and `launch` its
- * launch configuration. `epoch` must be
- * nonzero and differ from the previous run's on the same arena (a counter). `error` is one
- * int32 in device memory, zero before the run: once a wait passes `budget_us` microseconds from
- * the run's start, every wait gives up, the first one writing (1 << kind) to it (0: an input
- * from an earlier projection, 1: a piece's partial sums, 2: the compute waves' barrier, 3: a
- * weight chunk, 4: a free ring slot), and that run's outputs are undefined. Runs sharing an
- * arena must not overlap. */
+ * launch configuration. The low 16 bits of `epoch` tag the values the run publishes: they must
+ * be nonzero and differ from the previous run's on the same arena (a counter over 1..65535).
+ * `error` is one int32 in device memory, zero before the run: once a wait passes `budget_us`
+ * microseconds from the run's start, every wait gives up, the first one writing (1 << kind) to
+ * it (0: an input from an earlier projection, 1: a piece's partial sums), and that run's
+ * outputs are undefined. Runs sharing an arena must not overlap. */
 int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
                   int* error, long long budget_us, void* stream);
 

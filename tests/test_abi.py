@@ -123,9 +123,9 @@ def test_decode_stack_contract_on_host():
     assert lib.qlx_stack_desc_size() >= 128
     out = [ctypes.c_longlong(0), ctypes.byref(_lib.StackLaunch())]
 
-    def build(fmt, m, calls, gpc=1, waves=8, loaders=0, ring=0):
+    def build(fmt, m, calls, gpc=1, waves=8, pollers=0):
         arr = (_lib.StackCall * max(len(calls), 1))(*calls)
-        return lib.qlx_stack_build(fmt, m, arr, len(calls), waves, gpc, loaders, ring, None, None, None, *out)
+        return lib.qlx_stack_build(fmt, m, arr, len(calls), waves, gpc, pollers, None, None, None, *out)
 
     ok = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 0)
     assert build(_lib.FMT_REF8, 1, [ok]) == _lib.QLX_EINVAL
@@ -133,13 +133,10 @@ def test_decode_stack_contract_on_host():
     assert build(_lib.FMT_W4A16, 1, []) == _lib.QLX_EINVAL
     assert build(_lib.FMT_FP8, 1, [ok], gpc=5) == _lib.QLX_EINVAL
     assert build(_lib.FMT_FP8, 1, [ok], waves=6) == _lib.QLX_EINVAL
-    # loader waves: 4 or 6 beside 4 compute waves, 4 beside 8, one lane; ring sizes are powers
-    # of two >= 32
-    assert build(_lib.FMT_FP8, 1, [ok], loaders=3) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], loaders=6, waves=8) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], loaders=4, gpc=2) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], loaders=4, ring=48) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], loaders=4, ring=16) == _lib.QLX_EINVAL
+    # poller waves: 0, 2 or 4, and only beside 4 compute waves
+    assert build(_lib.FMT_FP8, 1, [ok], waves=4, pollers=3) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_FP8, 1, [ok], waves=8, pollers=4) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_FP8, 1, [ok], waves=4, pollers=6) == _lib.QLX_EINVAL
     bad_k = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 500, _lib.MODE_BF16, 0)
     assert build(_lib.FMT_W8A16, 1, [bad_k]) == _lib.QLX_EINVAL
     bad_kw = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 3)
@@ -155,17 +152,19 @@ def test_decode_stack_contract_on_host():
             DecodeStack(fmt, m)
     with pytest.raises(ValueError):
         DecodeStack("w8a16", 1).build()
-    launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 0, 0, 0, 0)
+    launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 0)
     assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, launch, 1, None, 10, None) == _lib.QLX_EINVAL
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, 0, 1 << 21, 10, None) == _lib.QLX_EINVAL
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0, 0, 0, 0, 0)  # descriptor copy past the LDS
+    bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0, 0)  # descriptor copy past the LDS
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    # a ring past the LDS, a ring that is no power of two, 6 loaders beside 8 compute waves, a
-    # ring below 32 slots
-    for ring in ((4, 45056, 32, 256, 8), (4, 1024, 48, 256, 8), (6, 1024, 32, 256, 8), (4, 1024, 16, 256, 8)):
-        bad = _lib.StackLaunch(256, 65536, 8, -1, 1, *ring)
+    # pollers beside 8 compute waves; FP8 row maxima past the LDS or misaligned; an epoch whose
+    # low 16 bits (the tag of published values) are 0
+    for shape in ((8, 4, 0), (4, 4, 1020), (4, 4, 8)):
+        bad = _lib.StackLaunch(256, 1024, shape[0], -1, 1, shape[1], shape[2])
         assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    good = _lib.StackLaunch(256, 1024, 4, -1, 1, 4, 0)
+    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, good, 1 << 16, 1 << 21, 10, None) == _lib.QLX_EINVAL
 
 
 def test_selection_api_mirrors_the_reference():

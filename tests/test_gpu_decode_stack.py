@@ -53,11 +53,11 @@ def source(bufs, src):
     return bufs[src]
 
 
-def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, loaders=0, ring_chunks=0):
+def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, pollers=0):
     quant = qlinear.FORMATS[fmt][0]
     bufs = {"x": rand((m, 1024), seed).to(DEV), "g": rand((m, 9728), seed + 1).to(DEV)}
     weights, raw = {}, {}
-    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes, loaders=loaders, ring_chunks=ring_chunks)
+    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes, pollers=pollers)
     for idx, (name, n, k, src, sw) in enumerate(CHAIN):
         w = rand((n, k), seed + 10 + idx, std=0.02).to(DEV)
         packed = quant(w)
@@ -100,9 +100,9 @@ def oracle_check(fmt, x_bits, packed, y):
     return O.rel_l2(y.float().cpu().numpy(), ref)
 
 
-def run_chain_checks(fmt, m, waves=8, loaders=0, ring_chunks=0):
-    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m, waves=waves, loaders=loaders, ring_chunks=ring_chunks)
-    assert chain.grid >= 256 and chain.lds > 0 and chain.launch.loaders == loaders
+def run_chain_checks(fmt, m, waves=8, pollers=0):
+    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m, waves=waves, pollers=pollers)
+    assert chain.grid >= 256 and chain.lds > 0 and chain.launch.pollers == pollers
     for run in range(3):
         if run:
             bufs["x"].copy_(rand((m, 1024), 7 * run + m).to(DEV))
@@ -129,27 +129,28 @@ def test_chain_matches_single_calls_and_oracle(fmt, m):
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
-@pytest.mark.parametrize("m,waves,loaders,ring", [(1, 4, 6, 0), (5, 4, 4, 0), (16, 8, 4, 0), (1, 4, 6, 32),
-                                                  (2, 8, 4, 32)])
-def test_ring_chain_matches_single_calls_and_oracle(fmt, m, waves, loaders, ring):
-    """Loader waves feeding the compute waves through the LDS weight ring (32 slots, the
-    least allowed: the ring wraps many times per item) give the same results as the
-    single-call linears."""
-    print(f"decode stack ring {fmt} m={m} waves={waves} loaders={loaders} ring={ring}", flush=True)
-    run_chain_checks(fmt, m, waves=waves, loaders=loaders, ring_chunks=ring)
+@pytest.mark.parametrize("m,pollers", [(1, 4), (5, 2), (16, 4)])
+def test_poller_chain_matches_single_calls_and_oracle(fmt, m, pollers):
+    """Poller waves staging the activations (m = 16 at FP8: more than one pass over each row
+    for the token maxima) give the same results as the single-call linears."""
+    print(f"decode stack pollers {fmt} m={m} pollers={pollers}", flush=True)
+    run_chain_checks(fmt, m, waves=4, pollers=pollers)
 
 
 @pytest.mark.parametrize("kw", [1, 2, 4, 8])
-@pytest.mark.parametrize("loaders", [0, 4])
-def test_every_tile_split_is_exact(kw, loaders):
+@pytest.mark.parametrize("pollers", [0, 4])
+def test_every_tile_split_is_exact(kw, pollers):
     """Forced waves-per-tile settings change the pieces, not the results' bound."""
-    print(f"decode stack kw={kw} loaders={loaders}", flush=True)
-    chain, bufs, weights, _ = build_chain("fp8" if loaders else "w4a16", 3, 77, kw=kw, loaders=loaders)
+    print(f"decode stack kw={kw} pollers={pollers}", flush=True)
+    if pollers and kw == 8:
+        pytest.skip("8 waves per tile needs 8 compute waves, which take no pollers")
+    fmt = "fp8" if pollers else "w4a16"
+    chain, bufs, weights, _ = build_chain(fmt, 3, 77, kw=kw, waves=4 if pollers else 8, pollers=pollers)
     assert all(c[1] == kw for c in chain.configs)
     chain.run()
     torch.cuda.synchronize()
     assert not chain.failed()
-    check_against_single_calls("fp8" if loaders else "w4a16", bufs, weights, ("kw", kw, loaders))
+    check_against_single_calls(fmt, bufs, weights, ("kw", kw, pollers))
 
 
 @pytest.mark.parametrize("fmt,waves,lanes", [("fp8", 4, 3), ("w4a16", 4, 2), ("w8a16", 8, 2)])
@@ -168,13 +169,13 @@ def test_lanes_and_small_workgroups(fmt, waves, lanes):
         check_against_single_calls(fmt, bufs, weights, (fmt, waves, lanes, run))
 
 
-@pytest.mark.parametrize("waves,loaders", [(8, 0), (4, 6)])
-def test_bounded_wait_gives_up_and_recovers(waves, loaders):
+@pytest.mark.parametrize("waves,pollers", [(8, 0), (4, 4)])
+def test_bounded_wait_gives_up_and_recovers(waves, pollers):
     """A zero wait budget makes the waits give up (forced from the host): the kernel still
     ends, flags the run, and after reset() a normal run is right again."""
     m = 2
-    print(f"decode stack bounded wait waves={waves} loaders={loaders}", flush=True)
-    chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves, loaders=loaders)
+    print(f"decode stack bounded wait waves={waves} pollers={pollers}", flush=True)
+    chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves, pollers=pollers)
     chain.run(budget_us=0)
     torch.cuda.synchronize()
     assert chain.failed()
