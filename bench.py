@@ -35,7 +35,7 @@ LAYERS = 36
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
-EXECUTOR_SHAPES = ((8, 0), (4, 0), (4, 2), (4, 4))  # (compute waves, poller waves)
+EXECUTOR_SHAPES = ((8, 0), (4, 4))  # (compute waves, poller waves)
 
 
 def log(*a):
