@@ -296,6 +296,44 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
     return stack, out
 
 
+PEAK_BF16_MFMA = 2.5e15  # dense bf16 MFMA, MI355X
+
+
+def measure_config4(reps, layers=LAYERS):
+    """W4A16 g128 gate_up (2 x 9728 rows, fused SwiGLU) then down, at
+    M = 16, 32, 64 (the skinny GEMM), over `layers` distinct weight pairs (1.4 GB, past the
+    Infinity Cache) replayed as one HIP graph. Per pair: algorithmic bytes (weights + scales,
+    x in, activation out and back in, y out), bf16-equivalent MFMA flops, and both roofline
+    fractions (HBM 8 TB/s; dense bf16 MFMA 2.5 PFLOP/s)."""
+    from kernels import qlinear
+    gen = torch.Generator(device="cuda").manual_seed(4)
+
+    def make(n, k):
+        w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        return qlinear.prepare(qlinear.quantize_w4(w))
+    pairs = [(make(2 * 9728, 2560), make(2560, 9728)) for _ in range(layers)]
+    out = {}
+    for m in (16, 32, 64):
+        x = torch.randn(m, 2560, generator=gen, device="cuda").to(torch.bfloat16)
+
+        def run():
+            for gu, dn in pairs:
+                qlinear.linear_w4a16(qlinear.linear_w4a16(x, gu, swiglu=True), dn)
+        g = graph_of(run)
+        us = median_graph_ms(g, reps, 2, trials=3) / layers * 1e3
+        del g
+        gu, dn = pairs[0]
+        alg = gu.bytes_moved() + dn.bytes_moved() + m * 2 * (2560 + 9728 + 9728 + 2560)
+        flop = 2 * m * (2 * 9728 * 2560 + 2560 * 9728)
+        out[f"M{m}"] = {"us_per_pair": round(us, 2), "alg_MB": round(alg / 1e6, 2),
+                        "TBps": round(alg / us / 1e6, 3), "hbm_frac": round(alg / us / 1e6 / 8.0, 4),
+                        "TFLOPs": round(flop / us / 1e6, 1), "mfma_frac_bf16": round(flop / us * 1e6 / PEAK_BF16_MFMA, 4)}
+        log(f"config 4 M={m}: {us:.1f} us per gate_up+down pair, {alg / us / 1e6:.2f} TB/s, {flop / us / 1e6:.0f} TFLOP/s")
+    del pairs
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +407,7 @@ def main():
             log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s")
             del st
             torch.cuda.empty_cache()
+        extra["config4_w4_gate_up_swiglu_down"] = measure_config4(max(3, args.steps // 4))
 
     line = {
         "metric": METRIC,

@@ -69,6 +69,8 @@ SIGNATURES = {
     "qlx_tile_rows": ([_P, _P, _I, _I, _P], _I),
     "qlx_linear_w8a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_plan_skinny": ([_I, _I, _I, _I, _I, _PLAN], _I),
+    "qlx_linear_skinny": ([_I, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8wo": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),

@@ -142,6 +142,18 @@ int qlx_linear_w8a16(const void* w, const void* w_scale, const void* x, void* y,
 int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
                      int k, int tiled, const qlx_plan* plan, void* stream);
 
+/* Skinny GEMM for 16..64 tokens (speculative verification, small batches), W4A16 or W8A16
+ * in the MI355X tile layout: the activation streams through LDS one K step at a time, shared
+ * by a workgroup's waves; K slices (plan->splits > 1) write fp32 planes to plan->workspace
+ * ([splits][m][n]) that are reduced in slice order (qlx_reduce_planes, or qlx_swiglu for
+ * mode SWIGLU) in the same call. Same arithmetic as qlx_linear_w4a16 / qlx_linear_w8a16.
+ * Serves the batches the reference runs through cuda_fp8.matmul's 8-token tiles
+ * (engine/kernels/cuda_fp8.py:1227-1234, 1316-1330). qlx_plan_skinny fills waves (4 or 8)
+ * and splits for a shape. */
+int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan);
+int qlx_linear_skinny(int fmt, const void* w, const void* w_scale, const void* x, void* y, int m, int n, int k,
+                      const qlx_plan* plan, void* stream);
+
 /* FP8 e4m3 W8A8: per-channel bf16 weight scales, activation quantized per token inside the
  * kernel (same arithmetic as qlx_quantize_fp8_act). Replaces cuda_int8.matmul's role
  * (engine/kernels/cuda_int8.py:251-281) for the north-star FP8 format. */

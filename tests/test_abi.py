@@ -76,6 +76,18 @@ def test_contract_violations_fail_before_any_launch():
     assert lib.qlx_linear_w4a16(None, None, None, None, 65, 256, 512, 0, ctypes.byref(good), None) == _lib.QLX_EINVAL
     assert lib.qlx_quantize_weight(None, None, None, 4, 100, 64, 8, 0, 1, 0, None) == _lib.QLX_EINVAL
     assert lib.qlx_tile_rows(None, None, 17, 128, None) == _lib.QLX_EINVAL
+    # skinny GEMM: W4A16/W8A16 only, m <= 64, whole 16-row tiles; NULL pointers; K slices
+    # without a workspace
+    sk = _lib.Plan()
+    assert lib.qlx_plan_skinny(_lib.FMT_FP8, 0, 16, 256, 512, sk) == _lib.QLX_EINVAL
+    assert lib.qlx_plan_skinny(_lib.FMT_W4A16, 0, 65, 256, 512, sk) == _lib.QLX_EINVAL
+    assert lib.qlx_plan_skinny(_lib.FMT_W4A16, 0, 16, 250, 512, sk) == _lib.QLX_EINVAL
+    assert lib.qlx_plan_skinny(_lib.FMT_W8A16, 0, 16, 2560, 9728, sk) == 0 and sk.waves == 4 and sk.splits > 1
+    assert lib.qlx_linear_skinny(_lib.FMT_W8A16, None, None, None, None, 16, 2560, 9728, ctypes.byref(sk),
+                                 None) == _lib.QLX_EINVAL
+    p = 1 << 20
+    assert lib.qlx_linear_skinny(_lib.FMT_W8A16, p, p, p, p, 16, 2560, 9728, ctypes.byref(sk), None) == _lib.QLX_EINVAL
+    assert "workspace" in _lib.last_error()
 
 
 def test_python_ops_refuse_cpu_tensors():

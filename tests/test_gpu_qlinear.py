@@ -218,6 +218,7 @@ def test_tiled_weights_match_oracle_and_row_major_bitwise(fmt):
     raw = packed[0].view(torch.uint8).cpu().numpy() if fmt == "fp8" else packed[0].cpu().numpy()
     want = O.tile_rows(raw)
     assert np.array_equal(tiled.weight.cpu().view(torch.uint8).numpy().reshape(want.shape), want)
+    same_kernel = {} if fmt == "fp8" else {"skinny": False}  # tiled batches > 8 default to the skinny GEMM
     for m in (1, 8, 33):
         x = acts(m, k, 600 + m).to(DEV)
         for cfg in (None, (4, 4, 1, 2), (8, 2, 2, 1)):
@@ -227,5 +228,40 @@ def test_tiled_weights_match_oracle_and_row_major_bitwise(fmt):
                 except ValueError as exc:
                     assert "LDS" in str(exc)
                     continue
-                b = linear(x, tiled, config=cfg, swiglu=sw)
+                b = linear(x, tiled, config=cfg, swiglu=sw, **same_kernel)
                 assert torch.equal(a, b), (fmt, m, cfg, sw)
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16"])
+@pytest.mark.parametrize("n,k,sw", [(2 * 2048, 2560, True), (2560, 9728, False), (4112, 1024, False)])
+def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
+    """The skinny GEMM (the default for tile-layout weights from 9 tokens): K slices with fp32
+    planes where row groups are few (2560 x 9728), a partial last workgroup (257 tiles), the
+    SwiGLU epilogue. Against the decode kernel on the same weights, within one bf16 rounding
+    step (the same products, summed in another order), and against the oracle's
+    dequantize-then-matmul (rel-L2 <= 1e-2); a zero weight row gives exactly zero."""
+    print(f"skinny {fmt} n={n} k={k} swiglu={sw}", flush=True)
+    quant, linear, _ = qlinear.FORMATS[fmt]
+    w = weights(n, k, 40)
+    packed = quant(w.to(DEV))
+    tiled = qlinear.prepare(packed)
+    q, s = packed
+    if fmt == "w4a16":
+        deq = O.dequantize(O.unpack_int4_k32(q.cpu().numpy()), bits16(s), bits=4, scale_dtype="bf16")
+    else:
+        deq = O.dequantize(q.cpu().numpy(), bits16(s)[:, None], bits=8, scale_dtype="bf16", storage="signed")
+    for m in (9, 17, 33, 64):
+        x = acts(m, k, 700 + m).to(DEV)
+        ys = linear(x, tiled, swiglu=sw)
+        yd = linear(x, tiled, swiglu=sw, skinny=False)
+        want = yd.float()
+        diff = (ys.float() - want).abs()
+        rowmax = want.abs().amax(dim=1, keepdim=True)
+        tol = (2.0 ** -6 if sw else 2.0 ** -7) * want.abs() + 2.0 ** -9 * rowmax
+        assert (diff > tol).sum().item() == 0, (fmt, n, k, m, diff.max().item())
+        ref = O.linear_dequant(bits16(x), deq)
+        if sw:
+            ref = O.bf16_to_f32(O.swiglu(O.f32_to_bf16(ref.astype(np.float32))))
+        assert O.rel_l2(ys.float().cpu().numpy(), ref) <= 1e-2, (fmt, n, k, m)
+        if not sw:
+            assert not ys[:, 0].float().abs().sum().item(), "zero weight row must give zero"
