@@ -343,6 +343,9 @@ def main():
     ap.add_argument("--m", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline stack only")
+    ap.add_argument("--only-config4", action="store_true",
+                    help="only BASELINE config 4 (W4 gate_up+SwiGLU then down, M = 16, 32, 64): one JSON line "
+                         "of its figures, for profiling the skinny GEMM (not the driver's line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
@@ -354,6 +357,9 @@ def main():
     from kernels import _lib
     _lib.lib()
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.only_config4:
+        print(json.dumps({"config4_w4_gate_up_swiglu_down": measure_config4(max(3, args.steps // 4))}), flush=True)
+        return
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
     log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
