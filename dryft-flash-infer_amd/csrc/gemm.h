@@ -740,6 +740,21 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
   }
 }
 
+// FP8 W8A8 prologue from an activation quantized beforehand (qlx_quantize_fp8_act: the same
+// per-token scale and codes the in-kernel prologue computes): the slice's e4m3 codes and the
+// token scales are copied, so no workgroup reads whole rows for the maxima.
+__device__ __forceinline__ void stage_fp8_pre(const GemmArgs& a, char* lds, int step0, int nst) {
+  const uint8_t* xq = reinterpret_cast<const uint8_t*>(a.x);
+  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+  for (int i = threadIdx.x; i < a.m; i += blockDim.x) sx[i] = a.xs[i];
+  const int cps = nst * 8;  // 16-byte chunks of a row's slice (128 codes per step)
+  for (int q = threadIdx.x; q < a.m * cps; q += blockDim.x) {
+    const int mm = q / cps, kc = q - mm * cps;
+    const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(xq + (size_t)mm * a.k + step0 * 128 + kc * 16));
+    *reinterpret_cast<u32x4*>(lds + mm * a.xstride + kc * 16) = v;
+  }
+}
+
 // cuda_int8 prologue: int8 activation slice and its fp32 group scales.
 __device__ void stage_int8_act(const GemmArgs& a, char* lds, int step0, int nst) {
   const int cps = nst * 8;
@@ -883,7 +898,12 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
 
   // ---- prologue
   if constexpr (std::is_same<F, FmtFP8>::value) {
-    stage_fp8_act(a, xs, lds, step0, nst);
+    bool pre = false;  // quantized beforehand: x holds e4m3 codes, xs the token scales
+    if constexpr (std::is_same<XS, XPlain>::value) pre = a.xs != nullptr;
+    if (pre)
+      stage_fp8_pre(a, lds, step0, nst);
+    else
+      stage_fp8_act(a, xs, lds, step0, nst);
   } else if constexpr (std::is_same<F, FmtInt8>::value) {
     static_assert(std::is_same<XS, XPlain>::value, "int8 activations are read from device memory");
     stage_int8_act(a, lds, step0, nst);

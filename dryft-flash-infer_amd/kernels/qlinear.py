@@ -220,13 +220,26 @@ def linear_w4a16(x, packed, config=None, planes=False, swiglu=False, skinny=None
                        (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
-def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False):
-    """``(x_q s_x) @ (W_q s_w).T`` with the activation quantized per token in the kernel."""
+#: From this many tokens the FP8 activation is quantized by its own kernel before the GEMM;
+#: one token's row is cheaper to read inside every workgroup.
+FP8_QUANTIZE_FROM = 2
+
+
+def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False, pre_quantize=None):
+    """``(x_q s_x) @ (W_q s_w).T`` with the activation quantized per token (``pre_quantize``:
+    None = by its own kernel from 2 tokens, else inside the GEMM; the codes are the same)."""
     q, s, n, k, tiled = _unpack(packed, "fp8")
     _check_x(x, k)
     _lib.require_device(q, s)
     if s.numel() != n:
         raise ValueError("FP8 W8A8 weight scales are one bf16 per output channel")
+    if pre_quantize is None:
+        pre_quantize = x.shape[0] >= FP8_QUANTIZE_FROM and k % 128 == 0
+    if pre_quantize:
+        xq, sx = quantize_fp8_activation(x)
+        return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8_q", x, n, k,
+                           (_lib.ptr(q), _lib.ptr(s), _lib.ptr(xq), _lib.ptr(sx)), (tiled,),
+                           mode=_mode(swiglu, planes), config=config)
     return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8", x, n, k,
                        (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 

@@ -160,6 +160,12 @@ int qlx_linear_skinny(int fmt, const void* w, const void* w_scale, const void* x
 int qlx_linear_fp8_w8a8(const void* w, const void* w_scale, const void* x, void* y, int m, int n,
                         int k, int tiled, const qlx_plan* plan, void* stream);
 
+/* qlx_linear_fp8_w8a8 on an activation qlx_quantize_fp8_act quantized beforehand (e4m3 codes
+ * [m][k], fp32 token scales [m]; K a multiple of 128): bit-identical results, one quantization
+ * per projection instead of one per workgroup. */
+int qlx_linear_fp8_w8a8_q(const void* w, const void* w_scale, const void* x_code, const float* x_scale, void* y,
+                          int m, int n, int k, int tiled, const qlx_plan* plan, void* stream);
+
 /* cuda_fp8.matmul / matmul_partials / gate_up_swiglu on the reference's own Prepared weights
  * (engine/kernels/cuda_fp8.py:1279-1330, 1381-1390): bits 8 (tiled or row-major) or 4. */
 int qlx_linear_ref(const void* w, const void* w_scale, const void* x, void* y, int m, int n,

@@ -146,6 +146,33 @@ def test_linear_fp8_w8a8(n, k):
         assert O.rel_l2(yf, O.round_bf16(ref.astype(np.float32))) <= 4e-3
 
 
+@pytest.mark.parametrize("tiled", [False, True])
+def test_fp8_pre_quantized_activation_is_bitwise_the_fused_prologue(tiled):
+    """From 2 tokens the FP8 activation is quantized by its own kernel and the GEMM stages the
+    codes; the per-token scale and codes are those of the in-kernel prologue, so every output
+    (plain, planes, SwiGLU; several plans) is bit-identical."""
+    n, k = 2 * 1024, 2560
+    w = weights(n, k, 11, edge=False).to(DEV)
+    packed = qlinear.quantize_fp8(w)
+    if tiled:
+        packed = qlinear.prepare(packed)
+    for m in (2, 5, 8, 16, 33, 64):
+        print(f"fp8 pre-quantized tiled={tiled} m={m}", flush=True)
+        x = acts(m, k, 900 + m).to(DEV)
+        for cfg in (None, (4, 1, 1, 3), (4, 2, 2, 2)):
+            try:
+                fused = qlinear.linear_fp8_w8a8(x, packed, config=cfg, pre_quantize=False)
+            except ValueError as exc:  # the plan's activation slice does not fit LDS
+                assert "LDS" in str(exc)
+                continue
+            pre = qlinear.linear_fp8_w8a8(x, packed, config=cfg, pre_quantize=True)
+            assert torch.equal(pre, fused), (tiled, m, cfg)
+            for kw in ({"swiglu": True}, {"planes": True}):
+                a = qlinear.linear_fp8_w8a8(x, packed, config=cfg, pre_quantize=False, **kw)
+                b = qlinear.linear_fp8_w8a8(x, packed, config=cfg, pre_quantize=True, **kw)
+                assert torch.equal(a, b), (tiled, m, cfg, kw)
+
+
 CONFIGS = [(4, 1, 1, 1), (4, 4, 1, 3), (8, 2, 1, 5), (4, 2, 2, 2), (8, 8, 1, 2), (4, 1, 2, 4)]
 
 
