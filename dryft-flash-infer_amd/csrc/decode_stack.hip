@@ -197,14 +197,20 @@ struct ExecDepth<FmtW4> {
 // Per-wave state of one executor work item: row block tg, steps [step0, step0 + nst), K
 // piece s of np; the wave streams tile row wrow at steps step0 + kwi + j * kw, j < my, the
 // last being `last`; plus the item's per-row scale for formats with one scale per row.
+// Group scales a workgroup's threads hold for one item (formats with per-group scales): up
+// to kScaleRegs bf16 values per thread, loaded with the weights instead of after staging.
+constexpr int kScaleRegs = 4;
+
 struct ExecItem {
   int tg, s, np, step0, nst, wt, kwi, my, last, wrow;
   uint32_t scb;  // the per-row scale's bf16 bits, converted only when staged
+  bool scpre;    // the item's group scales are in scw (else staged from memory)
+  uint32_t scw[kScaleRegs];  // group scales' bf16 bits, slot q = tid + u * threads
 };
 
 // Issue the wave's first ExecDepth<F>::PF weight steps (and the per-row scale) of a work
 // item. A wave without steps in the item (my == 0) loads nothing.
-template <class F>
+template <class F, int WAVES>
 __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
                                               ExecItem& it, uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -224,10 +230,27 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
   // weight load. It stays raw bits here: converting it now would wait for every memory
   // operation still in flight (the previous item's output stores among them).
   it.scb = 0u;
+  it.scpre = false;
   if constexpr (F::NSC == 0) {
     const int rl = threadIdx.x, tile = tg * a.rt + (rl >> 4);
     if (rl < 16 * a.rt && tile < a.ntiles)
       it.scb = gmem(reinterpret_cast<const uint16_t*>(a.ws))[weight_row(a, tile, rl & 15)];
+  } else {
+    // Group scales of the item: slot q is row q / nsj, group step0 * NSC + q % nsj (a row's
+    // groups are contiguous in memory, so consecutive threads read consecutive scales).
+    const int nsj = nst * F::NSC, total = nsj * 16 * a.rt;
+    it.scpre = total <= kScaleRegs * WAVES * 64;
+    if (it.scpre) {
+      const auto ws = gmem(reinterpret_cast<const uint16_t*>(a.ws));
+#pragma unroll
+      for (int u = 0; u < kScaleRegs; ++u) {
+        const int q = threadIdx.x + u * WAVES * 64;
+        const int rl = q / nsj, sj = q - rl * nsj, tile = tg * a.rt + (rl >> 4);
+        it.scw[u] = 0u;
+        if (q < total && tile < a.ntiles)
+          it.scw[u] = ws[(size_t)weight_row(a, tile, rl & 15) * (a.k >> 7) + step0 * F::NSC + sj];
+      }
+    }
   }
 #pragma unroll
   for (int p = 0; p < ExecDepth<F>::PF; ++p)
@@ -359,6 +382,15 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
       // Read on every path, so the register is not left pending for the next item's prefetch.
       const float scv = bf2f(it.scb);
       if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
+    } else if (it.scpre) {
+      const int nsj = nst * F::NSC, total = nsj * 16 * a.rt;
+      float* sc = reinterpret_cast<float*>(lds + a.off_sc);
+#pragma unroll
+      for (int u = 0; u < kScaleRegs; ++u) {
+        const int q = threadIdx.x + u * WAVES * 64;
+        const int rl = q / nsj, sj = q - rl * nsj;
+        if (q < total) sc[sj * a.sc_stride + rl] = bf2f(it.scw[u]);
+      }
     } else {
       stage_scales<F>(a, lds, it.tg, step0, nst, ComputeTeam<WAVES>{});
     }
@@ -521,12 +553,12 @@ __device__ __forceinline__ bool next_work(const StackDesc* calls, int ncalls, in
   return false;
 }
 
-template <class F>
+template <class F, int WAVES>
 __device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, ExecItem& it,
                                               uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
   int step0, nst, piece, np;
   share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
-  exec_prefetch<F>(d.a, g, step0, nst, piece, np, it, buf);
+  exec_prefetch<F, WAVES>(d.a, g, step0, nst, piece, np, it, buf);
 }
 
 // A workgroup's next work item, found ahead of time: finding it is arithmetic, and arithmetic
@@ -560,6 +592,7 @@ __device__ __forceinline__ void poll_item(const StackDesc& d, int p, int g, Exec
   it.nst = nst;
   it.wt = it.kwi = it.my = it.last = it.wrow = 0;
   it.scb = 0u;
+  it.scpre = false;
 }
 
 template <class F, int WAVES, int NP, bool DLDS>
@@ -590,7 +623,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
   if (have) {
     if (poller) poll_item(calls[nc], p, ng, nxt);
-    else prefetch_work<F>(calls[nc], p, ng, nxt, buf);
+    else prefetch_work<F, WAVES>(calls[nc], p, ng, nxt, buf);
   }
   while (have) {
     const int c = nc;
@@ -622,7 +655,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     ng = after.g;
     if (have) {
       if (poller) poll_item(calls[nc], p, ng, nxt);
-      else exec_prefetch<F>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+      else exec_prefetch<F, WAVES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     }
     __syncthreads();  // LDS is reused by the next item
   }

@@ -120,29 +120,33 @@ struct XPlain {
   __device__ __forceinline__ uint4 value(const Raw& r) const { return r.v; }
 };
 
-// Settle a batch of fetched chunks of a source whose data may not have arrived: wait for the
-// first chunk alone, then re-fetch every other stale chunk together (when the first is in,
-// the rest usually is: one round trip for all, not one per chunk), then settle each, until
-// ready or the source's deadline has passed. chunk(u, mm, kabs) says whether slot u holds a
-// chunk and where it is.
+// Settle a batch of fetched chunks of a source whose data may not have arrived: every round
+// re-fetches all of the batch's stale chunks together and waits for them, until all are ready
+// or the source's deadline has passed. Chunks written by different producers then cost one
+// round trip after the last of them lands, not one per chunk. chunk(u, mm, kabs) says whether
+// slot u holds a chunk and where it is.
 template <class XS, int U, class Chunk>
 __device__ __forceinline__ void settle_batch(const GemmArgs& a, const XS& xs, typename XS::Raw (&r)[U], Chunk chunk) {
   if constexpr (XS::POLLS) {
+    unsigned stale = 0;  // bit u: slot u holds a chunk that has not arrived
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int mm, kabs;
-      if (!chunk(u, mm, kabs)) continue;
-      while (!xs.ready(r[u]) && !xs.expired()) {
-        __builtin_amdgcn_s_sleep(1);
-        xs.refetch(a, mm, kabs, r[u]);
-      }
-      if (u == 0) {
+      if (chunk(u, mm, kabs) && !xs.ready(r[u])) stale |= 1u << u;
+    }
+    while (stale && !xs.expired()) {
+      __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int v = 1; v < U; ++v) {
-          int mv, kv;
-          if (chunk(v, mv, kv) && !xs.ready(r[v])) xs.refetch(a, mv, kv, r[v]);
+      for (int u = 0; u < U; ++u) {
+        int mm, kabs;
+        if (stale >> u & 1u) {
+          chunk(u, mm, kabs);
+          xs.refetch(a, mm, kabs, r[u]);
         }
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if ((stale >> u & 1u) && xs.ready(r[u])) stale &= ~(1u << u);
     }
   }
 }
@@ -786,12 +790,23 @@ __device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, in
       sc[rl] = tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), 0, 0) : 0.f;
     }
   } else {
+    // Four loads in flight per thread, then their stores: one memory round trip per batch.
     const int total = nst * F::NSC * rows;
-    for (int q = tid; q < total; q += nthr) {
-      const int sj = q / rows, rl = q - sj * rows;
-      const int tile = tg * a.rt + (rl >> 4);
-      sc[sj * a.sc_stride + rl] =
-          tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), step0 + sj / F::NSC, sj % F::NSC) : 0.f;
+    for (int q0 = tid; q0 < total; q0 += 4 * nthr) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = q0 + u * nthr, sj = q / rows, rl = q - sj * rows;
+        const int tile = tg * a.rt + (rl >> 4);
+        v[u] = q < total && tile < a.ntiles
+                   ? F::scale(a, weight_row(a, tile, rl & 15), step0 + sj / F::NSC, sj % F::NSC)
+                   : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = q0 + u * nthr, sj = q / rows, rl = q - sj * rows;
+        if (q < total) sc[sj * a.sc_stride + rl] = v[u];
+      }
     }
   }
 }
@@ -984,11 +999,22 @@ __device__ __forceinline__ void acc_to_lds(char* lds, const f32x4 (&acc)[RW][MT]
 template <class F, int MT, int RW>
 __device__ __forceinline__ float tile_value(const GemmArgs& a, const char* redp, const char* lds, int tl, int nl,
                                             int mm) {
-  constexpr int RC = 16 * MT;
+  constexpr int RC = 16 * MT, WSTRIDE = RW * 16 * RC;  // floats between two waves' partials
   const float* red = reinterpret_cast<const float*>(redp);
   const int slot = tl / RW, r = tl - slot * RW;  // tile tl of the block = slot's r-th tile
+  const float* base = red + ((slot * a.kw * RW + r) * 16 + nl) * RC + mm;
+  // Four waves' partials are read before any is added (one LDS round trip per four waves, not
+  // one per wave); indices past kw repeat the last partial and are not added. The sum keeps
+  // wave order.
   float v = 0.f;
-  for (int w = 0; w < a.kw; ++w) v += red[(((slot * a.kw + w) * RW + r) * 16 + nl) * RC + mm];
+  for (int w0 = 0; w0 < a.kw; w0 += 4) {
+    float part[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) part[w] = base[min(w0 + w, a.kw - 1) * WSTRIDE];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (w0 + w < a.kw) v += part[w];
+  }
   return F::finish(a, lds, v, tl * 16 + nl, mm);
 }
 
