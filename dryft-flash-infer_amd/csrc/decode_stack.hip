@@ -316,7 +316,7 @@ __device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, 
         float mx = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
-        atomicMax(&amax[q / cpr], __float_as_uint(mx));
+        amax_merge(amax, q / cpr, mx);
       }
     }
   }
