@@ -365,7 +365,7 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   if (!reuse) {
     if constexpr (NP == 0) {
       if constexpr (FP8)
-        stage_fp8_act(a, xs, lds, step0, nst);
+        stage_fp8_act(a, xs, lds, step0, nst, BlockTeam{}, amax);  // amax: zeroed, as the pollers' is
       else
         stage_bf16<F>(a, xs, lds, step0, nst);
     } else if (poller) {
@@ -396,6 +396,10 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
     }
   }
   __syncthreads();
+  // The token maxima are read (into the token scales) before that barrier: clear them for
+  // the next staging, which the end-of-item barrier orders after this.
+  if constexpr (FP8 && NP == 0)
+    if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   if constexpr (F::BIAS != 0.f) {
     if (!reuse) {
       if (!poller) stage_bias<F, WAVES>(a, lds, nst);
@@ -604,7 +608,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
-  uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 pollers' per-token maxima
+  uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 staging: per-token maxima
   if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   const StackDesc* calls = gcalls;
   if constexpr (DLDS) {
@@ -641,13 +645,12 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     // next item, issuing its loads (the stores would queue behind them) -- delays the chain
     // (measured: 60-160 us per decode step).
     if (poller) {
-      __syncthreads();  // the two barriers of acc_to_lds in exec_finish
-      __syncthreads();
+      __syncthreads();  // the barrier of acc_to_lds in exec_finish
       if (threadIdx.x - WAVES * 64 < 16) amax[threadIdx.x - WAVES * 64] = 0u;  // for the next staging
     } else if (d.sw) {
-      exec_finish<F, true>(d, lds, cur, acc, w, ComputeTeam<WAVES>{});
+      exec_finish<F, true>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     } else {
-      exec_finish<F, false>(d, lds, cur, acc, w, ComputeTeam<WAVES>{});
+      exec_finish<F, false>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     }
     const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
     have = after.have;
