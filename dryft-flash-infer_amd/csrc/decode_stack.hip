@@ -184,19 +184,22 @@ struct XWire {
 // ---- work items --------------------------------------------------------------------------
 
 // Weight steps in flight per wave: most workgroups' whole share of a decode projection
-// (fewer for 4-bit weights, whose dequantization needs more registers).
-template <class F>
+// (fewer for 4-bit weights, whose dequantization needs more registers). A chain whose row
+// blocks are never cut into K pieces runs a kernel without the piece reduction, whose
+// registers go to deeper prefetch.
+template <class F, bool PIECES>
 struct ExecDepth {
-  static constexpr int PF = 6;
+  static constexpr int PF = PIECES ? 6 : 12;
 };
-template <>
-struct ExecDepth<FmtW4> {
-  static constexpr int PF = 4;
+template <bool PIECES>
+struct ExecDepth<FmtW8, PIECES> {
+  static constexpr int PF = PIECES ? 6 : 8;
+};
+template <bool PIECES>
+struct ExecDepth<FmtW4, PIECES> {
+  static constexpr int PF = PIECES ? 4 : 5;
 };
 
-// Per-wave state of one executor work item: row block tg, steps [step0, step0 + nst), K
-// piece s of np; the wave streams tile row wrow at steps step0 + kwi + j * kw, j < my, the
-// last being `last`; plus the item's per-row scale for formats with one scale per row.
 // Group scales a workgroup's threads hold for one item (formats with per-group scales): up
 // to kScaleRegs bf16 values per thread, loaded with the weights instead of after staging.
 constexpr int kScaleRegs = 4;
@@ -208,11 +211,11 @@ struct ExecItem {
   uint32_t scw[kScaleRegs];  // group scales' bf16 bits, slot q = tid + u * threads
 };
 
-// Issue the wave's first ExecDepth<F>::PF weight steps (and the per-row scale) of a work
+// Issue the wave's first ExecDepth<F, PIECES>::PF weight steps (and the per-row scale) of a work
 // item. A wave without steps in the item (my == 0) loads nothing.
-template <class F, int WAVES>
+template <class F, int WAVES, bool PIECES>
 __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
-                                              ExecItem& it, uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
+                                              ExecItem& it, uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   it.tg = tg;
   it.s = s;
@@ -253,7 +256,7 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
     }
   }
 #pragma unroll
-  for (int p = 0; p < ExecDepth<F>::PF; ++p)
+  for (int p = 0; p < ExecDepth<F, PIECES>::PF; ++p)
     if (p < it.my) load_chunk<F>(buf[p], a, it.wrow, step0 + it.kwi + p * a.kw, lane);
 }
 
@@ -353,11 +356,11 @@ __device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, 
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
 // projection, same steps -- is still in place. With poller waves (NP > 0) they stage the
 // activation and leave after the staging barriers; `amax` is their zeroed FP8 scratch.
-template <class F, int WAVES, int NP, class XS>
+template <class F, int WAVES, int NP, bool PIECES, class XS>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
-                                          uint4 (&buf)[ExecDepth<F>::PF][F::LOADS], f32x4 (&acc)[1][1],
+                                          uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS], f32x4 (&acc)[1][1],
                                           uint32_t* amax) {
-  constexpr int PF = ExecDepth<F>::PF;
+  constexpr int PF = ExecDepth<F, PIECES>::PF;
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
   const int step0 = it.step0, nst = it.nst, kwi = it.kwi, my = it.my;
@@ -443,7 +446,7 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
 // Combine the item's waves; then, per output pair: write it (np == 1), publish this piece's
 // partial sums (piece > 0), or add the other pieces' partials in piece order and write
 // (piece 0). Outputs go to y and, when a later projection reads them, to ywire.
-template <class F, bool SW, class Team = BlockTeam>
+template <class F, bool SW, bool PIECES, class Team = BlockTeam>
 __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const ExecItem& it,
                                             const f32x4 (&acc)[1][1], const Waits& w, const Team& team = {},
                                             bool guard = true) {
@@ -479,7 +482,7 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
       v[0] = tile_value<F, 1, 1>(a, red, lds, tl, nl, mm);
       v[1] = tile_value<F, 1, 1>(a, red, lds, tl, nl + 1, mm);
     }
-    if (np > 1) {
+    if (PIECES && np > 1) {
       if (piece > 0) {
         uint64_t* part = d.part + ((size_t)(piece - 1) * a.m + mm) * a.n;
 #pragma unroll
@@ -557,12 +560,12 @@ __device__ __forceinline__ bool next_work(const StackDesc* calls, int ncalls, in
   return false;
 }
 
-template <class F, int WAVES>
+template <class F, int WAVES, bool PIECES>
 __device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, ExecItem& it,
-                                              uint4 (&buf)[ExecDepth<F>::PF][F::LOADS]) {
+                                              uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS]) {
   int step0, nst, piece, np;
   share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
-  exec_prefetch<F, WAVES>(d.a, g, step0, nst, piece, np, it, buf);
+  exec_prefetch<F, WAVES, PIECES>(d.a, g, step0, nst, piece, np, it, buf);
 }
 
 // A workgroup's next work item, found ahead of time: finding it is arithmetic, and arithmetic
@@ -599,7 +602,7 @@ __device__ __forceinline__ void poll_item(const StackDesc& d, int p, int g, Exec
   it.scpre = false;
 }
 
-template <class F, int WAVES, int NP, bool DLDS>
+template <class F, int WAVES, int NP, bool DLDS, bool PIECES>
 __global__ void __launch_bounds__((WAVES + NP) * 64)
 stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
              int desc_off, int lanes, int amax_off) {
@@ -620,14 +623,14 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
   }
   __syncthreads();
   ExecItem cur, nxt;
-  uint4 buf[ExecDepth<F>::PF][F::LOADS];
+  uint4 buf[ExecDepth<F, PIECES>::PF][F::LOADS];
   f32x4 acc[1][1];
   int nc = -1, ng = 0;
   int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
   if (have) {
     if (poller) poll_item(calls[nc], p, ng, nxt);
-    else prefetch_work<F, WAVES>(calls[nc], p, ng, nxt, buf);
+    else prefetch_work<F, WAVES, PIECES>(calls[nc], p, ng, nxt, buf);
   }
   while (have) {
     const int c = nc;
@@ -635,9 +638,9 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     cur = nxt;
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire)
-      exec_main<F, WAVES, NP>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax);
+      exec_main<F, WAVES, NP, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax);
     else
-      exec_main<F, WAVES, NP>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax);
+      exec_main<F, WAVES, NP, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax);
     staged_c = c;
     staged_step0 = cur.step0;
     staged_nst = cur.nst;
@@ -648,9 +651,9 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
       __syncthreads();  // the barrier of acc_to_lds in exec_finish
       if (threadIdx.x - WAVES * 64 < 16) amax[threadIdx.x - WAVES * 64] = 0u;  // for the next staging
     } else if (d.sw) {
-      exec_finish<F, true>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
+      exec_finish<F, true, PIECES>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     } else {
-      exec_finish<F, false>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
+      exec_finish<F, false, PIECES>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     }
     const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
     have = after.have;
@@ -658,16 +661,19 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     ng = after.g;
     if (have) {
       if (poller) poll_item(calls[nc], p, ng, nxt);
-      else exec_prefetch<F, WAVES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+      else exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     }
     __syncthreads();  // LDS is reused by the next item
   }
 }
 
 template <class F, int WAVES, int NP>
-const void* stack_fn2(bool dlds) {
-  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true>)
-              : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false>);
+const void* stack_fn2(bool dlds, bool pieces) {
+  if (pieces)
+    return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true, true>)
+                : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false, true>);
+  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true, false>)
+              : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false, false>);
 }
 
 // Compute and poller waves the executor is built for: 8 compute waves alone, or 4 with 0, 2 or
@@ -678,19 +684,20 @@ bool stack_shape_ok(int waves, int pollers) {
 }
 
 template <class F>
-const void* stack_fn(int waves, int pollers, bool dlds) {
-  if (waves == 8) return stack_fn2<F, 8, 0>(dlds);
-  if (pollers == 2) return stack_fn2<F, 4, 2>(dlds);
-  if (pollers == 4) return stack_fn2<F, 4, 4>(dlds);
-  return stack_fn2<F, 4, 0>(dlds);
+const void* stack_fn(int waves, int pollers, bool dlds, bool pieces) {
+  if (waves == 8) return stack_fn2<F, 8, 0>(dlds, pieces);
+  if (pollers == 2) return stack_fn2<F, 4, 2>(dlds, pieces);
+  if (pollers == 4) return stack_fn2<F, 4, 4>(dlds, pieces);
+  return stack_fn2<F, 4, 0>(dlds, pieces);
 }
 
-const void* stack_fn_for(int fmt, int waves, int pollers, bool dlds) {
+// The kernel for a launch: `pieces` when some row block of the chain is cut into K pieces.
+const void* stack_fn_for(int fmt, int waves, int pollers, bool dlds, bool pieces) {
   if (!stack_shape_ok(waves, pollers)) return nullptr;
   switch (fmt) {
-    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, pollers, dlds);
-    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, pollers, dlds);
-    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, pollers, dlds);
+    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, pollers, dlds, pieces);
+    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, pollers, dlds, pieces);
+    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, pollers, dlds, pieces);
     default: return nullptr;
   }
 }
@@ -819,7 +826,7 @@ int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
                     int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
                     qlx_stack_launch* launch) {
-  QLX_REQUIRE(stack_fn_for(fmt, 8, 0, false) != nullptr,
+  QLX_REQUIRE(stack_fn_for(fmt, 8, 0, false, false) != nullptr,
               "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
   QLX_REQUIRE(m >= 1 && m <= 16, "the decode executor serves m = 1..16 (got %d)", m);
@@ -875,6 +882,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
   const long long desc_bytes = (long long)ncalls * sizeof(StackDesc);
   // Plan for P workgroups, then shrink P to what fits the CUs with that LDS; repeat until
   // plan and grid agree. LDS: [items][64 B of FP8 row maxima][descriptors, if they fit].
+  bool pieces = false;  // some row block is cut into K pieces: the kernel with their reduction
   for (int round = 0;; ++round) {
     QLX_REQUIRE(round < 4, "no stable executor grid");
     int items_lds = 0;
@@ -890,7 +898,9 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     const int items_end = amax_off + 64;
     desc_lds = items_end + desc_bytes <= kLdsLimit ? items_end : -1;
     lds = desc_lds >= 0 ? (int)(items_end + desc_bytes) : items_end;
-    const void* fn = stack_fn_for(fmt, waves, pollers, desc_lds >= 0);
+    pieces = false;
+    for (int c = 0; c < ncalls; ++c) pieces |= sp[c].max_np > 1;
+    const void* fn = stack_fn_for(fmt, waves, pollers, desc_lds >= 0, pieces);
     if (lds > 64 * 1024) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       if (e != hipSuccess) return hip_status(e, "stack_build");
@@ -959,6 +969,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     launch->desc_lds = desc_lds;
     launch->pollers = pollers;
     launch->amax_off = amax_off;
+    launch->pieces = pieces ? 1 : 0;
   }
   return QLX_OK;
 }
@@ -967,7 +978,8 @@ int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch*
                   int* error, long long budget_us, void* stream) {
   QLX_REQUIRE(launch != nullptr && stack_shape_ok(launch->waves, launch->pollers) && launch->grid >= 1,
               "bad executor launch configuration");
-  const void* fn = stack_fn_for(fmt, launch->waves, launch->pollers, launch->desc_lds >= 0);
+  QLX_REQUIRE(launch->pieces == 0 || launch->pieces == 1, "launch.pieces must be 0 or 1 (got %d)", launch->pieces);
+  const void* fn = stack_fn_for(fmt, launch->waves, launch->pollers, launch->desc_lds >= 0, launch->pieces != 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(desc && error && ncalls >= 1, "bad executor arguments");
   QLX_REQUIRE(launch->desc_lds < 0 || launch->desc_lds + (long long)ncalls * (long long)sizeof(StackDesc) <=

@@ -42,9 +42,10 @@ class StackCall(ctypes.Structure):
 
 class StackLaunch(ctypes.Structure):
     """``qlx_stack_launch``: grid, LDS bytes, compute waves, descriptor LDS offset, lanes, poller
-    waves, and the LDS offset of the pollers' FP8 row maxima."""
+    waves, the LDS offset of the FP8 row maxima, and whether row blocks are cut into K pieces."""
 
-    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "pollers", "amax_off")]
+    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "pollers", "amax_off",
+                                            "pieces")]
 
 
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong

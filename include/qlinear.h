@@ -241,7 +241,9 @@ typedef struct qlx_stack_launch {
   int desc_lds;    /* byte offset of the descriptors' LDS copy, or -1 (read from memory) */
   int lanes;       /* workgroup sets: lane l runs projections l, l + lanes, ... */
   int pollers;     /* waves per workgroup that only read and stage published activations */
-  int amax_off;    /* LDS byte offset of the pollers' per-token FP8 maxima (64 bytes) */
+  int amax_off;    /* LDS byte offset of the per-token FP8 maxima (64 bytes) */
+  int pieces;      /* 1 when a row block of the chain is cut into K pieces (the kernel with their
+                      reduction, whose registers otherwise go to deeper weight prefetch), else 0 */
 } qlx_stack_launch;
 
 /* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
