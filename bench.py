@@ -268,7 +268,7 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
             if ms_exec * 1e3 < out.get("executor_us", 1e30):
                 out["executor_us"] = ms_exec * 1e3
                 out["executor_launch"] = {"grid": chain.grid, "lds": chain.lds, "waves": waves, "pollers": pollers,
-                                          "desc_lds": chain.launch.desc_lds >= 0}
+                                          "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
             del chain
     cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
@@ -370,7 +370,8 @@ def main():
     if head["path"] == "executor":
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
         el = head["executor_launch"]
-        kname = f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}>"
+        kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
+                 f"{str(el['pieces']).lower()}>")
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
