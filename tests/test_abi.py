@@ -177,6 +177,10 @@ def test_decode_stack_contract_on_host():
         assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
     good = _lib.StackLaunch(256, 1024, 4, -1, 1, 4, 0)
     assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, good, 1 << 16, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    # the pieces flag selects the kernel with or without the K-piece reduction: 0 or 1 only
+    bad = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 0, 2)
+    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    assert "pieces" in _lib.last_error()
 
 
 def test_selection_api_mirrors_the_reference():

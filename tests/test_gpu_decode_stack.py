@@ -45,6 +45,17 @@ CHAIN = [
 ]
 
 
+# One Qwen3-4B decoder layer's projections (hidden 2560, intermediate 9728; o reads the query
+# part of qkv): at M = 1 the planner cuts no row block into K pieces, so the launch runs the
+# kernel instance without the piece reduction (and with deeper prefetch).
+QWEN_LAYER = [
+    ("qkv", 6144, 2560, "x2560", False),
+    ("o", 2560, 4096, "qkv[:4096]", False),
+    ("gu", 19456, 2560, "o", True),
+    ("dn", 2560, 9728, "gu", False),
+]
+
+
 def source(bufs, src):
     """The input tensor named by `src`: a buffer, or "name[:k]" for its first k columns."""
     if "[" in src:
@@ -53,12 +64,13 @@ def source(bufs, src):
     return bufs[src]
 
 
-def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, pollers=0):
+def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, pollers=0, chain_def=None):
     quant = qlinear.FORMATS[fmt][0]
-    bufs = {"x": rand((m, 1024), seed).to(DEV), "g": rand((m, 9728), seed + 1).to(DEV)}
+    bufs = {"x": rand((m, 1024), seed).to(DEV), "g": rand((m, 9728), seed + 1).to(DEV),
+            "x2560": rand((m, 2560), seed + 2).to(DEV)}
     weights, raw = {}, {}
     chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes, pollers=pollers)
-    for idx, (name, n, k, src, sw) in enumerate(CHAIN):
+    for idx, (name, n, k, src, sw) in enumerate(chain_def or CHAIN):
         w = rand((n, k), seed + 10 + idx, std=0.02).to(DEV)
         packed = quant(w)
         raw[name] = packed
@@ -69,10 +81,10 @@ def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, pollers=0):
     return chain, bufs, weights, raw
 
 
-def check_against_single_calls(fmt, bufs, weights, tag):
+def check_against_single_calls(fmt, bufs, weights, tag, chain_def=None):
     """Each projection vs the single-call linear on the executor's own input."""
     linear = qlinear.FORMATS[fmt][1]
-    for name, n, k, src, sw in CHAIN:
+    for name, n, k, src, sw in chain_def or CHAIN:
         want = linear(source(bufs, src).contiguous(), weights[name], swiglu=sw).float()
         got = bufs[name].float()
         diff = (got - want).abs()
@@ -137,6 +149,31 @@ def test_poller_chain_matches_single_calls_and_oracle(fmt, m, pollers):
     run_chain_checks(fmt, m, waves=4, pollers=pollers)
 
 
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+def test_layer_chain_without_pieces(fmt):
+    """A Qwen3-4B layer at M = 1 (the decode step's shapes): no row block is cut into pieces,
+    so the run takes the executor instance without the piece reduction; same bounds as the
+    other chains, deterministic, and within the north star's bound of the oracle."""
+    print(f"decode stack layer {fmt}", flush=True)
+    chain, bufs, weights, raw = build_chain(fmt, 1, 31, chain_def=QWEN_LAYER)
+    assert chain.launch.pieces == 0 and all(c[3] == 1 for c in chain.configs), chain.configs
+    for run in range(2):
+        if run:
+            bufs["x2560"].copy_(rand((1, 2560), 99).to(DEV))
+        chain.run()
+        torch.cuda.synchronize()
+        assert not chain.failed(), chain.failed_waits()
+        first = {name: bufs[name].clone() for name, *_ in QWEN_LAYER}
+        chain.run()
+        torch.cuda.synchronize()
+        for name, *_ in QWEN_LAYER:
+            assert torch.equal(bufs[name], first[name]), (fmt, run, name, "deterministic")
+        check_against_single_calls(fmt, bufs, weights, (fmt, "layer", run), chain_def=QWEN_LAYER)
+    for name in ("o", "dn"):
+        src = [c for c in QWEN_LAYER if c[0] == name][0][3]
+        assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name]) < 1e-2, name
+
+
 @pytest.mark.parametrize("kw", [1, 2, 4, 8])
 @pytest.mark.parametrize("pollers", [0, 4])
 def test_every_tile_split_is_exact(kw, pollers):
@@ -147,6 +184,7 @@ def test_every_tile_split_is_exact(kw, pollers):
     fmt = "fp8" if pollers else "w4a16"
     chain, bufs, weights, _ = build_chain(fmt, 3, 77, kw=kw, waves=4 if pollers else 8, pollers=pollers)
     assert all(c[1] == kw for c in chain.configs)
+    assert chain.launch.pieces == int(any(c[3] > 1 for c in chain.configs))
     chain.run()
     torch.cuda.synchronize()
     assert not chain.failed()
