@@ -30,11 +30,13 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p) {
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 bits, RNE by integer add (cuda_fp8.py:64-68); NaN -> sign | 0x7FC0.
+// fp32 -> bf16 bits, RNE by integer add (cuda_fp8.py:64-68); NaN -> sign | 0x7FC0. Both
+// results are formed and one selected: no divergent branch in the epilogues that call it.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = ((u >> 16) & 0x8000u) | 0x7fc0u;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
@@ -53,16 +55,13 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   const uint32_t u = __float_as_uint(f);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7fffffffu;
-  uint32_t code;
-  if (a > 0x7f800000u) {
-    code = 0x7fu;
-  } else if (a < (121u << 23)) {
-    code = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
-  } else {
-    const uint32_t ar = a + 0x7ffffu + ((a >> 20) & 1u);
-    code = (ar >> 20) - (120u << 3);
-    if (code > 0x7eu) code = 0x7fu;
-  }
+  // Every case is computed and one selected (no divergent branches): the subnormal code from
+  // |f| clamped to the subnormal range (so the conversion stays in range), the normal code
+  // (meaningless below 2^-6, where it is not used), NaN.
+  const uint32_t sub = (uint32_t)rintf(fminf(__uint_as_float(a), 0.015625f) * 512.0f);
+  const uint32_t nrm = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
+  uint32_t code = a < (121u << 23) ? sub : (nrm > 0x7eu ? 0x7fu : nrm);
+  code = a > 0x7f800000u ? 0x7fu : code;
   return code | sign;
 }
 
