@@ -405,15 +405,25 @@ def main():
     del stack
     torch.cuda.empty_cache()
     if not args.quick:
-        for fmt, m in (("w4a16", 1), ("fp8", 8), ("w4a16", 8)):
+        # BASELINE configs 2 and 3 per projection (single calls, 36 distinct weights per
+        # projection in one graph): FP8 W8A8 at M = 1, 8; W4A16 at M = 1, 4, 8 with the lm_head.
+        per_cfg = {"config2_fp8_w8a8": {}, "config3_w4a16": {}}
+        if args.workload == "fp8" and args.m == 1 and "per_projection" in head:
+            per_cfg["config2_fp8_w8a8"]["M1"] = head["per_projection"]
+        for fmt, m in (("w4a16", 1), ("w4a16", 4), ("fp8", 8), ("w4a16", 8)):
             if (fmt, m) == (args.workload, args.m):
                 continue
-            st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=False)
-            extra[f"{fmt}_M{m}_stack"] = {k: (round(v, 4 if k == "hbm_frac" else 2) if isinstance(v, float) else v)
-                                          for k, v in res.items()}
-            log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s")
+            st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=True)
+            per = res.pop("per_projection")
+            per_cfg["config2_fp8_w8a8" if fmt == "fp8" else "config3_w4a16"][f"M{m}"] = per
+            if m != 4:
+                extra[f"{fmt}_M{m}_stack"] = {k: (round(v, 4 if k == "hbm_frac" else 2) if isinstance(v, float) else v)
+                                              for k, v in res.items()}
+            log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s; per projection "
+                + ", ".join(f"{n} {v['us']:.1f} us" for n, v in per.items()))
             del st
             torch.cuda.empty_cache()
+        extra["per_projection_single_calls"] = per_cfg
         extra["config4_w4_gate_up_swiglu_down"] = measure_config4(max(3, args.steps // 4))
 
     line = {

@@ -164,9 +164,14 @@ __device__ __forceinline__ uint2 bytes_to_bf16(uint32_t d) {
   return r;
 }
 
-// Low nibbles of bytes (0,2) and (1,3) of d, shifted by `sh`, as bf16(128 + code) pairs.
+// Low nibbles of bytes (0,2) and (1,3) of d, shifted by `sh` (0, 4, 8 or 12), as bf16(128 +
+// code) pairs, i.e. ((d >> sh) & 0x000f000f) | 0x43004300. Built with a byte permute from the
+// dword's low or high nibbles (d & 0x0f0f0f0f, shared by the four calls on one dword): 7
+// instructions per dword instead of 11 (the compiler splits (x & m) | c with two literal
+// constants into two instructions).
 __device__ __forceinline__ uint32_t nib_pair(uint32_t d, int sh) {
-  return ((d >> sh) & 0x000f000fu) | 0x43004300u;
+  const uint32_t n = ((sh & 4) ? d >> 4 : d) & 0x0f0f0f0fu;
+  return __builtin_amdgcn_perm(0x43434343u, n, (sh & 8) ? 0x04030401u : 0x04020400u);
 }
 
 __device__ __forceinline__ uint32_t bf16_at(const uint16_t* p, int i) { return p[i]; }
