@@ -52,16 +52,21 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 // above, 20 mantissa bits are dropped with round-half-even by integer add.
 // Anything that rounds past 448 (and Inf/NaN) becomes NaN (0x7F), as torch's cast.
 __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  // Branches, not selects: in a wave almost every value takes the normal path, so only that
+  // path runs (computing every case and selecting measured ~15 us slower per FP8 decode step).
   const uint32_t u = __float_as_uint(f);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7fffffffu;
-  // Every case is computed and one selected (no divergent branches): the subnormal code from
-  // |f| clamped to the subnormal range (so the conversion stays in range), the normal code
-  // (meaningless below 2^-6, where it is not used), NaN.
-  const uint32_t sub = (uint32_t)rintf(fminf(__uint_as_float(a), 0.015625f) * 512.0f);
-  const uint32_t nrm = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
-  uint32_t code = a < (121u << 23) ? sub : (nrm > 0x7eu ? 0x7fu : nrm);
-  code = a > 0x7f800000u ? 0x7fu : code;
+  uint32_t code;
+  if (a > 0x7f800000u) {
+    code = 0x7fu;
+  } else if (a < (121u << 23)) {
+    code = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
+  } else {
+    const uint32_t ar = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (ar >> 20) - (120u << 3);
+    if (code > 0x7eu) code = 0x7fu;
+  }
   return code | sign;
 }
 
