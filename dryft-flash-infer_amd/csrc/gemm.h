@@ -657,23 +657,6 @@ __device__ __forceinline__ void store_e4m3_chunk(char* dst, uint4 v, float sc) {
   *reinterpret_cast<uint2*>(dst) = o;
 }
 
-// Merge an active lane's |x| maximum mx of token mm into amax[mm] (non-negative floats as
-// uint bits, so an integer max orders them). When the whole wave is active and on one token
-// (every m = 1 row), the wave's maximum is taken by shuffles and written with one LDS atomic:
-// 64 atomics on one address serialize. The result is the same maximum.
-__device__ __forceinline__ void amax_merge(uint32_t* amax, int mm, float mx) {
-  const unsigned long long act = __ballot(1);
-  const int mm0 = __builtin_amdgcn_readfirstlane(mm);
-  if (act == ~0ull && __all(mm == mm0)) {
-    float r = mx;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) r = fmaxf(r, __shfl_xor(r, off));
-    if ((threadIdx.x & 63) == 0) atomicMax(&amax[mm0], __float_as_uint(r));
-  } else {
-    atomicMax(&amax[mm], __float_as_uint(mx));
-  }
-}
-
 // The per-token bf16 maxima (as uint bits) of the FP8 prologue, after the token scales.
 __device__ __forceinline__ uint32_t* fp8_amax(const GemmArgs& a, char* lds) {
   return reinterpret_cast<uint32_t*>(lds + a.off_sx) + a.m;
@@ -721,7 +704,7 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
         float mx = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
-        amax_merge(amax, q / cpr, mx);
+        atomicMax(&amax[q / cpr], __float_as_uint(mx));
       }
     }
   }
