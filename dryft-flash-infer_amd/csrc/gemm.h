@@ -576,8 +576,14 @@ struct FmtInt8 {
 // Prologue: stage the workgroup's activation slice (B order), its scales, bias sums.
 // ====================================================================================
 
-// Chunks each thread keeps in flight while staging.
-constexpr int kStageUnroll = 4;
+// Chunks each thread keeps in flight while staging: 4 from device memory; from published
+// activations (the decode executor's polls) 3 for the FP8 prologue and 2 for bf16, the
+// fastest of 2-8 on the Qwen3-4B M=1 chain (FP8 1223 / 1190 / 1202 / 1218 us at 2 / 3 / 4 /
+// 6; W4A16 1199 / 1213 / 1221 us at 2 / 3 / 4).
+template <class XS, bool FP8>
+__host__ __device__ constexpr int stage_unroll() {
+  return XS::POLLS ? (FP8 ? 3 : 2) : 4;
+}
 
 // The threads that stage and finish a work item, and how they wait for each other: the
 // whole workgroup and its barrier here; the decode executor's compute waves (without its
@@ -591,6 +597,7 @@ struct BlockTeam {
 template <class F, class XS, class Team = BlockTeam>
 __device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {}) {
   const int tid = team.tid(), nthr = team.size();
+  constexpr int U_ = stage_unroll<XS, false>();
   constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
   const int cpr = nst * CPS;
   const int total = a.m * cpr;
@@ -601,8 +608,8 @@ __device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char
       *reinterpret_cast<uint4*>(lds + mm * a.xstride + kc * 16) = F::stage_chunk(a, mm, step0 * F::KSTEP + kc * 8);
     }
   } else {
-    for (int q0 = tid; q0 < total; q0 += kStageUnroll * nthr) {
-      typename XS::Raw r[kStageUnroll];
+    for (int q0 = tid; q0 < total; q0 += U_ * nthr) {
+      typename XS::Raw r[U_];
       auto chunk = [&](int u, int& mm, int& kabs) {
         const int q = q0 + u * nthr;
         mm = q / cpr;
@@ -610,13 +617,13 @@ __device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char
         return q < total;
       };
 #pragma unroll
-      for (int u = 0; u < kStageUnroll; ++u) {
+      for (int u = 0; u < U_; ++u) {
         int mm, kabs;
         if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
       }
-      settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
+      settle_batch<XS, U_>(a, xs, r, chunk);
 #pragma unroll
-      for (int u = 0; u < kStageUnroll; ++u) {
+      for (int u = 0; u < U_; ++u) {
         int mm, kabs;
         if (chunk(u, mm, kabs))
           *reinterpret_cast<uint4*>(lds + mm * a.xstride + (kabs - step0 * F::KSTEP) * 2) = F::order(xs.value(r[u]));
@@ -670,6 +677,7 @@ template <class XS, class Team = BlockTeam>
 __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {},
                               uint32_t* zeroed_amax = nullptr) {
   const int tid = team.tid(), nthr = team.size();
+  constexpr int U_ = stage_unroll<XS, true>();
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
   uint32_t* amax = zeroed_amax ? zeroed_amax : fp8_amax(a, lds);
   if (!zeroed_amax) {
@@ -678,10 +686,10 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
   }
   const int cpr = a.k >> 3;
   const int total = a.m * cpr;
-  const bool one_pass = total <= kStageUnroll * nthr;
-  uint4 kept[kStageUnroll];
-  for (int q0 = tid; q0 < total; q0 += kStageUnroll * nthr) {
-    typename XS::Raw r[kStageUnroll];
+  const bool one_pass = total <= U_ * nthr;
+  uint4 kept[U_];
+  for (int q0 = tid; q0 < total; q0 += U_ * nthr) {
+    typename XS::Raw r[U_];
     auto chunk = [&](int u, int& mm, int& kabs) {
       const int q = q0 + u * nthr;
       mm = q / cpr;
@@ -689,13 +697,13 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
       return q < total;
     };
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u) {
+    for (int u = 0; u < U_; ++u) {
       int mm, kabs;
       if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
     }
-    settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
+    settle_batch<XS, U_>(a, xs, r, chunk);
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u) {
+    for (int u = 0; u < U_; ++u) {
       const int q = q0 + u * nthr;
       if (q < total) {
         const uint4 v = xs.value(r[u]);
@@ -716,7 +724,7 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
   const int c0 = step0 * 16, c1 = c0 + nst * 16;  // the slice's 8-value chunks within a row
   if (one_pass) {
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u) {
+    for (int u = 0; u < U_; ++u) {
       const int q = tid + u * nthr;
       if (q < total) {
         const int mm = q / cpr, kc = q - mm * cpr;
@@ -726,8 +734,8 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
     return;
   }
   const int cps = nst * 16;  // 8-value chunks per row of the slice
-  for (int q0 = tid; q0 < a.m * cps; q0 += kStageUnroll * nthr) {
-    typename XS::Raw r[kStageUnroll];
+  for (int q0 = tid; q0 < a.m * cps; q0 += U_ * nthr) {
+    typename XS::Raw r[U_];
     auto chunk = [&](int u, int& mm, int& kabs) {
       const int q = q0 + u * nthr;
       mm = q / cps;
@@ -735,13 +743,13 @@ __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, c
       return q < a.m * cps;
     };
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u) {
+    for (int u = 0; u < U_; ++u) {
       int mm, kabs;
       if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
     }
-    settle_batch<XS, kStageUnroll>(a, xs, r, chunk);
+    settle_batch<XS, U_>(a, xs, r, chunk);
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u) {
+    for (int u = 0; u < U_; ++u) {
       int mm, kabs;
       if (chunk(u, mm, kabs))
         store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), token_scale(mm));
