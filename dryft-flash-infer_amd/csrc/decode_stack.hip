@@ -203,8 +203,9 @@ struct ExecDepth<FmtW4, PIECES> {
 };
 
 // Group scales a workgroup's threads hold for one item (formats with per-group scales): up
-// to kScaleRegs bf16 values per thread, loaded with the weights instead of after staging.
-constexpr int kScaleRegs = 4;
+// to kScaleRegs bf16 values per thread, loaded with the weights instead of after staging
+// (5 x 512 threads: every Qwen3-4B item at M = 1, gate_up's 2560 included).
+constexpr int kScaleRegs = 5;
 
 struct ExecItem {
   int tg, s, np, step0, nst, wt, kwi, my, last, wrow;

@@ -577,12 +577,12 @@ struct FmtInt8 {
 // ====================================================================================
 
 // Chunks each thread keeps in flight while staging: 4 from device memory; from published
-// activations (the decode executor's polls) 3 for the FP8 prologue and 2 for bf16, the
-// fastest of 2-8 on the Qwen3-4B M=1 chain (FP8 1223 / 1190 / 1202 / 1218 us at 2 / 3 / 4 /
-// 6; W4A16 1199 / 1213 / 1221 us at 2 / 3 / 4).
+// activations (the decode executor's polls) 3 for the FP8 prologue and 1 for bf16, the
+// fastest on the Qwen3-4B M=1 chain (FP8 1223 / 1190 / 1202 / 1218 us at 2 / 3 / 4 / 6;
+// W4A16 1185 / 1190 / 1213 / 1221 us at 1 / 2 / 3 / 4).
 template <class XS, bool FP8>
 __host__ __device__ constexpr int stage_unroll() {
-  return XS::POLLS ? (FP8 ? 3 : 2) : 4;
+  return XS::POLLS ? (FP8 ? 3 : 1) : 4;
 }
 
 // The threads that stage and finish a work item, and how they wait for each other: the
