@@ -23,17 +23,21 @@
 
 namespace qlx {
 
-// Weight steps in flight per wave (even: the two activation register sets alternate with
-// the step's parity): 4 where the registers allow it.
-__host__ __device__ constexpr int skinny_pf(int mt) { return mt == 1 ? 4 : 2; }
+// Weight steps in flight per wave, and activation chunks in flight per thread (the same
+// depth: the activation of step i + PF is fetched with the weights of step i + PF).
+__host__ __device__ constexpr int skinny_pf(int mt, bool wide) { return wide || mt == 1 ? 3 : 2; }
+// 4-bit weights at 33..64 tokens run one workgroup per CU, each wave with the 512 registers of
+// a whole SIMD: two activation sets of 64 rows, the MT = 4 accumulators and the code-bias
+// chains spill at 256.
 // 16-row tiles per wave, sharing each activation fragment read from LDS: two up to 32 tokens,
 // one at 64 (two would need more than the 256 registers of two waves per SIMD).
 __host__ __device__ constexpr int skinny_rw(int mt) { return mt >= 4 ? 1 : 2; }
 // Token fragments (16 tokens each) a batch is computed with: 1, 2 or 4 (33..48 tokens run as 4).
 __host__ __device__ constexpr int skinny_mt_of(int m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
-// LDS of one activation chunk: [m rows][xstride bytes] of x in the format's B order, then
-// the group scales [NSC][16 rows x the workgroup's tiles] as floats.
+// LDS of one activation chunk: [16 MT rows][xstride bytes] of x in the format's B order (rows
+// past m hold zeros and are never read), then the group scales [NSC][16 rows x
+// the workgroup's tiles] as floats.
 struct SkinnyLayout {
   int xstride, off_sc, sc_stride, chunk;
 };
@@ -45,16 +49,17 @@ __host__ __device__ inline SkinnyLayout skinny_layout(int m, int waves) {
   SkinnyLayout L{};
   L.xstride = F::KSTEP * F::XBYTES + 16;  // rows 4 banks apart: a B read of 16 rows is conflict-free
   L.sc_stride = 16 * waves * skinny_rw(skinny_mt_of(m));
-  L.off_sc = up16(m * L.xstride);
+  L.off_sc = up16(16 * skinny_mt_of(m) * L.xstride);
   L.chunk = up16(L.off_sc + (F::NSC > 0 ? F::NSC : 0) * L.sc_stride * 4);
   return L;
 }
 
-// x chunks (16 bytes, 8 values) of one K step that each thread stages.
-template <class F, int WAVES>
+// x chunks (16 bytes, 8 values) of one K step that each thread stages: 16 MT rows.
+template <class F, int WAVES, int MT>
 struct SkinnyStage {
   static constexpr int PER_ROW = F::KSTEP / 8;
-  static constexpr int MAX = (64 * PER_ROW + WAVES * 64 - 1) / (WAVES * 64);
+  static constexpr int CHUNKS = 16 * MT * PER_ROW;
+  static constexpr int MAX = (CHUNKS + WAVES * 64 - 1) / (WAVES * 64);
 };
 
 // One K step of RW tiles against MT token fragments of the staged chunk `ch`, the format's
@@ -148,15 +153,37 @@ __device__ __forceinline__ void skinny_step(f32x4 (&acc)[RW][MT], const uint4 (&
   }
 }
 
-// Two workgroups per CU: each wave at most 256 registers.
+// Buffer resource over `bytes` of device memory (base address uniform across the workgroup).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t skinny_rsrc(const void* p, unsigned bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// Buffer access policy sc1: device scope (past this XCD's L2, which other XCDs' stores do not update).
+constexpr int kSc1 = 16;
+
+// fn(integral_constant<int, P>) for P = B .. E - 1, unrolled at compile time.
+template <int B, int E, class Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+  if constexpr (B < E) {
+    fn(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(fn);
+  }
+}
+
+// Two workgroups per CU (each wave at most 256 registers), or one for the wide instances.
 template <class F, int MT, int WAVES, bool SW>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES == 4 ? 2 : 1)))
+__global__ void __launch_bounds__(WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(WAVES == 4 && !(MT == 4 && F::NSC > 0) ? 2 : 1)))
 skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
   static_assert(F::LOADS == 2, "a tile step is two 1 KB loads per wave");
   static_assert(F::NSC == 0 || std::is_same<F, FmtW4>::value, "group scales as W4A16 lays them out");
   extern __shared__ __align__(16) char lds[];
-  constexpr int PF = skinny_pf(MT), RW = skinny_rw(MT);
-  constexpr int SPR = SkinnyStage<F, WAVES>::PER_ROW, SMAX = SkinnyStage<F, WAVES>::MAX;
+  constexpr int PF = skinny_pf(MT, WAVES == 4 && MT == 4 && F::NSC > 0), RW = skinny_rw(MT);
+  constexpr int SPR = SkinnyStage<F, WAVES, MT>::PER_ROW, SMAX = SkinnyStage<F, WAVES, MT>::MAX;
+  constexpr int CHUNKS = SkinnyStage<F, WAVES, MT>::CHUNKS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tg = blockIdx.x / a.splits, s = blockIdx.x - tg * a.splits;
   const int step0 = s * steps_per_slice;
@@ -173,75 +200,81 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
     rowl[r] = (wave * RW + r) * 16 + 4 * (lane >> 4);
   }
 
-  // Weight steps step0 .. step0 + PF - 1 first: nothing else they wait for. A tile past the
-  // end streams tile 0 of the workgroup (always real); its results are dropped.
-  uint4 buf[PF][RW][F::LOADS];
+  // Every load below is issued unconditionally (indices clamped to real rows, tiles and steps),
+  // so the compiler counts the in-order memory queue exactly: a wait for step i's data never
+  // waits for loads issued after it. (Loads under branches made it drain the whole queue,
+  // vmcnt(0), several times per step.) A tile past the end streams tile 0 of the workgroup
+  // (always real); its results are dropped.
+  int lrow[RW];
 #pragma unroll
-  for (int p = 0; p < PF; ++p)
-#pragma unroll
-    for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, act[r] ? wrow[r] : weight_row(a, tg * WAVES * RW, lane & 15),
-                                               min(step0 + p, last), lane);
+  for (int r = 0; r < RW; ++r) lrow[r] = act[r] ? wrow[r] : weight_row(a, tg * WAVES * RW, lane & 15);
 
   // A step's staged data: SMAX 16-byte activation chunks and (group formats) SCMAX raw bf16
   // scales per thread, fetched into registers ahead of time and written to LDS later.
   constexpr int SCMAX = F::NSC > 0 ? (F::NSC * 16 * WAVES * RW + WAVES * 64 - 1) / (WAVES * 64) : 1;
   struct Staged {
     uint4 x[SMAX];
-    uint32_t sc[SCMAX];
+    uint16_t sc[SCMAX];  // widened only when written to LDS: no copy of an in-flight load
   };
-  const uint16_t* x = reinterpret_cast<const uint16_t*>(a.x);
-  auto fetch_x = [&](int step, Staged& st) {
+  // The activation through a buffer resource over its m rows: a thread's chunks u = 0, 1, ..
+  // are rows row0 + u XROWS of one column, so one 32-bit offset serves every chunk (the row
+  // step is a scalar offset), and rows past m read as zeros (the resource's bounds check).
+  constexpr int XROWS = WAVES * 64 / SPR;
+  static_assert(WAVES * 64 % SPR == 0, "a thread's chunks share their column");
+  const __amdgpu_buffer_rsrc_t xr = skinny_rsrc(a.x, (unsigned)a.m * (unsigned)a.k * 2u);
+  const int xrow0 = threadIdx.x / SPR, xcol = threadIdx.x - xrow0 * SPR;
+  const unsigned xoff0 = ((unsigned)xrow0 * (unsigned)a.k + (unsigned)xcol * 8u) * 2u;
+  auto fetch_x = [&](int step, Staged& st) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < SMAX; ++u) {
-      const int q = threadIdx.x + u * WAVES * 64;
-      if (q < a.m * SPR) {
-        const int mm = q / SPR, c = q - mm * SPR;
-        const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(x + (size_t)mm * a.k + step * F::KSTEP + c * 8));
-        st.x[u] = uint4{v[0], v[1], v[2], v[3]};
-      }
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(xoff0 + (unsigned)step * (F::KSTEP * 2)),
+                                                            u * XROWS * a.k * 2, 0);
+      st.x[u] = uint4{v[0], v[1], v[2], v[3]};
     }
     if constexpr (F::NSC > 0) {
 #pragma unroll
       for (int u = 0; u < SCMAX; ++u) {
-        const int q = threadIdx.x + u * WAVES * 64;
-        st.sc[u] = 0u;
-        if (q < F::NSC * L.sc_stride) {
-          const int j = q / L.sc_stride, rl = q - j * L.sc_stride;
-          const int t = tg * WAVES * RW + (rl >> 4);
-          if (t < a.ntiles)  // group 2 step + j of the tile row's weight row, as F::scale reads it
-            st.sc[u] = gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)weight_row(a, t, rl & 15) * (a.k >> 7) +
-                                                                      F::NSC * step + j];
-        }
+        const int q = min((int)threadIdx.x + u * WAVES * 64, F::NSC * L.sc_stride - 1);
+        const int j = q / L.sc_stride, rl = q - j * L.sc_stride;
+        const int t = min(tg * WAVES * RW + (rl >> 4), a.ntiles - 1);  // a tile past the end: dropped
+        // group 2 step + j of the tile row's weight row, as F::scale reads it
+        st.sc[u] = gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)weight_row(a, t, rl & 15) * (a.k >> 7) +
+                                                                  F::NSC * step + j];
       }
     }
   };
-  auto put_x = [&](char* ch, const Staged& st) {
+  auto put_x = [&](char* ch, const Staged& st) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < SMAX; ++u) {
-      const int q = threadIdx.x + u * WAVES * 64;
-      if (q < a.m * SPR) {
-        const int mm = q / SPR, c = q - mm * SPR;
-        *reinterpret_cast<uint4*>(ch + mm * L.xstride + c * 16) = F::order(st.x[u]);
-      }
+      const int mm = xrow0 + u * XROWS;  // rows past m hold zeros and are never read
+      if (CHUNKS % (WAVES * 64) == 0 || mm < 16 * MT)
+        *reinterpret_cast<uint4*>(ch + mm * L.xstride + xcol * 16) = F::order(st.x[u]);
     }
     if constexpr (F::NSC > 0) {
       float* sc = reinterpret_cast<float*>(ch + L.off_sc);
 #pragma unroll
       for (int u = 0; u < SCMAX; ++u) {
-        const int q = threadIdx.x + u * WAVES * 64;
-        if (q < F::NSC * L.sc_stride) sc[q] = bf2f(st.sc[u]);  // [j][row]: q = j sc_stride + row
+        const int q = min((int)threadIdx.x + u * WAVES * 64, F::NSC * L.sc_stride - 1);
+        sc[q] = bf2f((uint32_t)st.sc[u]);  // [j][row]: q = j sc_stride + row
       }
     }
   };
 
-  // Two chunk buffers and two register sets: step i's MFMAs run from buffer i & 1; the
-  // activation of step i + 2 is fetched into register set i & 1 (its previous contents, step
-  // i, went to LDS a step ago), and step i + 1's, fetched a whole step earlier, is written to
-  // the other buffer (whose step i - 1 every wave finished before the last barrier); one
-  // barrier per step publishes it. The fetches thus have a step of MFMAs to arrive in.
-  Staged rr[2];
-  fetch_x(step0, rr[0]);
-  if (nst > 1) fetch_x(step0 + 1, rr[1]);
+  // Pipeline: register sets rr[p] hold the activation of the steps = p (mod PF), buf[p] their
+  // weights; both are fetched PF steps ahead, the activation of a step just before its weights.
+  // Step i: its MFMAs read chunk buffer i & 1 and buf[i % PF]; then the activation and weights
+  // of step i + PF refill rr/buf[i % PF]; then the activation of step i + 1 (fetched before the
+  // weights of step i + 1, so waiting for it waits for nothing the MFMAs did not) goes to the
+  // other chunk buffer, whose step i - 1 every wave finished before the last barrier; one
+  // barrier per step publishes it. Steps past the slice are clamped to its last (cache hits).
+  uint4 buf[PF][RW][F::LOADS];
+  Staged rr[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    fetch_x(min(step0 + p, last), rr[p]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, lrow[r], min(step0 + p, last), lane);
+  }
   put_x(lds, rr[0]);
   __syncthreads();
   f32x4 acc[RW][MT];
@@ -253,24 +286,29 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xoff[mt] = min(16 * mt + (lane & 15), a.m - 1) * L.xstride;
 
-  for (int i0 = 0; i0 < nst; i0 += PF) {
+  // Every lambda is inlined: an outlined one would take the register arrays by address (scratch).
+  auto body = [&](int i, auto pc) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value;
+    skinny_step<F, MT, RW>(acc, buf[p], lds + (i & 1) * L.chunk, L, lane, xoff, rowl);
+    __builtin_amdgcn_sched_barrier(0);
+    const int nx = min(step0 + i + PF, last);
+    fetch_x(nx, rr[p]);
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const int i = i0 + p;
-      if (i < nst) {  // uniform across the workgroup
-        if (i + 2 < nst) fetch_x(step0 + i + 2, rr[p & 1]);
-        skinny_step<F, MT, RW>(acc, buf[p], lds + (i & 1) * L.chunk, L, lane, xoff, rowl);
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-          load_chunk<F>(buf[p][r], a, act[r] ? wrow[r] : weight_row(a, tg * WAVES * RW, lane & 15),
-                        min(step0 + i + PF, last), lane);
-        if (i + 1 < nst) put_x(lds + ((i + 1) & 1) * L.chunk, rr[(p + 1) & 1]);
-        __syncthreads();
-      }
-    }
-  }
+    for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, lrow[r], nx, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    put_x(lds + ((i + 1) & 1) * L.chunk, rr[(p + 1) % PF]);
+    __syncthreads();
+  };
+  int i0 = 0;
+  for (; i0 + PF <= nst; i0 += PF) static_for<0, PF>([&](auto pc) __attribute__((always_inline)) { body(i0 + decltype(pc)::value, pc); });
+  static_for<0, PF>([&](auto pc) __attribute__((always_inline)) {  // the last nst % PF steps (uniform branches)
+    if (i0 + decltype(pc)::value < nst) body(i0 + decltype(pc)::value, pc);
+  });
 
   // Epilogue: lane holds rows 4 (lane >> 4) + 0..3 of each tile for token 16 mt + (lane & 15).
+  // K-slice planes shared through tickets go through a buffer resource at device scope.
+  const __amdgpu_buffer_rsrc_t wr =
+      skinny_rsrc(a.work, a.tickets != nullptr ? (unsigned)a.splits * (unsigned)a.m * (unsigned)a.n * 4u : 0u);
   const int r0 = 4 * (lane >> 4);
   const uint16_t* ws = reinterpret_cast<const uint16_t*>(a.ws);
   uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
@@ -290,8 +328,16 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
       if (a.splits > 1) {  // fp32 plane s, rows in natural order
         if (mm < a.m) {
           float* plane = a.work + ((size_t)s * a.m + mm) * a.n;
+          if (a.tickets != nullptr) {  // read by the row group's last workgroup below
+            // rows r0 .. r0 + 3 of a tile are consecutive weight rows: one 16-byte store
+            const unsigned off = (unsigned)(((size_t)s * a.m + mm) * a.n + weight_row(a, tile[r], r0)) * 4u;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+                wr, (int)off, 0, kSc1);
+          } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) plane[weight_row(a, tile[r], r0 + i)] = v[i];
+            for (int i = 0; i < 4; ++i) plane[weight_row(a, tile[r], r0 + i)] = v[i];
+          }
         }
       } else if constexpr (SW) {
         // Tile rows 0..7 are gate rows 8 tile + 0..7 (lanes 0..31), rows 8..15 the matching up
@@ -309,6 +355,66 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
         store_pair(y, (size_t)mm * a.n + o, v[0], v[1]);
         store_pair(y, (size_t)mm * a.n + o + 2, v[2], v[3]);
       }
+    }
+  }
+  if (a.splits == 1 || a.tickets == nullptr) return;
+
+  // K slices with tickets: the row group's last workgroup to finish sums the planes in slice
+  // order, as qlx_reduce_planes / qlx_swiglu would in a second launch (the same sums, so the
+  // same bits). The partials went out with device-coherent stores; every wave waits for its
+  // stores before the ticket is taken (a workgroup-scope release does not wait for them).
+  __shared__ int s_last;
+  publish_stores();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&a.tickets[tg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == a.splits - 1;
+    if (s_last) __hip_atomic_store(&a.tickets[tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // Thread items: 4 consecutive output rows of one token (SwiGLU: 4 gate rows and their up
+  // rows), each plane's chunk one 16-byte device-scope load, 4 planes in flight at a time.
+  constexpr int RT = WAVES * RW, QUADS = SW ? 2 : 4;  // 4-row chunks per tile
+  const int per_tok = RT * QUADS;
+  const unsigned pstride = (unsigned)a.m * (unsigned)a.n * 4u;
+  auto f4 = [](const u32x4& u) { return f32x4{__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]),
+                                              __uint_as_float(u[3])}; };
+  for (int idx = threadIdx.x; idx < per_tok * a.m; idx += WAVES * 64) {
+    const int mm = idx / per_tok, c = idx - mm * per_tok;
+    const int t = tg * RT + c / QUADS, q4 = 4 * (c - (c / QUADS) * QUADS);
+    if (t >= a.ntiles) continue;
+    const int row = SW ? 8 * t + q4 : 16 * t + q4;  // first of the 4 rows (SwiGLU: gate rows)
+    const unsigned off = (unsigned)((size_t)mm * a.n + row) * 4u;
+    f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = 0; sp0 < a.splits; sp0 += 4) {
+      u32x4 lg[4], lu[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int sp = min(sp0 + j, a.splits - 1);
+        lg[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(off + sp * pstride), 0, kSc1);
+        if constexpr (SW) lu[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(off + sp * pstride + a.half * 4), 0, kSc1);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sp0 + j < a.splits) {  // slice order
+          const f32x4 vg = f4(lg[j]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) g[i] += vg[i];
+          if constexpr (SW) {
+            const f32x4 vu = f4(lu[j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] += vu[i];
+          }
+        }
+      }
+    }
+    if constexpr (SW) {
+      store_pair(y, (size_t)mm * a.half + row, swiglu_bf(g[0], u[0]), swiglu_bf(g[1], u[1]));
+      store_pair(y, (size_t)mm * a.half + row + 2, swiglu_bf(g[2], u[2]), swiglu_bf(g[3], u[3]));
+    } else {
+      store_pair(y, (size_t)mm * a.n + row, g[0], g[1]);
+      store_pair(y, (size_t)mm * a.n + row + 2, g[2], g[3]);
     }
   }
 }
@@ -338,8 +444,9 @@ hipError_t skinny_mt(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStrea
   return skinny_launch<F, 4, WAVES>(a, L, sps, st);
 }
 
-// Waves and K slices: 4 waves per workgroup (two workgroups per CU), and K slices until about
-// 240 workgroups, each slice at least 2 steps (the weight pipeline).
+// Waves and K slices: 4 waves per workgroup, and K slices until about 160 workgroups up to 32
+// tokens (measured on the Qwen3 shapes: gate_up runs fastest as 152 whole-K workgroups, down as
+// 8 K slices of 20 row groups), 240 from 33 tokens; each slice at least 2 steps.
 template <class F>
 void skinny_plan(int m, int n, int k, int* waves, int* splits) {
   const int nsteps = k / F::KSTEP;
@@ -347,7 +454,8 @@ void skinny_plan(int m, int n, int k, int* waves, int* splits) {
   *waves = 4;
   const int rt = 4 * skinny_rw(skinny_mt_of(m));
   const int groups = (ntiles + rt - 1) / rt;
-  int s = (240 + groups - 1) / groups;
+  const int target = skinny_mt_of(m) == 4 ? 240 : 160;
+  int s = target / groups;
   const int most = nsteps / 2 > 1 ? nsteps / 2 : 1;
   if (s > most) s = most;
   if (s < 1) s = 1;
@@ -381,12 +489,15 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   a.half = n / 2;
   a.tiled = 1;
   a.work = plan->workspace;
+  a.tickets = splits > 1 ? plan->tickets : nullptr;
+  QLX_REQUIRE(a.tickets == nullptr || (long long)splits * m * n * 4 < (1ll << 31),
+              "%s: %d planes of %d x %d floats exceed the 2 GiB a shared reduction addresses", name, splits, m, n);
   const SkinnyLayout L = plan->waves == 8 ? skinny_layout<F>(m, 8) : skinny_layout<F>(m, 4);
   QLX_REQUIRE(2 * L.chunk <= kLdsLimit, "%s: %d bytes of LDS", name, 2 * L.chunk);
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = plan->waves == 8 ? skinny_mt<F, 8>(a, L, sps, st) : skinny_mt<F, 4>(a, L, sps, st);
   if (e != hipSuccess) return hip_status(e, name);
-  if (splits > 1) {
+  if (splits > 1 && a.tickets == nullptr) {  // without tickets: the planes reduced in a second launch
     if (mode == QLX_MODE_SWIGLU) return qlx_swiglu(nullptr, plan->workspace, splits, a.y, m, n / 2, stream);
     return qlx_reduce_planes(plan->workspace, a.y, (long long)m * n, splits, stream);
   }

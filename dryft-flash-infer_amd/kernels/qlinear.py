@@ -163,8 +163,10 @@ def _mode(swiglu=False, planes=False):
     return _lib.MODE_SWIGLU if swiglu else (_lib.MODE_PLANES if planes else _lib.MODE_BF16)
 
 
-def _skinny(fmt, q, s, x, n, k, swiglu):
-    """The skinny GEMM (``qlx_linear_skinny``): the activation streams through LDS per K step."""
+def _skinny(fmt, q, s, x, n, k, swiglu, fused_reduce=False):
+    """The skinny GEMM (``qlx_linear_skinny``): the activation streams through LDS per K step.
+    K slices write fp32 planes that the row group's last workgroup reduces in slice order
+    (``fused_reduce``: split-K tickets) or a second launch reduces (bit-identical)."""
     m = x.shape[0]
     mode = _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16
     plan = _lib.Plan()
@@ -174,6 +176,8 @@ def _skinny(fmt, q, s, x, n, k, swiglu):
     if plan.splits > 1:  # fp32 planes, reduced in slice order inside the call
         work = torch.empty((plan.splits, m, n), dtype=torch.float32, device=x.device)
         plan.workspace = work.data_ptr()
+        if fused_reduce:  # one counter per row group: n / 16 always suffices
+            plan.tickets = _lib.tickets(x.device, n // 16).data_ptr()
     _lib.call("qlx_linear_skinny", fmt, _lib.ptr(q), _lib.ptr(s), _lib.ptr(x), _lib.ptr(out), m, n, k,
               ctypes.byref(plan), _lib.stream(x.device))
     return out

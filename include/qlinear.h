@@ -145,8 +145,11 @@ int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y,
 /* Skinny GEMM for 16..64 tokens (speculative verification, small batches), W4A16 or W8A16
  * in the MI355X tile layout: the activation streams through LDS one K step at a time, shared
  * by a workgroup's waves; K slices (plan->splits > 1) write fp32 planes to plan->workspace
- * ([splits][m][n]) that are reduced in slice order (qlx_reduce_planes, or qlx_swiglu for
- * mode SWIGLU) in the same call. Same arithmetic as qlx_linear_w4a16 / qlx_linear_w8a16.
+ * ([splits][m][n]) that are reduced in slice order: with plan->tickets (>= n/16 int32, zero
+ * before the first call, left zero by every call; calls sharing them must not overlap) by the
+ * last workgroup of each row group in the same launch, else by a second launch
+ * (qlx_reduce_planes, or qlx_swiglu for mode SWIGLU) -- the same sums either way, bit-identical.
+ * Same arithmetic as qlx_linear_w4a16 / qlx_linear_w8a16.
  * Serves the batches the reference runs through cuda_fp8.matmul's 8-token tiles
  * (engine/kernels/cuda_fp8.py:1227-1234, 1316-1330). qlx_plan_skinny fills waves (4 or 8)
  * and splits for a shape. */
