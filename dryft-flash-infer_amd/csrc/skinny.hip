@@ -5,18 +5,20 @@
 // Past 16 tokens that costs too much: the staged slice outgrows LDS, so K is cut into many
 // slices (each re-staging 64 tokens of x and writing fp32 partials), and at 64 tokens the
 // registers spill. Here the activation streams through LDS one K step at a time instead:
-//   * a workgroup owns WAVES x RW 16-row tiles (RW = 2 per wave up to 32 tokens: every
-//     activation fragment read from LDS feeds two tiles' MFMAs) and one K slice; every wave runs the same steps, so
-//     the waves share each staged activation chunk [m][KSTEP] and its scales, in two
-//     buffers: while a step's MFMAs run, the next step's activation is fetched and written
-//     to the other buffer, and one barrier per step publishes it;
-//   * weights stream into registers PF steps ahead, in the MI355X tile layout, and go
-//     through the format's MFMA step with the decode kernel's arithmetic: per-group fp32
-//     partials times the group scale, the code bias removed by the same MFMA chain with
-//     every code at the bias (run here on the fragments the step reads anyway);
-//   * K slices write fp32 planes [slices][m][n] that the plane consumers reduce in slice
-//     order (qlx_reduce_planes, qlx_swiglu): deterministic, like the reference's split-K
-//     planes (engine/kernels/cuda_fp8.py:965-981).
+//   * a workgroup owns WAVES x RW 16-row tiles (RW = 1 by default; 2, up to 32 tokens, lets
+//     every activation fragment read from LDS feed two tiles' MFMAs) and one K slice; every
+//     wave runs the same steps, so the waves share each staged activation chunk
+//     [16 MT rows][KSTEP] and its scales, in two LDS buffers, one barrier per step;
+//   * the activation and the weights of step i + PF are fetched together, PF steps ahead,
+//     with every load unconditional, so the in-order memory counter waits only for what a
+//     step needs; weights come in the MI355X tile layout and go through the format's MFMA
+//     step with the decode kernel's arithmetic: per-group fp32 partials times the group
+//     scale, the code bias removed by the same MFMA chain with every code at the bias (run
+//     here on the fragments the step reads anyway);
+//   * K slices write fp32 planes [slices][m][n] reduced in slice order, by the plane
+//     consumers (qlx_reduce_planes, qlx_swiglu) or, with tickets, by the row group's last
+//     workgroup: deterministic, like the reference's split-K planes
+//     (engine/kernels/cuda_fp8.py:965-981).
 // The reference serves these batches with the same kernels as decode, up to 64 rows in
 // tiles of 8 tokens (engine/kernels/cuda_fp8.py:1227-1234, 1404-1423).
 #include "gemm_launch.h"
@@ -31,7 +33,7 @@ __host__ __device__ constexpr int skinny_pf(int mt, bool wide) { return wide || 
 // chains spill at 256.
 // 16-row tiles per wave, sharing each activation fragment read from LDS: two up to 32 tokens,
 // one at 64 (two would need more than the 256 registers of two waves per SIMD).
-__host__ __device__ constexpr int skinny_rw(int mt) { return mt >= 4 ? 1 : 2; }
+__host__ __device__ constexpr int skinny_rw_max(int mt) { return mt >= 4 ? 1 : 2; }
 // Token fragments (16 tokens each) a batch is computed with: 1, 2 or 4 (33..48 tokens run as 4).
 __host__ __device__ constexpr int skinny_mt_of(int m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
@@ -45,10 +47,10 @@ struct SkinnyLayout {
 __host__ __device__ constexpr int up16(int v) { return (v + 15) & ~15; }
 
 template <class F>
-__host__ __device__ inline SkinnyLayout skinny_layout(int m, int waves) {
+__host__ __device__ inline SkinnyLayout skinny_layout(int m, int waves, int rw) {
   SkinnyLayout L{};
   L.xstride = F::KSTEP * F::XBYTES + 16;  // rows 4 banks apart: a B read of 16 rows is conflict-free
-  L.sc_stride = 16 * waves * skinny_rw(skinny_mt_of(m));
+  L.sc_stride = 16 * waves * rw;
   L.off_sc = up16(16 * skinny_mt_of(m) * L.xstride);
   L.chunk = up16(L.off_sc + (F::NSC > 0 ? F::NSC : 0) * L.sc_stride * 4);
   return L;
@@ -174,14 +176,15 @@ __device__ __forceinline__ void static_for(Fn&& fn) {
 }
 
 // Two workgroups per CU (each wave at most 256 registers), or one for the wide instances.
-template <class F, int MT, int WAVES, bool SW>
+template <class F, int MT, int RW, int WAVES, bool SW>
 __global__ void __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(WAVES == 4 && !(MT == 4 && F::NSC > 0) ? 2 : 1)))
 skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
   static_assert(F::LOADS == 2, "a tile step is two 1 KB loads per wave");
   static_assert(F::NSC == 0 || std::is_same<F, FmtW4>::value, "group scales as W4A16 lays them out");
   extern __shared__ __align__(16) char lds[];
-  constexpr int PF = skinny_pf(MT, WAVES == 4 && MT == 4 && F::NSC > 0), RW = skinny_rw(MT);
+  static_assert(RW >= 1 && RW <= skinny_rw_max(MT), "tiles per wave");
+  constexpr int PF = skinny_pf(MT, WAVES == 4 && MT == 4 && F::NSC > 0);
   constexpr int SPR = SkinnyStage<F, WAVES, MT>::PER_ROW, SMAX = SkinnyStage<F, WAVES, MT>::MAX;
   constexpr int CHUNKS = SkinnyStage<F, WAVES, MT>::CHUNKS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -419,43 +422,45 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
   }
 }
 
-template <class F, int MT, int WAVES>
+template <class F, int MT, int RW, int WAVES>
 hipError_t skinny_launch(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStream_t st) {
   const int lds = 2 * L.chunk;
   const dim3 grid(a.tile_groups * a.splits), block(WAVES * 64);
-  const void* fn = a.mode == QLX_MODE_SWIGLU ? reinterpret_cast<const void*>(&skinny_kernel<F, MT, WAVES, true>)
-                                              : reinterpret_cast<const void*>(&skinny_kernel<F, MT, WAVES, false>);
+  const void* fn = a.mode == QLX_MODE_SWIGLU ? reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, true>)
+                                              : reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, false>);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
   }
   if (a.mode == QLX_MODE_SWIGLU)
-    skinny_kernel<F, MT, WAVES, true><<<grid, block, lds, st>>>(a, L, sps);
+    skinny_kernel<F, MT, RW, WAVES, true><<<grid, block, lds, st>>>(a, L, sps);
   else
-    skinny_kernel<F, MT, WAVES, false><<<grid, block, lds, st>>>(a, L, sps);
+    skinny_kernel<F, MT, RW, WAVES, false><<<grid, block, lds, st>>>(a, L, sps);
   return hipGetLastError();
 }
 
 template <class F, int WAVES>
 hipError_t skinny_mt(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStream_t st) {
-  const int mt = skinny_mt_of(a.m);  // the plan and the layout derive the tiles per wave from it too
-  if (mt == 1) return skinny_launch<F, 1, WAVES>(a, L, sps, st);
-  if (mt == 2) return skinny_launch<F, 2, WAVES>(a, L, sps, st);
-  return skinny_launch<F, 4, WAVES>(a, L, sps, st);
+  const int mt = skinny_mt_of(a.m), rw = a.rt / WAVES;
+  if (mt == 1) return rw == 2 ? skinny_launch<F, 1, 2, WAVES>(a, L, sps, st) : skinny_launch<F, 1, 1, WAVES>(a, L, sps, st);
+  if (mt == 2) return rw == 2 ? skinny_launch<F, 2, 2, WAVES>(a, L, sps, st) : skinny_launch<F, 2, 1, WAVES>(a, L, sps, st);
+  return skinny_launch<F, 4, 1, WAVES>(a, L, sps, st);
 }
 
-// Waves and K slices: 4 waves per workgroup, and K slices until about 160 workgroups up to 32
-// tokens (measured on the Qwen3 shapes: gate_up runs fastest as 152 whole-K workgroups, down as
-// 8 K slices of 20 row groups), 240 from 33 tokens; each slice at least 2 steps.
+// Waves, tiles per wave and K slices: 4 waves per workgroup, one tile per wave (two, which reuse
+// each activation fragment read from LDS twice, measured no faster on any config-4 shape: gate_up
+// 12.6 vs 12.7 us at 16 tokens, 17.4 vs 16.6 at 32; down 13.1 vs 11.0 at 16), and K slices until
+// about 240 workgroups (gate_up: 304 whole-K workgroups; down: 40 row groups x 6 slices), each
+// slice at least 2 steps. Measured on the Qwen3 config-4 shapes over every slice count.
 template <class F>
-void skinny_plan(int m, int n, int k, int* waves, int* splits) {
+void skinny_plan(int m, int n, int k, int* waves, int* rw, int* splits) {
   const int nsteps = k / F::KSTEP;
   const int ntiles = n / 16;  // SwiGLU tiles hold 8 gate + 8 up rows: also n / 16
   *waves = 4;
-  const int rt = 4 * skinny_rw(skinny_mt_of(m));
+  *rw = 1;
+  const int rt = 4 * *rw;
   const int groups = (ntiles + rt - 1) / rt;
-  const int target = skinny_mt_of(m) == 4 ? 240 : 160;
-  int s = target / groups;
+  int s = 240 / groups;
   const int most = nsteps / 2 > 1 ? nsteps / 2 : 1;
   if (s > most) s = most;
   if (s < 1) s = 1;
@@ -470,6 +475,8 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
               "%s: n=%d k=%d do not fit the tiled format", name, n, k);
   QLX_REQUIRE(mode == QLX_MODE_BF16 || mode == QLX_MODE_SWIGLU, "%s: mode %d", name, mode);
   QLX_REQUIRE(plan->waves == 4 || plan->waves == 8, "%s: waves must be 4 or 8", name);
+  QLX_REQUIRE(plan->rw >= 1 && plan->rw <= skinny_rw_max(skinny_mt_of(m)),
+              "%s: rw=%d tiles per wave (1, or 2 up to 32 tokens)", name, plan->rw);
   const int nsteps = k / F::KSTEP;
   QLX_REQUIRE(plan->splits >= 1 && plan->splits <= nsteps, "%s: splits must be 1..%d", name, nsteps);
   const int sps = (nsteps + plan->splits - 1) / plan->splits;
@@ -483,7 +490,7 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   a.splits = splits;
   a.sps = sps;
   a.kw = 1;
-  a.rt = plan->waves * skinny_rw(skinny_mt_of(m));
+  a.rt = plan->waves * plan->rw;
   a.ntiles = n / 16;
   a.tile_groups = (a.ntiles + a.rt - 1) / a.rt;
   a.half = n / 2;
@@ -492,9 +499,27 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   a.tickets = splits > 1 ? plan->tickets : nullptr;
   QLX_REQUIRE(a.tickets == nullptr || (long long)splits * m * n * 4 < (1ll << 31),
               "%s: %d planes of %d x %d floats exceed the 2 GiB a shared reduction addresses", name, splits, m, n);
-  const SkinnyLayout L = plan->waves == 8 ? skinny_layout<F>(m, 8) : skinny_layout<F>(m, 4);
-  QLX_REQUIRE(2 * L.chunk <= kLdsLimit, "%s: %d bytes of LDS", name, 2 * L.chunk);
   hipStream_t st = (hipStream_t)stream;
+  if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && splits == 1 && a.tile_groups > 256) {
+    // Token blocks: 33..64 tokens over more whole-K row groups than CUs (gate_up: 304) run as
+    // two blocks of at most 32 tokens on the two-workgroups-per-CU instance; the one-per-CU
+    // 64-token instance would run 48 CUs' second workgroup after the first round. The second
+    // block re-reads the weights, mostly from the Infinity Cache. Each token's sums are the
+    // same, so the output is bit-identical.
+    const size_t ybytes = (size_t)(mode == QLX_MODE_SWIGLU ? n / 2 : n) * 2;
+    for (int m0 = 0; m0 < m; m0 += 32) {
+      GemmArgs b = a;
+      b.m = min(32, m - m0);
+      b.x = static_cast<const char*>(a.x) + (size_t)m0 * k * 2;
+      b.y = static_cast<char*>(a.y) + (size_t)m0 * ybytes;
+      const SkinnyLayout Lb = skinny_layout<F>(b.m, 4, plan->rw);
+      const hipError_t e = skinny_mt<F, 4>(b, Lb, sps, st);
+      if (e != hipSuccess) return hip_status(e, name);
+    }
+    return QLX_OK;
+  }
+  const SkinnyLayout L = skinny_layout<F>(m, plan->waves, plan->rw);
+  QLX_REQUIRE(2 * L.chunk <= kLdsLimit, "%s: %d bytes of LDS", name, 2 * L.chunk);
   hipError_t e = plan->waves == 8 ? skinny_mt<F, 8>(a, L, sps, st) : skinny_mt<F, 4>(a, L, sps, st);
   if (e != hipSuccess) return hip_status(e, name);
   if (splits > 1 && a.tickets == nullptr) {  // without tickets: the planes reduced in a second launch
@@ -519,11 +544,10 @@ int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan) {
   qlx_plan p = {};
   p.mode = mode;
   p.kw = 1;
-  p.rw = 1;
   if (fmt == QLX_FMT_W4A16)
-    skinny_plan<FmtW4>(m, n, k, &p.waves, &p.splits);
+    skinny_plan<FmtW4>(m, n, k, &p.waves, &p.rw, &p.splits);
   else
-    skinny_plan<FmtW8>(m, n, k, &p.waves, &p.splits);
+    skinny_plan<FmtW8>(m, n, k, &p.waves, &p.rw, &p.splits);
   const int nsteps = k / kstep;
   const int sps = (nsteps + p.splits - 1) / p.splits;
   p.splits = (nsteps + sps - 1) / sps;

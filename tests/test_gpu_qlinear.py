@@ -5,6 +5,8 @@ the reference's dequantize-then-matmul and close to the ex
 per-group statement of what the kernel computes. Every call goes through the C ABI.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -296,3 +298,24 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
         assert O.rel_l2(ys.float().cpu().numpy(), ref) <= 1e-2, (fmt, n, k, m)
         if not sw:
             assert not ys[:, 0].float().abs().sum().item(), "zero weight row must give zero"
+
+
+@pytest.mark.parametrize("m", [33, 64])
+def test_skinny_token_blocks_bit_identical(m):
+    """W4A16 batches of 33-64 tokens over more than 256 whole-K row groups (gate_up 2 x 9728 rows:
+    304) run as two blocks of at most 32 tokens; each token's sums are unchanged, so the output
+    equals, bit for bit, the one-launch 64-token kernel (reached here with an 8-wave plan)."""
+    n, k = 2 * 9728, 2560
+    print(f"skinny token blocks m={m}", flush=True)
+    tiled = qlinear.prepare(qlinear.quantize_w4(weights(n, k, 41).to(DEV)))
+    x = acts(m, k, 900 + m).to(DEV)
+    ys = qlinear.linear_w4a16(x, tiled, swiglu=True)  # default plan: token blocks
+    lib = _lib.lib()
+    plan = _lib.Plan()
+    _lib.check(lib.qlx_plan_skinny(_lib.FMT_W4A16, _lib.MODE_SWIGLU, m, n, k, plan), "plan_skinny")
+    assert plan.waves == 4 and plan.splits == 1 and plan.rw == 1
+    plan.waves = 8  # one launch of the 64-token instance, 8 tiles per workgroup
+    y8 = torch.empty((m, n // 2), dtype=torch.bfloat16, device=DEV)
+    _lib.call("qlx_linear_skinny", _lib.FMT_W4A16, _lib.ptr(tiled.weight), _lib.ptr(tiled.scale), _lib.ptr(x),
+              _lib.ptr(y8), m, n, k, ctypes.byref(plan), _lib.stream(x.device))
+    assert torch.equal(ys, y8), m
