@@ -57,6 +57,7 @@ struct GemmArgs {
   int off_sc, off_xb, off_sx;  // LDS byte offsets (x region starts at 0)
   int sc_stride;     // floats per staged scale row ([step*nsc + j][16*rt])
   int xb_stride;     // floats per token in xb ([m][sps*nsc])
+  int tblocks;       // skinny GEMM: 2 = two 32-token blocks in one launch (else 0)
 };
 
 // Weight row held by tile row r (0..15). SwiGLU tiles pair gate rows 8t..8t+7 with the

@@ -179,7 +179,7 @@ __device__ __forceinline__ void static_for(Fn&& fn) {
 template <class F, int MT, int RW, int WAVES, bool SW>
 __global__ void __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(WAVES == 4 && !(MT == 4 && F::NSC > 0) ? 2 : 1)))
-skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
+skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   static_assert(F::LOADS == 2, "a tile step is two 1 KB loads per wave");
   static_assert(F::NSC == 0 || std::is_same<F, FmtW4>::value, "group scales as W4A16 lays them out");
   extern __shared__ __align__(16) char lds[];
@@ -188,7 +188,17 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
   constexpr int SPR = SkinnyStage<F, WAVES, MT>::PER_ROW, SMAX = SkinnyStage<F, WAVES, MT>::MAX;
   constexpr int CHUNKS = SkinnyStage<F, WAVES, MT>::CHUNKS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tg = blockIdx.x / a.splits, s = blockIdx.x - tg * a.splits;
+  GemmArgs a = a0;
+  int bid = blockIdx.x;
+  if (a.tblocks == 2) {  // token blocks: block ids 16 q + 8 b + x are row group 8 q + x, tokens 32 b..
+    // (ids 8 apart share an XCD, so the second block finds the weights in that XCD's L2)
+    const int b = (bid >> 3) & 1;
+    bid = 8 * (bid >> 4) + (bid & 7);
+    a.x = static_cast<const char*>(a.x) + (size_t)b * 32 * a.k * 2;
+    a.y = static_cast<char*>(a.y) + (size_t)b * 32 * (SW ? a.half : a.n) * 2;
+    a.m = min(32, a.m - 32 * b);
+  }
+  const int tg = bid / a.splits, s = bid - tg * a.splits;
   const int step0 = s * steps_per_slice;
   const int nst = min(a.nsteps, step0 + steps_per_slice) - step0;
   const int last = step0 + nst - 1;
@@ -425,7 +435,7 @@ skinny_kernel(GemmArgs a, SkinnyLayout L, int steps_per_slice) {
 template <class F, int MT, int RW, int WAVES>
 hipError_t skinny_launch(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStream_t st) {
   const int lds = 2 * L.chunk;
-  const dim3 grid(a.tile_groups * a.splits), block(WAVES * 64);
+  const dim3 grid(a.tile_groups * a.splits * (a.tblocks == 2 ? 2 : 1)), block(WAVES * 64);
   const void* fn = a.mode == QLX_MODE_SWIGLU ? reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, true>)
                                               : reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, false>);
   if (lds > 64 * 1024) {
@@ -503,17 +513,23 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && splits == 1 && a.tile_groups > 256) {
     // Token blocks: 33..64 tokens over more whole-K row groups than CUs (gate_up: 304) run as
     // two blocks of at most 32 tokens on the two-workgroups-per-CU instance; the one-per-CU
-    // 64-token instance would run 48 CUs' second workgroup after the first round. The second
-    // block re-reads the weights, mostly from the Infinity Cache. Each token's sums are the
-    // same, so the output is bit-identical.
+    // 64-token instance would run 48 CUs' second workgroup after the first round. With row
+    // groups a multiple of 8, both blocks go in one launch, a row group's two blocks on one XCD
+    // (its L2 serves the second weight read); else two launches, the second block's weights
+    // mostly from the Infinity Cache. Each token's sums are the same: bit-identical output.
+    const SkinnyLayout Lb = skinny_layout<F>(32, 4, plan->rw);
+    if (a.tile_groups % 8 == 0) {
+      a.tblocks = 2;
+      const hipError_t e = skinny_launch<F, 2, 1, 4>(a, Lb, sps, st);
+      return e == hipSuccess ? QLX_OK : hip_status(e, name);
+    }
     const size_t ybytes = (size_t)(mode == QLX_MODE_SWIGLU ? n / 2 : n) * 2;
     for (int m0 = 0; m0 < m; m0 += 32) {
       GemmArgs b = a;
       b.m = min(32, m - m0);
       b.x = static_cast<const char*>(a.x) + (size_t)m0 * k * 2;
       b.y = static_cast<char*>(a.y) + (size_t)m0 * ybytes;
-      const SkinnyLayout Lb = skinny_layout<F>(b.m, 4, plan->rw);
-      const hipError_t e = skinny_mt<F, 4>(b, Lb, sps, st);
+      const hipError_t e = skinny_mt<F, 4>(b, skinny_layout<F>(b.m, 4, plan->rw), sps, st);
       if (e != hipSuccess) return hip_status(e, name);
     }
     return QLX_OK;

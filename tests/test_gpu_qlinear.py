@@ -301,12 +301,14 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
 
 
 @pytest.mark.parametrize("m", [33, 64])
-def test_skinny_token_blocks_bit_identical(m):
-    """W4A16 batches of 33-64 tokens over more than 256 whole-K row groups (gate_up 2 x 9728 rows:
-    304) run as two blocks of at most 32 tokens; each token's sums are unchanged, so the output
-    equals, bit for bit, the one-launch 64-token kernel (reached here with an 8-wave plan)."""
-    n, k = 2 * 9728, 2560
-    print(f"skinny token blocks m={m}", flush=True)
+@pytest.mark.parametrize("n", [2 * 9728, 2 * 8320])
+def test_skinny_token_blocks_bit_identical(m, n):
+    """W4A16 batches of 33-64 tokens over more than 256 whole-K row groups run as two blocks of at
+    most 32 tokens: in one launch where the row groups are a multiple of 8 (gate_up 2 x 9728 rows:
+    304), else in two (2 x 8320 rows: 260). Each token's sums are unchanged, so the output equals,
+    bit for bit, the one-launch 64-token kernel (reached here with an 8-wave plan)."""
+    k = 2560
+    print(f"skinny token blocks m={m} n={n}", flush=True)
     tiled = qlinear.prepare(qlinear.quantize_w4(weights(n, k, 41).to(DEV)))
     x = acts(m, k, 900 + m).to(DEV)
     ys = qlinear.linear_w4a16(x, tiled, swiglu=True)  # default plan: token blocks
