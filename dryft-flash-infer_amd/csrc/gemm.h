@@ -58,6 +58,7 @@ struct GemmArgs {
   int sc_stride;     // floats per staged scale row ([step*nsc + j][16*rt])
   int xb_stride;     // floats per token in xb ([m][sps*nsc])
   int tblocks;       // skinny GEMM: 2 = two 32-token blocks in one launch (else 0)
+  int pm;            // skinny GEMM token blocks: rows of a K-slice plane (the whole batch)
 };
 
 // Weight row held by tile row r (0..15). SwiGLU tiles pair gate rows 8t..8t+7 with the

@@ -196,6 +196,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
     bid = 8 * (bid >> 4) + (bid & 7);
     a.x = static_cast<const char*>(a.x) + (size_t)b * 32 * a.k * 2;
     a.y = static_cast<char*>(a.y) + (size_t)b * 32 * (SW ? a.half : a.n) * 2;
+    a.work += (size_t)b * 32 * a.n;  // K-slice planes keep the whole batch's rows (a.pm)
     a.m = min(32, a.m - 32 * b);
   }
   const int tg = bid / a.splits, s = bid - tg * a.splits;
@@ -340,7 +341,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
       }
       if (a.splits > 1) {  // fp32 plane s, rows in natural order
         if (mm < a.m) {
-          float* plane = a.work + ((size_t)s * a.m + mm) * a.n;
+          float* plane = a.work + ((size_t)s * (a.tblocks == 2 ? a.pm : a.m) + mm) * a.n;
           if (a.tickets != nullptr) {  // read by the row group's last workgroup below
             // rows r0 .. r0 + 3 of a tile are consecutive weight rows: one 16-byte store
             const unsigned off = (unsigned)(((size_t)s * a.m + mm) * a.n + weight_row(a, tile[r], r0)) * 4u;
@@ -510,6 +511,19 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   QLX_REQUIRE(a.tickets == nullptr || (long long)splits * m * n * 4 < (1ll << 31),
               "%s: %d planes of %d x %d floats exceed the 2 GiB a shared reduction addresses", name, splits, m, n);
   hipStream_t st = (hipStream_t)stream;
+  const int wgs = a.tile_groups * splits;
+  if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && a.tickets == nullptr && splits > 1 &&
+      wgs % 8 == 0 && 2 * wgs <= 512) {
+    // K-sliced batches of 33..64 tokens whose two 32-token blocks still fit the two-per-CU
+    // instance in one round (down: 40 row groups x 6 slices = 240 per block): one launch, a
+    // (row group, slice)'s two blocks on one XCD; each block writes its rows of the planes.
+    a.tblocks = 2;
+    a.pm = m;
+    const hipError_t e = skinny_launch<F, 2, 1, 4>(a, skinny_layout<F>(32, 4, plan->rw), sps, st);
+    if (e != hipSuccess) return hip_status(e, name);
+    if (mode == QLX_MODE_SWIGLU) return qlx_swiglu(nullptr, plan->workspace, splits, a.y, m, n / 2, stream);
+    return qlx_reduce_planes(plan->workspace, a.y, (long long)m * n, splits, stream);
+  }
   if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && splits == 1 && a.tile_groups > 256) {
     // Token blocks: 33..64 tokens over more whole-K row groups than CUs (gate_up: 304) run as
     // two blocks of at most 32 tokens on the two-workgroups-per-CU instance; the one-per-CU

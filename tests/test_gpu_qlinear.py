@@ -301,23 +301,27 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
 
 
 @pytest.mark.parametrize("m", [33, 64])
-@pytest.mark.parametrize("n", [2 * 9728, 2 * 8320])
-def test_skinny_token_blocks_bit_identical(m, n):
-    """W4A16 batches of 33-64 tokens over more than 256 whole-K row groups run as two blocks of at
-    most 32 tokens: in one launch where the row groups are a multiple of 8 (gate_up 2 x 9728 rows:
-    304), else in two (2 x 8320 rows: 260). Each token's sums are unchanged, so the output equals,
-    bit for bit, the one-launch 64-token kernel (reached here with an 8-wave plan)."""
-    k = 2560
-    print(f"skinny token blocks m={m} n={n}", flush=True)
+@pytest.mark.parametrize("n,k,sw", [(2 * 9728, 2560, True), (2 * 8320, 2560, True), (2560, 9728, False)])
+def test_skinny_token_blocks_bit_identical(m, n, k, sw):
+    """W4A16 batches of 33-64 tokens run as two blocks of at most 32 tokens where that fills the
+    GPU better: whole-K over more than 256 row groups, in one launch where the row groups are a
+    multiple of 8 (gate_up 2 x 9728 rows: 304), else in two (2 x 8320 rows: 260); K-sliced
+    (down: 40 row groups x 6 slices) in one launch whose blocks write their rows of the planes.
+    Each token's sums are unchanged, so the output equals, bit for bit, the one-launch 64-token
+    kernel (reached here with an 8-wave plan)."""
+    print(f"skinny token blocks m={m} n={n} k={k}", flush=True)
     tiled = qlinear.prepare(qlinear.quantize_w4(weights(n, k, 41).to(DEV)))
     x = acts(m, k, 900 + m).to(DEV)
-    ys = qlinear.linear_w4a16(x, tiled, swiglu=True)  # default plan: token blocks
+    ys = qlinear.linear_w4a16(x, tiled, swiglu=sw)  # default plan: token blocks
     lib = _lib.lib()
+    mode = _lib.MODE_SWIGLU if sw else _lib.MODE_BF16
     plan = _lib.Plan()
-    _lib.check(lib.qlx_plan_skinny(_lib.FMT_W4A16, _lib.MODE_SWIGLU, m, n, k, plan), "plan_skinny")
-    assert plan.waves == 4 and plan.splits == 1 and plan.rw == 1
-    plan.waves = 8  # one launch of the 64-token instance, 8 tiles per workgroup
-    y8 = torch.empty((m, n // 2), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib.qlx_plan_skinny(_lib.FMT_W4A16, mode, m, n, k, plan), "plan_skinny")
+    assert plan.waves == 4 and plan.rw == 1 and (plan.splits == 1) == sw
+    plan.waves = 8  # one launch of the 64-token instance, 8 tiles per workgroup, same K slices
+    work = torch.empty((plan.splits, m, n), dtype=torch.float32, device=DEV)
+    plan.workspace = work.data_ptr() if plan.splits > 1 else None
+    y8 = torch.empty((m, n // 2 if sw else n), dtype=torch.bfloat16, device=DEV)
     _lib.call("qlx_linear_skinny", _lib.FMT_W4A16, _lib.ptr(tiled.weight), _lib.ptr(tiled.scale), _lib.ptr(x),
               _lib.ptr(y8), m, n, k, ctypes.byref(plan), _lib.stream(x.device))
-    assert torch.equal(ys, y8), m
+    assert torch.equal(ys, y8), (m, n, k)
