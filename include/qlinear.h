@@ -149,8 +149,9 @@ int qlx_linear_w4a16(const void* w, const void* w_scale, const void* x, void* y,
  * before the first call, left zero by every call; calls sharing them must not overlap) by the
  * last workgroup of each row group in the same launch, else by a second launch
  * (qlx_reduce_planes, or qlx_swiglu for mode SWIGLU) -- the same sums either way, bit-identical.
- * W4A16 batches of 33..64 tokens with one K slice and more than 256 row groups of 4 tiles run
- * as two token blocks of at most 32 (bit-identical; see skinny.hip).
+ * W4A16 batches of 33..64 tokens on 4-wave plans may run as two token blocks of at most 32
+ * (one K slice over more than 256 row groups; or K slices without tickets whose two blocks fit
+ * 512 workgroups): bit-identical output, chosen inside the call (skinny.hip).
  * Same arithmetic as qlx_linear_w4a16 / qlx_linear_w8a16.
  * Serves the batches the reference runs through cuda_fp8.matmul's 8-token tiles
  * (engine/kernels/cuda_fp8.py:1227-1234, 1316-1330). qlx_plan_skinny fills waves (4 or 8)
