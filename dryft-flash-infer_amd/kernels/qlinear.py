@@ -163,11 +163,13 @@ def _mode(swiglu=False, planes=False):
     return _lib.MODE_SWIGLU if swiglu else (_lib.MODE_PLANES if planes else _lib.MODE_BF16)
 
 
-def _skinny(fmt, q, s, x, n, k, swiglu, fused_reduce=False):
+def _skinny(fmt, q, s, x, n, k, swiglu, fused_reduce=None):
     """The skinny GEMM (``qlx_linear_skinny``): the activation streams through LDS per K step.
     K slices write fp32 planes that the row group's last workgroup reduces in slice order
     (``fused_reduce``: split-K tickets) or a second launch reduces (bit-identical)."""
     m = x.shape[0]
+    if fused_reduce is None:  # up to 32 tokens (33-64 token blocks need the planes launch)
+        fused_reduce = m <= 32
     mode = _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16
     plan = _lib.Plan()
     _lib.check(_lib.lib().qlx_plan_skinny(fmt, mode, m, n, k, plan), "plan_skinny")

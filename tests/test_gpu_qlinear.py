@@ -285,8 +285,9 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
         yd = linear(x, tiled, swiglu=sw, skinny=False)
         # K slices reduced by the row group's last workgroup (tickets) or by a second launch
         code = _lib.FMT_W4A16 if fmt == "w4a16" else _lib.FMT_W8A16
-        yu = qlinear._skinny(code, tiled.weight, tiled.scale, x, n, k, sw, fused_reduce=True)
-        assert torch.equal(ys, yu), (fmt, n, k, m, "fused split-K reduction differs from the planes launch")
+        for fused in (True, False):
+            yu = qlinear._skinny(code, tiled.weight, tiled.scale, x, n, k, sw, fused_reduce=fused)
+            assert torch.equal(ys, yu), (fmt, n, k, m, fused, "fused split-K reduction differs from the planes launch")
         want = yd.float()
         diff = (ys.float() - want).abs()
         rowmax = want.abs().amax(dim=1, keepdim=True)
