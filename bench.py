@@ -189,46 +189,68 @@ def untile(tiled):
     return v.reshape(rows, width).contiguous().view(tiled.dtype).view(rows, cols)
 
 
-def cpu_baseline(stack, reps=3):
-    """The reference's torch CPU dequantize-then-matmul path, timed on the host cores.
-
-    Sample: layer 0's four projections plus the lm_head (the same synthetic weights and
-    activations, copied to host), median of `reps` after one warmup; scaled to a step as
-    36 x layer + lm_head."""
-    sys.path.insert(0, ROOT)
-    from oracle import cpu_baseline as cb
-    fn = cb.LINEARS[stack.fmt]
-    threads = torch.get_num_threads()
-    sample = [c for c in stack.calls[:4]] + [stack.calls[-1]]
-    host = []
-    for name, t, k, sw in sample:
-        # the CPU path reads the row-major packed weight: undo the tile relayout on the host
-        qc = untile(t.weight.cpu())
-        host.append((name, qc, t.scale.cpu(), stack.x[k].cpu()))
-    times = {}
-    for name, q, s, x in host:
-        fn(x, q, s)  # warmup
-        runs = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn(x, q, s)
-            runs.append(time.perf_counter() - t0)
-        times[name] = statistics.median(runs)
-    layer = sum(times[n] for n, _, _, _ in host[:4])
-    step_s = LAYERS * layer + times["lm_head"]
-    model = ""
+def cpu_model_name():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            if ln.startswith("Model name:"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
-        pass
+        return platform.processor()
+
+
+def cpu_baseline(stack, reps=5, warmup=2):
+    """The reference's torch CPU path, timed on the host cores.
+
+    Every projection of the stack (36 distinct layers + the lm_head: the same synthetic
+    weights and activations, copied to host memory in their row-major packed form) runs
+    once per step, each on its own resident input; the step is timed `warmup` + `reps`
+    times and the median of the last `reps` is reported. Two variants: dequantize + matmul
+    per call (the baseline) and the matmul alone on weights dequantized beforehand."""
+    sys.path.insert(0, ROOT)
+    from oracle import cpu_baseline as cb
+    fmt = stack.fmt
+    deq, mm = cb.DEQUANT[fmt], cb.matmul
+    # the CPU path reads the row-major packed weight: undo the tile relayout on the host
+    host = [(untile(t.weight.cpu()), t.scale.cpu(), k) for _, t, k, _ in stack.calls]
+    xs = {k: v.cpu() for k, v in stack.x.items()}
+
+    def timed(step):
+        runs = []
+        for _ in range(warmup + reps):
+            t0 = time.perf_counter()
+            step()
+            runs.append(time.perf_counter() - t0)
+        return statistics.median(runs[warmup:])
+
+    def dequant_matmul():
+        for q, s, k in host:
+            mm(fmt, xs[k], deq(q, s))
+
+    step_s = timed(dequant_matmul)
+    weights = [(deq(q, s), k) for q, s, k in host]
+    del host
+
+    def matmul_only():
+        for w, k in weights:
+            mm(fmt, xs[k], w)
+
+    mm_s = timed(matmul_only)
+    del weights
     return {
-        "value": round(step_s * 1e6, 1), "unit": "us per step", "cores": threads,
+        "value": round(step_s * 1e6, 1), "unit": "us per step", "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"dequantize+matmul (torch CPU, {stack.fmt}, M={stack.m}) of layer 0's qkv/o/gate_up/down "
-                   f"and the lm_head, median of {reps}; step = 36 x layer + lm_head"),
-        "per_call_ms": {k: round(v * 1e3, 3) for k, v in times.items()},
-        "cpu_model": model or platform.processor(), "os_cpu_count": os.cpu_count(),
+        "sample": (f"one whole step: torch CPU dequantize + matmul ({fmt}, M={stack.m}) of every projection of "
+                   f"the 36 distinct layers and the lm_head, median of {reps} steps after {warmup}"),
+        "matmul_only_us": round(mm_s * 1e6, 1),
+        "cpu_model": cpu_model_name(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
         "effective_weight_GBps": round(stack.weight_bytes() / step_s / 1e9, 2),
     }
 
@@ -402,6 +424,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(stack)
+        log(f"cpu baseline {args.workload} M={args.m}: {cpu['value'] / 1e3:.1f} ms per step, matmul only "
+            f"{cpu['matmul_only_us'] / 1e3:.1f} ms ({cpu['cores']} threads, {cpu['cpu_model']})")
     del stack
     torch.cuda.empty_cache()
     if not args.quick:
@@ -414,7 +438,10 @@ def main():
             if (fmt, m) == (args.workload, args.m):
                 continue
             st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=True)
-            per = res.pop("per_projection")
+            if (fmt, m) == ("w4a16", 1) and not args.no_cpu:
+                res["cpu_baseline"] = cpu_baseline(st)
+                log(f"cpu baseline w4a16 M=1: {res['cpu_baseline']['value'] / 1e3:.1f} ms per step "
+                    f"({res['cpu_baseline']['cores']} threads)")
             per_cfg["config2_fp8_w8a8" if fmt == "fp8" else "config3_w4a16"][f"M{m}"] = per
             if m != 4:
                 extra[f"{fmt}_M{m}_stack"] = {k: (round(v, 4 if k == "hbm_frac" else 2) if isinstance(v, float) else v)

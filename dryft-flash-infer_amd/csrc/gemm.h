@@ -59,6 +59,15 @@ struct GemmArgs {
   int xb_stride;     // floats per token in xb ([m][sps*nsc])
   int tblocks;       // skinny GEMM: 2 = two 32-token blocks in one launch (else 0)
   int pm;            // skinny GEMM token blocks: rows of a K-slice plane (the whole batch)
+  // Fused residual add + RMSNorm (qlx_linear_add_norm): y receives delta = bf16(x W^T)
+  // with device-coherent stores; the workgroup that completes the last row block adds
+  // `resid`, normalises with `norm_w` and writes `res_out` and `normed`.
+  const void* resid;
+  const void* norm_w;
+  void* res_out;
+  void* normed;
+  int* an_counter;   // row blocks completed; zero before the launch, zero again after it
+  float eps;
 };
 
 // Weight row held by tile row r (0..15). SwiGLU tiles pair gate rows 8t..8t+7 with the
@@ -909,6 +918,140 @@ __device__ __forceinline__ uint32_t bf16_pair(float v0, float v1) {
 __device__ __forceinline__ void store_pair(uint16_t* y, size_t idx, float v0, float v1) {
   *gmem(reinterpret_cast<uint32_t*>(y + idx)) = bf16_pair(v0, v1);
 }
+// The same pair written device-coherent (agent scope), for values another workgroup of the
+// launch reads back (the fused add-norm tail).
+__device__ __forceinline__ void store_pair_coherent(uint16_t* y, size_t idx, float v0, float v1) {
+  __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(y + idx)), bf16_pair(v0, v1), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 8 bf16 values (16 bytes at element e of p) that other workgroups of this launch wrote: two
+// device-coherent 8-byte loads, each single-copy atomic.
+__device__ __forceinline__ uint4 load8_coherent(const uint16_t* p, size_t e) {
+  const auto q = gmem(reinterpret_cast<const uint64_t*>(p + e));
+  const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return uint4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+}
+
+__device__ __forceinline__ uint4 load8_plain(const uint16_t* p, size_t e) {
+  const u32x4 v = *gmem(reinterpret_cast<const u32x4*>(p + e));
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+// Residual add + RMSNorm of the whole [m][n] output, run by the workgroup that completes the
+// last row block: res = bf16(resid + delta), normed = bf16(bf16(res * rsqrt(mean res^2 + eps)) * w)
+// (the fused epilogue of engine/kernels/cuda_fp8.py:1339-1374 with the rounding of
+// engine/kernels/reference.py:19-28; the same arithmetic as qlx_add_rms_norm). Each token row
+// is taken by a group of G threads (a power of two), which reads it 8 values at a time in two
+// passes: the sum of squares (fp64, reduced over the group in a fixed order), then the outputs.
+__device__ __noinline__ void add_norm_tail(const GemmArgs& a) {
+  __shared__ double s_part[16];
+  const int tid = threadIdx.x;
+  int mp = 1;
+  while (mp < a.m) mp <<= 1;
+  const int G = (int)blockDim.x / mp;  // threads per row
+  const int mm = tid / G, gi = tid - mm * G;
+  const bool live = mm < a.m;
+  const int nch = a.n >> 3;
+  const size_t base = (size_t)(live ? mm : 0) * a.n;
+  const uint16_t* dl = reinterpret_cast<const uint16_t*>(a.y);
+  const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.resid);
+  const uint16_t* wn = reinterpret_cast<const uint16_t*>(a.norm_w);
+  auto residual = [](uint4 x, uint4 d, float (&r)[8]) {
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ds[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t xb = e & 1 ? xs[e >> 1] >> 16 : xs[e >> 1] & 0xffffu;
+      const uint32_t db = e & 1 ? ds[e >> 1] >> 16 : ds[e >> 1] & 0xffffu;
+      r[e] = round_bf(bf2f(xb) + bf2f(db));
+    }
+  };
+  constexpr int U = 4;  // chunks in flight per thread
+  double ss = 0.0;
+  for (int c0 = gi; live && c0 < nch; c0 += U * G) {
+    uint4 d[U], x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * G;
+      if (c < nch) {
+        d[u] = load8_coherent(dl, base + (size_t)c * 8);
+        x[u] = load8_plain(xr, base + (size_t)c * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u * G < nch) {
+        float r[8];
+        residual(x[u], d[u], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (double)r[e] * (double)r[e];
+      }
+    }
+  }
+  const int lanes = G < 64 ? G : 64;
+  for (int o = lanes >> 1; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  double total = ss;
+  if (G > 64) {  // a row spans G / 64 waves: their sums in wave order
+    const int wpg = G >> 6;
+    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+    __syncthreads();
+    total = 0.0;
+    if (live)
+      for (int w = 0; w < wpg; ++w) total += s_part[mm * wpg + w];
+  }
+  // mean rounded to fp32, + eps and 1/sqrt in fp32, as torch's rsqrt(mean + eps)
+  const float scale = 1.0f / sqrtf((float)(total / (double)a.n) + a.eps);
+  uint16_t* ro = reinterpret_cast<uint16_t*>(a.res_out);
+  uint16_t* yo = reinterpret_cast<uint16_t*>(a.normed);
+  for (int c0 = gi; live && c0 < nch; c0 += U * G) {
+    uint4 d[U], x[U], w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * G;
+      if (c < nch) {
+        d[u] = load8_coherent(dl, base + (size_t)c * 8);
+        x[u] = load8_plain(xr, base + (size_t)c * 8);
+        w[u] = load8_plain(wn, (size_t)c * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * G;
+      if (c < nch) {
+        float r[8];
+        residual(x[u], d[u], r);
+        const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        uint32_t rb[4], yb[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float w0 = bf2f(ws[e >> 1] & 0xffffu), w1 = bf2f(ws[e >> 1] >> 16);
+          rb[e >> 1] = bf16_pair(r[e], r[e + 1]);
+          yb[e >> 1] = bf16_pair(round_bf(round_bf(r[e] * scale) * w0), round_bf(round_bf(r[e + 1] * scale) * w1));
+        }
+        *gmem(reinterpret_cast<u32x4*>(ro + base + (size_t)c * 8)) = u32x4{rb[0], rb[1], rb[2], rb[3]};
+        *gmem(reinterpret_cast<u32x4*>(yo + base + (size_t)c * 8)) = u32x4{yb[0], yb[1], yb[2], yb[3]};
+      }
+    }
+  }
+}
+
+// After a workgroup has written a completed row block of delta (device-coherent stores): count
+// it, and let the workgroup that completes the last row block run the add-norm tail. The
+// counter is left at zero for the next launch.
+__device__ __forceinline__ void add_norm_ticket(const GemmArgs& a) {
+  __shared__ int s_tail;
+  publish_stores();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(a.an_counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_tail = prev == a.tile_groups - 1;
+    if (s_tail) __hip_atomic_store(a.an_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_tail) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  add_norm_tail(a);
+}
 
 // y = bf16(bf16(silu(g)) * u) with g and u rounded to bf16 first (swiglu.py:12-30).
 __device__ __forceinline__ float swiglu_bf(float g, float u) {
@@ -1036,7 +1179,7 @@ __device__ __forceinline__ float tile_value(const GemmArgs& a, const char* redp,
 // Combine the kw waves of each tile, write the output (bf16, SwiGLU or fp32 planes), and
 // when the row block is cut into pieces let the last workgroup to finish reduce the
 // planes in piece order.
-template <class F, int MT, int RW, int WAVES, bool SW>
+template <class F, int MT, int RW, int WAVES, bool SW, bool AN = false>
 __device__ __forceinline__ void item_finish(const GemmArgs& a, char* lds, const Item<RW>& it,
                                             const f32x4 (&acc)[RW][MT]) {
   const int tg = it.tg, s = it.s, np = it.np;
@@ -1080,14 +1223,20 @@ __device__ __forceinline__ void item_finish(const GemmArgs& a, char* lds, const 
         store_coherent(pl, v0);
         if (two) store_coherent(pl + 1, v1);
       } else if (two && (a.n & 1) == 0) {
-        store_pair(y, (size_t)mm * a.n + row, v0, v1);
+        if constexpr (AN)
+          store_pair_coherent(y, (size_t)mm * a.n + row, v0, v1);
+        else
+          store_pair(y, (size_t)mm * a.n + row, v0, v1);
       } else {
         y[(size_t)mm * a.n + row] = f2bf(v0);
         if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
       }
     }
   }
-  if (direct) return;
+  if (direct) {
+    if constexpr (AN) add_norm_ticket(a);
+    return;
+  }
 
   // ---- split-K: the last workgroup of this row block reduces the planes in slice order.
   // The partials went out with device-coherent stores; every wave waits for its stores to
@@ -1131,18 +1280,22 @@ __device__ __forceinline__ void item_finish(const GemmArgs& a, char* lds, const 
         if (two) v1 += load_coherent(p + sp * plane + 1);
       }
       if (two && (a.n & 1) == 0) {
-        store_pair(y, (size_t)mm * a.n + row, v0, v1);
+        if constexpr (AN)
+          store_pair_coherent(y, (size_t)mm * a.n + row, v0, v1);
+        else
+          store_pair(y, (size_t)mm * a.n + row, v0, v1);
       } else {
         y[(size_t)mm * a.n + row] = f2bf(v0);
         if (two) y[(size_t)mm * a.n + row + 1] = f2bf(v1);
       }
     }
   }
+  if constexpr (AN) add_norm_ticket(a);
 }
 
 // One launch = one linear call. SW: the SwiGLU epilogue (a separate instantiation, so
-// profiles tell it apart).
-template <class F, int MT, int RW, int WAVES, bool SW>
+// profiles tell it apart); AN: the fused residual add + RMSNorm after the last row block.
+template <class F, int MT, int RW, int WAVES, bool SW, bool AN = false>
 __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   extern __shared__ __align__(16) char lds[];
   int tg, s;
@@ -1152,7 +1305,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   item_prefetch<F, RW>(a, tg, s, it, buf);
   f32x4 acc[RW][MT];
   item_main<F, MT, RW, WAVES>(a, XPlain{}, lds, it, buf, acc);
-  item_finish<F, MT, RW, WAVES, SW>(a, lds, it, acc);
+  item_finish<F, MT, RW, WAVES, SW, AN>(a, lds, it, acc);
 }
 
 }  // namespace qlx

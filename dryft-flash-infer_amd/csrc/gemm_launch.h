@@ -68,20 +68,29 @@ inline int check_plan(const qlx_plan* p, int m, int n, int k, int kstep) {
 }
 
 // Opt a kernel into more than 64 KB of dynamic LDS (raised to what the launch needs).
-template <class F, int MT, int RW, int WAVES, bool SW>
+template <class F, int MT, int RW, int WAVES, bool SW, bool AN = false>
 hipError_t allow_lds(int lds) {
   static int allowed = 64 * 1024;
   if (lds <= allowed) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<F, MT, RW, WAVES, SW>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<F, MT, RW, WAVES, SW, AN>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e == hipSuccess) allowed = lds;
   return e;
 }
 
-template <class F, int MT, int RW, int WAVES>
+// AN_OK: this format's entry points include the fused add-norm (qlx_linear_add_norm), which
+// launches the AN instantiation when a.an_counter is set.
+template <class F, int MT, int RW, int WAVES, bool AN_OK>
 hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   const int grid = a.tile_groups * a.splits;
   hipError_t e;
+  if constexpr (AN_OK) {
+    if (a.an_counter) {
+      if ((e = allow_lds<F, MT, RW, WAVES, false, true>(lds)) != hipSuccess) return e;
+      gemm_kernel<F, MT, RW, WAVES, false, true><<<grid, WAVES * 64, lds, st>>>(a);
+      return hipGetLastError();
+    }
+  }
   if (a.mode == QLX_MODE_SWIGLU) {
     if ((e = allow_lds<F, MT, RW, WAVES, true>(lds)) != hipSuccess) return e;
     gemm_kernel<F, MT, RW, WAVES, true><<<grid, WAVES * 64, lds, st>>>(a);
@@ -92,13 +101,14 @@ hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <class F, int MT>
+template <class F, int MT, bool AN_OK>
 hipError_t launch_mt(const GemmArgs& a, const qlx_plan& p, int lds, hipStream_t st) {
-  if (p.waves == 4) return p.rw == 1 ? launch_one<F, MT, 1, 4>(a, lds, st) : launch_one<F, MT, 2, 4>(a, lds, st);
-  return p.rw == 1 ? launch_one<F, MT, 1, 8>(a, lds, st) : launch_one<F, MT, 2, 8>(a, lds, st);
+  if (p.waves == 4)
+    return p.rw == 1 ? launch_one<F, MT, 1, 4, AN_OK>(a, lds, st) : launch_one<F, MT, 2, 4, AN_OK>(a, lds, st);
+  return p.rw == 1 ? launch_one<F, MT, 1, 8, AN_OK>(a, lds, st) : launch_one<F, MT, 2, 8, AN_OK>(a, lds, st);
 }
 
-template <class F>
+template <class F, bool AN_OK = false>
 int launch_gemm(const char* name, GemmArgs a, const qlx_plan* plan, int m, int n, int k, void* stream) {
   int rc = check_plan(plan, m, n, k, F::KSTEP);
   if (rc) return rc;
@@ -116,13 +126,25 @@ int launch_gemm(const char* name, GemmArgs a, const qlx_plan* plan, int m, int n
   const int mt = (m + 15) / 16;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
+  if (a.an_counter) {
+    QLX_REQUIRE(AN_OK && p.mode == QLX_MODE_BF16, "%s: the fused add-norm takes bf16 output (mode 0)", name);
+    QLX_REQUIRE(n % 8 == 0, "%s: the fused add-norm needs n %% 8 == 0 (n=%d)", name, n);
+    QLX_REQUIRE(a.resid && a.norm_w && a.res_out && a.normed, "%s: add-norm operand is NULL", name);
+  }
   if (mt == 1)
-    e = launch_mt<F, 1>(a, p, lds, st);
+    e = launch_mt<F, 1, AN_OK>(a, p, lds, st);
   else if (mt == 2)
-    e = launch_mt<F, 2>(a, p, lds, st);
+    e = launch_mt<F, 2, AN_OK>(a, p, lds, st);
   else
-    e = launch_mt<F, 4>(a, p, lds, st);
+    e = launch_mt<F, 4, AN_OK>(a, p, lds, st);
   return hip_status(e, name);
 }
+
+// Fused residual add + RMSNorm launches (a.an_counter and the add-norm operands set), one per
+// format, each defined in the file that instantiates that format's GEMM.
+int add_norm_w8a16(const GemmArgs& a, const qlx_plan* plan, int m, int n, int k, void* stream);
+int add_norm_w4a16(const GemmArgs& a, const qlx_plan* plan, int m, int n, int k, void* stream);
+int add_norm_fp8(const GemmArgs& a, const qlx_plan* plan, int m, int n, int k, void* stream);
+int add_norm_ref(const GemmArgs& a, int bits, const qlx_plan* plan, int m, int n, int k, void* stream);
 
 }  // namespace qlx

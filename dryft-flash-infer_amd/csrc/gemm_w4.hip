@@ -9,5 +9,10 @@ extern "C" int qlx_linear_w4a16(const void* w, const void* w_scale, const void* 
   a.x = x;
   a.y = y;
   a.tiled = tiled;
-  return qlx::launch_gemm<qlx::FmtW4>("linear_w4a16", a, plan, m, n, k, stream);
+  return qlx::launch_gemm<qlx::FmtW4, true>("linear_w4a16", a, plan, m, n, k, stream);
+}
+
+// The fused residual add + RMSNorm form (qlx_linear_add_norm) of the same kernels.
+int qlx::add_norm_w4a16(const GemmArgs& a, const qlx_plan* plan, int m, int n, int k, void* stream) {
+  return launch_gemm<FmtW4, true>("linear_add_norm", a, plan, m, n, k, stream);
 }

@@ -77,6 +77,7 @@ SIGNATURES = {
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8wo": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_int8": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_add_norm": ([_I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P, _PLAN, _P], _I),
     "qlx_reduce_planes": ([_P, _P, _LL, _I, _P], _I),
     "qlx_residual_planes": ([_P, _P, _P, _LL, _I, _P], _I),
     "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),

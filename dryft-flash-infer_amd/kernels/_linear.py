@@ -56,3 +56,24 @@ def run(fmt, entry, x, n, k, args_before_y, args_after_dims=(), mode=_lib.MODE_B
 
 def splits_for(fmt, mode, m, n, k, config=None, fit=False, comp=1):
     return make_plan(fmt, mode, m, n, k, config, fit, comp).splits
+
+
+def run_add_norm(fmt, weight_args, x, n, k, tiled, residual, norm_weight, eps, delta, counter, config=None):
+    """``qlx_linear_add_norm``: delta = bf16(x W^T) into ``delta``, then (new residual, normed)
+    in the same launch. Split-K workspace and tickets are handled as in ``run``."""
+    m = x.shape[0]
+    device = x.device
+    plan = make_plan(fmt, _lib.MODE_BF16, m, n, k, config, fit=True)
+    work = None
+    if plan.splits > 1:
+        work = torch.empty((plan.splits, m, n), dtype=torch.float32, device=device)
+        plan.workspace = work.data_ptr()
+        count = _lib.lib().qlx_plan_tickets(plan, fmt, m, n, k)
+        plan.tickets = _lib.tickets(device, count).data_ptr()
+    res = torch.empty_like(residual)
+    normed = torch.empty_like(residual)
+    w, ws = weight_args
+    _lib.call("qlx_linear_add_norm", fmt, _lib.ptr(w), _lib.ptr(ws), _lib.ptr(x), m, n, k, int(tiled),
+              _lib.ptr(residual), _lib.ptr(norm_weight), float(eps), _lib.ptr(delta), _lib.ptr(counter),
+              _lib.ptr(res), _lib.ptr(normed), ctypes.byref(plan), _lib.stream(device))
+    return res, normed

@@ -13,7 +13,25 @@ A ``config`` is the reference's race entry ``(warps, splitk[, stage, nshare, rin
 ``splitk`` keeps its meaning (K slices, reduced in slice order); the other fields pick
 NVIDIA kernel variants and have no MI355X counterpart: the library plans the workgroup
 shape itself (``qlx_plan_linear``).
+
+The same signatures also carry the MI355X north-star formats, so an engine that calls
+``prepare(quantize(w, bits=bits))`` and then ``matmul`` / ``matmul_partials`` /
+``gate_up_swiglu`` / ``matmul_add_norm`` reaches them without changing a call site:
+
+* ``quantize(..., fmt=...)`` or the module default ``FORMAT`` (environment variable
+  ``QLX_WEIGHT_FORMAT``) selects ``"ref"`` (the reference's format, the default),
+  ``"w8a16"`` (int8 per output channel, bf16 scales), ``"w4a16"`` (int4 group 128, bf16
+  scales, eight codes per int32 along K), ``"fp8"`` (e4m3 per output channel with the
+  activation quantized per token: FP8 W8A8), or ``"auto"`` (w8a16 for 8 bits, w4a16 for 4);
+* ``prepare`` then relays the codes into the MI355X tile layout and returns a
+  ``FormatPrepared`` with the attributes the engine reads (``bits``, ``k``, ``rows``,
+  ``bytes_moved()``);
+* the linears dispatch on it: ``matmul``/``gate_up_swiglu`` take the library's planned
+  path for the batch (decode kernel, skinny GEMM from 9 tokens, FP8 activation quantized
+  once from 2 tokens), ``matmul_partials``/``splits`` honour the config's split-K.
 """
+
+import os
 
 import torch
 
@@ -21,10 +39,9 @@ from . import _lib, _linear
 
 #: Weight layout selected by ``prepare`` when ``tiled`` is None (engine/kernels/cuda_fp8.py:42-44).
 TILED = True
-#: NVIDIA launch knobs of the reference (programmatic dependent launch, coalesced epilogue);
-#: kept so callers that read them still import, no effect here.
-PDL = 0
-COALESCED = False
+#: Weight format ``quantize`` produces when the call names none (see the module docstring).
+FORMAT = os.environ.get("QLX_WEIGHT_FORMAT", "ref")
+FORMATS = ("ref", "w8a16", "w4a16", "fp8", "auto")
 #: Values per scale (engine/kernels/cuda_fp8.py:57).
 GROUP = 64
 _FUSED_ROWS = 2560   # the hidden width; matmul_add_norm normalises rows of this length
@@ -59,17 +76,40 @@ def _permutation(device) -> torch.Tensor:
     return torch.tensor(order, dtype=torch.int64, device=device)
 
 
-def quantize(weight: torch.Tensor, group: int = GROUP, bits: int = 8):
+def _resolve(fmt, bits):
+    fmt = FORMAT if fmt is None else fmt
+    if fmt not in FORMATS:
+        raise ValueError(f"unknown weight format {fmt!r} (one of {FORMATS})")
+    if fmt == "auto":
+        fmt = "w4a16" if bits == 4 else "w8a16"
+    if fmt != "ref" and bits != (4 if fmt == "w4a16" else 8):
+        raise ValueError(f"format {fmt} stores {4 if fmt == 'w4a16' else 8}-bit codes, not {bits}")
+    return fmt
+
+
+def quantize(weight: torch.Tensor, group: int = GROUP, bits: int = 8, *, fmt=None):
     """``[out, in]`` bfloat16 -> offset bytes ``[out, in]`` plus ``[out, in/group]`` fp16 scales.
 
     Symmetric absmax with the fp16 scale nudged up one fp16 ulp (cuda_fp8.py:1127-1151);
     bits 8 stores -127..127 offset by 128, bits 4 stores -7..7 offset by 8, one per byte.
     Returns ``(bytes, scales, bits)``.
+
+    With a north-star ``fmt`` (or ``FORMAT``) the result is ``(codes, scales, bits, fmt)`` in
+    that format (``qlinear.quantize_w8/w4/fp8``); ``group`` must then be the default or the
+    format's own (128 for w4a16, K for the per-channel formats).
     """
     if bits not in (8, 4):
         raise ValueError("weights are 8 or 4 bits")
     if weight.dim() != 2 or weight.dtype != torch.bfloat16:
         raise ValueError("weight must be a 2-D bfloat16 tensor")
+    fmt = _resolve(fmt, bits)
+    if fmt != "ref":
+        from . import qlinear
+        own = 128 if fmt == "w4a16" else weight.shape[1]
+        if group not in (GROUP, own):
+            raise ValueError(f"format {fmt} uses group {own}, not {group}")
+        q, s = qlinear.FORMATS[fmt][0](weight)
+        return q, s, bits, fmt
     out, inner = weight.shape
     if inner % group:
         raise ValueError(f"{inner} is not a multiple of {group}")
@@ -83,6 +123,9 @@ def quantize(weight: torch.Tensor, group: int = GROUP, bits: int = 8):
 
 def dequantize(packed) -> torch.Tensor:
     """The bfloat16 weight the kernel effectively multiplies by: bf16((byte - offset) * scale)."""
+    if len(packed) > 3 and packed[3] != "ref":
+        from . import qlinear
+        return qlinear.dequantize(packed[:2], packed[3])
     weight, scale = packed[0], packed[1]
     bits = packed[2] if len(packed) > 2 else 8
     rows, k = weight.shape
@@ -103,6 +146,7 @@ class Prepared:
     """
 
     __slots__ = ("weight", "scale", "rows", "k", "groups", "tiled", "bits")
+    fmt = "ref"
 
     def __init__(self, packed: torch.Tensor, scale: torch.Tensor, tiled: bool = None, bits: int = 8):
         rows, k = packed.shape
@@ -140,10 +184,41 @@ class Prepared:
         return self.weight.numel() + self.scale.numel() * 2
 
 
+class FormatPrepared(Prepared):
+    """A north-star weight (``quantize(..., fmt=...)``) relaid into the MI355X tile layout.
+
+    Carries the attributes the engine reads from ``Prepared`` (``weight``, ``scale``,
+    ``rows``, ``k``, ``groups``, ``tiled``, ``bits``, ``bytes_moved()``) plus ``fmt`` and
+    ``tiles``, the ``qlinear.Tiled`` weight the linears consume."""
+
+    __slots__ = ("fmt", "tiles")
+
+    def __init__(self, codes, scale, bits, fmt):  # noqa: super().__init__ relays the reference format
+        from . import qlinear
+        self.tiles = qlinear.prepare((codes, scale), fmt)
+        self.fmt = fmt
+        self.weight, self.scale = self.tiles.weight, self.tiles.scale
+        self.rows, self.k = self.tiles.rows, self.tiles.k
+        self.groups = self.k // 128
+        self.tiled = True
+        self.bits = bits
+
+    def row_major(self):
+        raise ValueError(f"row_major() serves the reference's 8-bit format, not {self.fmt}")
+
+    def bytes_moved(self) -> int:
+        return self.tiles.bytes_moved()
+
+
 def prepare(packed, tiled: bool = None) -> Prepared:
-    """``packed`` is ``(uint8 weight, fp16 scales[, bits])`` from ``quantize``."""
+    """``packed`` is ``(uint8 weight, fp16 scales[, bits])`` from ``quantize``, or a
+    north-star ``(codes, scales, bits, fmt)``."""
     weight, scale = packed[0], packed[1]
     bits = packed[2] if len(packed) > 2 else 8
+    if len(packed) > 3 and packed[3] != "ref":
+        if tiled is False:
+            raise ValueError(f"{packed[3]} weights are consumed in the MI355X tile layout")
+        return FormatPrepared(weight, scale, bits, packed[3])
     return Prepared(weight, scale, tiled, bits)
 
 
@@ -163,7 +238,12 @@ def _plan_config(prepared, batch, config, mode):
     return (base.waves, base.kw, base.rw, splitk)
 
 
+_LIB_FMT = {"w8a16": _lib.FMT_W8A16, "w4a16": _lib.FMT_W4A16, "fp8": _lib.FMT_FP8}
+
+
 def _fmt(prepared):
+    if prepared.fmt != "ref":
+        return _LIB_FMT[prepared.fmt]
     return _lib.FMT_REF8 if prepared.bits == 8 else _lib.FMT_REF4
 
 
@@ -174,6 +254,12 @@ def _run(x, prepared, config, mode):
     if x.dtype != torch.bfloat16:
         raise ValueError("activation must be bfloat16")
     _lib.require_device(x, prepared.weight)
+    if prepared.fmt != "ref":
+        from . import qlinear
+        linear = qlinear.FORMATS[prepared.fmt][1]
+        if mode == _lib.MODE_PLANES:
+            return linear(x, prepared.tiles, config=_plan_config(prepared, batch, config, mode), planes=True)
+        return linear(x, prepared.tiles, swiglu=mode == _lib.MODE_SWIGLU)
     cfg = _plan_config(prepared, batch, config, mode)
     return _linear.run(_fmt(prepared), "qlx_linear_ref", x, prepared.rows, prepared.k,
                        (_lib.ptr(prepared.weight), _lib.ptr(prepared.scale), _lib.ptr(x)),
@@ -214,13 +300,14 @@ def add_norm_scratch(batch: int, rows: int, device):
 
 def matmul_add_norm(x: torch.Tensor, prepared: Prepared, residual: torch.Tensor,
                     norm_weight: torch.Tensor, eps: float, scratch, warps: int = 8):
-    """``residual + x @ W.T`` in bfloat16 and its RMSNorm: returns ``(new_residual, normed)``.
+    """``residual + x @ W.T`` in bfloat16 and its RMSNorm, in one launch: returns
+    ``(new_residual, normed)``.
 
-    Delta = bf16(x @ W.T) lands in ``scratch``'s buffer, then r = bf16(residual + delta) and
-    y = bf16(bf16(r * rsqrt(mean r^2 + eps)) * w), the rounding of
-    engine/kernels/cuda_fp8.py:1339-1374. Two launches here (GEMM, then the add-norm), not
-    one: the reference's single-launch form serialises a whole-row tail and is off by
-    default there (engine/engine.py:115-119).
+    Delta = bf16(x @ W.T) lands in ``scratch``'s buffer; the workgroup that completes the
+    last row block (``scratch``'s counter) then forms r = bf16(residual + delta) and
+    y = bf16(bf16(r * rsqrt(mean r^2 + eps)) * w) for every row, the rounding of
+    engine/kernels/cuda_fp8.py:1339-1374 (``qlx_linear_add_norm``). ``warps`` is the
+    reference's block shape and has no MI355X counterpart (the library plans the launch).
     """
     batch, k = x.shape
     n = prepared.rows
@@ -230,15 +317,16 @@ def matmul_add_norm(x: torch.Tensor, prepared: Prepared, residual: torch.Tensor,
         raise ValueError("residual must be bfloat16 [batch, rows]")
     if batch > 16:
         raise ValueError("the fused add-norm serves up to sixteen rows")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("activation must be bfloat16")
     delta, counter = scratch
-    if tuple(delta.shape) != (batch, n):
+    if tuple(delta.shape) != (batch, n) or delta.dtype != torch.bfloat16:
         raise ValueError("scratch does not match this batch")
-    delta.copy_(matmul(x, prepared, (warps, 1)))
-    out_res = torch.empty_like(residual)
-    out_norm = torch.empty_like(residual)
-    _lib.call("qlx_add_rms_norm", _lib.ptr(residual), _lib.ptr(delta), None, 0, _lib.ptr(norm_weight),
-              _lib.ptr(out_res), _lib.ptr(out_norm), batch, n, float(eps), _lib.stream(x.device))
-    return out_res, out_norm
+    if counter.dtype != torch.int32 or counter.numel() < 1:
+        raise ValueError("scratch's counter is one int32")
+    _lib.require_device(x, residual, norm_weight, delta, counter, prepared.weight)
+    return _linear.run_add_norm(_fmt(prepared), (prepared.weight, prepared.scale), x, n, k, prepared.tiled,
+                                residual, norm_weight, eps, delta, counter)
 
 
 def applicable(config, batch: int, swiglu: bool = False) -> bool:

@@ -107,7 +107,13 @@ class DecodeStack:
         return self
 
     def run(self, budget_us=BUDGET_US):
-        """Run the whole chain once on the current stream."""
+        """Run the whole chain once on the current stream.
+
+        Not capturable into a graph: each run tags what it publishes with a new epoch passed
+        as a kernel argument, and every replay of a captured run would carry the same one, so
+        waiting workgroups would take the previous replay's values for this one's."""
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("DecodeStack.run cannot be captured into a graph: every run needs a new epoch")
         if self.desc is None:
             self.build()
         self.epoch = self.epoch % 0xFFFF + 1  # its low 16 bits tag published values: 1..65535

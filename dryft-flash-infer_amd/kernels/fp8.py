@@ -41,15 +41,6 @@ def quantize(weight: torch.Tensor, group: int = GROUP):
     return q.view(torch.float8_e4m3fn), s
 
 
-def _plan(rows_out: int):
-    """The reference's default (BLOCK_N, warps, stages, splits) for a shape (fp8.py:153-159)."""
-    block_n = 64 if rows_out >= 8448 else 32
-    splits = 1
-    while splits < 8 and -(-rows_out // block_n) * splits < 264:
-        splits *= 2
-    return block_n, 8 if block_n >= 64 else 4, 4, splits
-
-
 def fp8_matmul(x: torch.Tensor, packed, config=None) -> torch.Tensor:
     """``x @ weight.T`` where ``packed`` is ``(e4m3 weight, group scales)``."""
     weight, scale = packed

@@ -149,6 +149,17 @@ def dequantize_w4(packed):
     return out
 
 
+def dequantize_fp8(packed):
+    """bf16(e4m3 code * bf16 scale) per output channel."""
+    q, s = packed
+    return (q.float() * s.float()[:, None]).to(torch.bfloat16)
+
+
+def dequantize(packed, fmt):
+    """The bf16 weight a north-star ``(codes, scales)`` pair stands for."""
+    return {"w8a16": dequantize_w8, "w4a16": dequantize_w4, "fp8": dequantize_fp8}[fmt](packed)
+
+
 # ---- linears ---------------------------------------------------------------------------
 
 def _check_x(x, k):

@@ -3,9 +3,11 @@
  *
  * Plain pointers and sizes only. Every pointer argument is device memory (HBM) unless
  * it says otherwise; `stream` is a hipStream_t (NULL = the default stream). No entry
- * point allocates, synchronises or reads device memory on the host, so every call is
- * safe to capture into a hipGraph. Each returns QLX_OK (0) or a negative status;
- * qlx_last_error() then holds a message (thread-local).
+ * point allocates, synchronises or reads device memory on the host, so every call except
+ * qlx_stack_run is safe to capture into a hipGraph (a run's `epoch` argument must differ
+ * from the previous run's, and every replay of a captured run would repeat it). Each
+ * returns QLX_OK (0) or a negative status; qlx_last_error() then holds a message
+ * (thread-local).
  *
  * Number formats travel as raw bits: bf16 and fp16 as uint16, OCP e4m3fn as one byte.
  *
@@ -188,6 +190,19 @@ int qlx_linear_fp8wo(const void* w, const void* w_scale, const void* x, void* y,
 int qlx_linear_int8(const void* w, const void* w_scale, const void* xq, const float* x_scale,
                     const void* xq2, const float* x_scale2, void* y, int m, int n, int k,
                     const qlx_plan* plan, void* stream);
+
+/* y = x . W^T into `delta` (bf16 [m][n]), then in the same launch res_out = bf16(residual +
+ * delta) and normed = bf16(bf16(res_out * rsqrt(mean res_out^2 + eps)) * norm_w) over rows of
+ * n: the workgroup that completes the last row block finishes every row. fmt is
+ * QLX_FMT_W8A16, QLX_FMT_W4A16 or QLX_FMT_FP8 (weights as their linears take them, `tiled`
+ * as there) or QLX_FMT_REF8 / QLX_FMT_REF4 (the cuda_fp8 layouts; `tiled` as in
+ * qlx_linear_ref). plan->mode must be QLX_MODE_BF16; splits > 1 use plan->workspace and
+ * plan->tickets as the linears do. `counter` is one int32, zero before the first call and
+ * left zero by every call: calls sharing it must not overlap. n % 8 == 0.
+ * Replaces cuda_fp8.matmul_add_norm (engine/kernels/cuda_fp8.py:1333-1374, kernel 695-963). */
+int qlx_linear_add_norm(int fmt, const void* w, const void* w_scale, const void* x, int m, int n, int k,
+                        int tiled, const void* residual, const void* norm_w, float eps, void* delta,
+                        int* counter, void* res_out, void* normed, const qlx_plan* plan, void* stream);
 
 /* ---- split-K plane consumers and epilogues ----------------------------------------- */
 

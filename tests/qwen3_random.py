@@ -186,29 +186,28 @@ class RandomQwen3:
 
     def generate(self, prompt, steps):
         """Greedy decode: prefill with the reference linears (out of scope), then `steps`
-        decode steps through the library. Returns [B, steps] token ids."""
+        decode steps through the library. Returns ([B, steps] token ids, [B, steps, VOCAB]
+        fp32 logits each emitted token was chosen from): token t is the argmax of logits t,
+        which the prefill (t = 0) or decode step t - 1 produced."""
         cache = {"len": 0, "k": {}, "v": {}}
-        logits = self.forward(prompt, cache, reference=True)[:, -1, :]
-        out = []
-        tok = logits.float().argmax(dim=-1)
-        for _ in range(steps):
+        logits = self.forward(prompt, cache, reference=True)[:, -1, :].float()
+        out, seen = [], []
+        for t in range(steps):
+            tok = logits.argmax(dim=-1)
             out.append(tok)
-            logits = self.forward(tok[:, None], cache, reference=False)[:, -1, :]
-            tok = logits.float().argmax(dim=-1)
-        return torch.stack(out, dim=1)
+            seen.append(logits)
+            if t + 1 < steps:
+                logits = self.forward(tok[:, None], cache, reference=False)[:, -1, :].float()
+        return torch.stack(out, dim=1), torch.stack(seen, dim=1)
 
-    def replay(self, prompt, tokens, dtype=torch.float32):
+    def replay_logits(self, prompt, tokens, dtype=torch.float32):
         """Teacher-forced reference logits at every emitted step (bench/harness.py:136-152):
-        returns (gap [B, steps] = best - chosen logit, exact [B, steps] bool, best logit [B, steps],
-        argmax [B, steps]). `dtype` is the reference matmuls' precision."""
+        [B, steps, VOCAB] fp32, entry t conditioned on the prompt and tokens[:, :t]. `dtype` is
+        the reference matmuls' precision."""
         full = torch.cat([prompt, tokens], dim=1)
         cache = {"len": 0, "k": {}, "v": {}}
         self.ref_dtype = dtype
         try:
-            logits = self.forward(full, cache, reference=True)[:, prompt.shape[1] - 1:-1, :].float()
+            return self.forward(full, cache, reference=True)[:, prompt.shape[1] - 1:-1, :].float()
         finally:
             self.ref_dtype = torch.float32
-        best = logits.max(dim=-1).values
-        chose = logits.gather(2, tokens[:, :, None])[:, :, 0]
-        top = logits.argmax(dim=-1)
-        return best - chose, top == tokens, best, top

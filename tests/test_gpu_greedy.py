@@ -5,10 +5,18 @@ reference harness's teacher-forced replay (bench/harness.py:136-152, TIE_MARGIN 
 Every decode-step projection (qkv, o, gate_up with the fused SwiGLU, down, lm_head) runs
 through the gfx950 library; attention, norms and RoPE are shared torch code (qwen3_random).
 
-Measured on MI355X (seed 5; batch 1 / batch 32): argmax-exact W4A16 0.906 / 0.888 (the
-reference against itself at fp64: 0.922 / 0.902), W8A16 0.922 / 0.888 (0.891 / 0.918),
-FP8 W8A8 0.563 / 0.510 (0.547 / 0.517); largest gap 0.19 logits at 16-bit weights, 1.19 at
-FP8, against the reference's margin of 2.
+The check, per emitted step t of every sequence:
+
+* the library's logits (those token t was chosen from) against the reference's logits on
+  the same context (teacher-forced replay): max |delta| and relative L2 are measured. The
+  library rounds to bf16 exactly where the reference does, so what separates them is fp32
+  summation order inside each projection, amplified through 36 layers -- the same kind of
+  difference as between the reference's own fp32 and fp64 matmuls. The relative L2 must stay
+  within twice that self-spread (the largest over the run's steps);
+* **identity where the reference decides**: wherever the reference's top-1 / top-2 margin
+  exceeds twice that step's max |delta|, the emitted token must be the reference's argmax
+  (every step is counted; the ones below the bound are printed);
+* the harness's own gate: best - chosen reference logit <= TIE_MARGIN on every step.
 """
 
 import pytest
@@ -20,6 +28,9 @@ pytestmark = pytest.mark.gpu
 
 PROMPT, STEPS = 512, 64
 TIE_MARGIN = 2.0  # the reference harness's gate on best - chosen logit (bench/harness.py:21)
+#: The library's logits may differ from the fp32 reference's by this multiple of the
+#: reference's own fp32-vs-fp64 spread (relative L2 per step, largest over the run).
+SELF_SPREAD_FACTOR = 2.0
 
 
 @pytest.fixture(autouse=True)
@@ -37,29 +48,30 @@ def test_greedy_tokens_match_reference(fmt):
         g = torch.Generator(device="cuda").manual_seed(1000 + batch)
         prompt = torch.randint(0, VOCAB, (batch, PROMPT), generator=g, device="cuda")
         with torch.inference_mode():
-            tokens = model.generate(prompt, STEPS)
-            gap, exact, best, top = model.replay(prompt, tokens)
-            # the same reference with fp64 matmuls: how often two roundings of the reference agree
-            _, _, _, top64 = model.replay(prompt, tokens, dtype=torch.float64)
-        self_agree = (top64 == top).float().mean().item()
-        n = exact.numel()
-        frac = exact.float().mean().item()
-        worst = gap.max().item()
-        # the gaps of the steps whose token is not the reference's argmax, in units of one
-        # bf16 step of that step's best logit (the logits are bf16 on both sides)
-        ulp = torch.ldexp(torch.ones_like(best), torch.frexp(best.abs())[1] - 8)
-        miss = (gap[~exact] / ulp[~exact]).tolist()
-        print(f"greedy {fmt} batch {batch}: {int(exact.sum())}/{n} argmax exact ({frac:.4f}; reference fp32 vs fp64 "
-              f"{self_agree:.4f}), max gap {worst:.4f}, "
-              f"misses in bf16 steps {sorted(miss)[-8:]}, best logit range "
-              f"{best.min().item():.2f}..{best.max().item():.2f}", flush=True)
-        assert worst <= TIE_MARGIN, (fmt, batch, worst)
-        # Exact agreement cannot be asked of any path that does not round exactly as the
-        # reference: two roundings of the reference itself (fp32 vs fp64 matmuls) disagree on
-        # 8-10 % of these random-init steps at 16-bit weights and on ~45 % at FP8 W8A8, whose
-        # 3-bit-mantissa activation codes turn one-ulp differences into code flips. The library
-        # must agree with the reference as well as the reference agrees with itself, within the
-        # sampling noise of the proportion (2 sigma: ~0.12 at 64 steps, ~0.03 at 2048).
-        noise = 2.0 * (2 * 0.25 / n) ** 0.5
-        assert frac >= self_agree - noise, (fmt, batch, frac, self_agree)
+            tokens, lib = model.generate(prompt, STEPS)
+            ref = model.replay_logits(prompt, tokens)
+            ref64 = model.replay_logits(prompt, tokens, dtype=torch.float64)
+        delta = (lib - ref).abs().amax(dim=-1)                       # [B, steps]
+        rel = (lib - ref).norm(dim=-1) / ref.norm(dim=-1)
+        self_delta = (ref64 - ref).abs().amax(dim=-1)                # the reference's own spread
+        self_rel = (ref64 - ref).norm(dim=-1) / ref.norm(dim=-1)
+        bound = SELF_SPREAD_FACTOR * self_rel.max().item()
+        top2 = ref.topk(2, dim=-1).values
+        margin = top2[..., 0] - top2[..., 1]
+        top = ref.argmax(dim=-1)
+        gap = top2[..., 0] - ref.gather(2, tokens[:, :, None])[:, :, 0]
+        decided = margin > 2.0 * delta
+        agree = tokens == top
+        n = tokens.numel()
+        print(f"greedy {fmt} batch {batch}: max|dlogit| {delta.max().item():.4f} (median "
+              f"{delta.median().item():.4f}; reference fp32 vs fp64 {self_delta.max().item():.4f}), rel-L2 max "
+              f"{rel.max().item():.2e} (reference fp32 vs fp64 {self_rel.max().item():.2e}, bound {bound:.2e}); "
+              f"{int(decided.sum())}/{n} steps decided by the reference "
+              f"(margin > 2 max|dlogit|), all identical: {bool(agree[decided].all())}; "
+              f"{n - int(decided.sum())} steps below the bound, of which {int((~agree & ~decided).sum())} "
+              f"differ (max gap {gap.max().item():.4f}); argmax-exact overall {int(agree.sum())}/{n}", flush=True)
+        assert rel.max().item() <= bound, (fmt, batch, rel.max().item(), bound)
+        assert bool(agree[decided].all()), (fmt, batch, "token differs where the reference decides")
+        assert gap.max().item() <= TIE_MARGIN, (fmt, batch, gap.max().item())
+        del lib, ref, ref64
     del model

@@ -223,6 +223,10 @@ def test_cuda_int8_quantize_matmul_add_norm_quant():
             got_res, actual = cuda_int8.add_norm_quant(x, delta, weight, 1.e-6)
             assert torch.equal(got_res, want_res), (m, splits)
             assert torch.equal(actual[0], expected[0]) and torch.equal(actual[1], expected[1]), (m, splits)
+            o_res, o_q, o_s = O.add_norm_quant(bits16(x), delta.cpu().numpy(), bits16(weight), 1.e-6)
+            assert np.array_equal(bits16(got_res), o_res), (m, splits, "residual vs oracle")
+            assert np.array_equal(actual[0].cpu().numpy(), o_q), (m, splits, "int8 codes vs oracle")
+            assert np.array_equal(actual[1].cpu().numpy(), o_s), (m, splits, "scales vs oracle")
 
 
 def test_plane_consumers_bit_exact():

@@ -273,3 +273,40 @@ def test_int8_activation_quantize_closed_form():
             assert s[r, grp] == sc
             for p in range(64):
                 assert q[r, grp * 64 + p] == np.int8(np.rint(xf[r, grp, nat[p]] / sc))
+
+
+def test_int8_w8a8_product_pinned_by_golden_weights_and_fp64(gold):
+    """oracle.linear_w8a8_int8 (the INT8 W8A8 GEMM's checker) against an fp64 torch product in
+    natural column order: activation s_x * rint(x / s_x) per 64-group (torch ops), weight
+    (byte - 128) * fp16 scale from the golden quantize vectors, while the oracle is fed the
+    golden fragment-ordered cuda_int8.Prepared bytes. Plus a closed form and a planted
+    fragment-order mistake."""
+    g = torch.Generator().manual_seed(23)
+    for name, rows in (("a", 32), ("b", 64)):
+        k = 256
+        x = torch.randn(3, k, generator=g).to(torch.bfloat16)
+        q8 = gold[f"{name}_q8_g64"] if f"{name}_q8_g64" in gold else None
+        if q8 is None:  # b has prepared bytes only: requantize its weight with the pinned oracle
+            q8, s8, _ = O.quantize(gold[f"{name}_w"])
+        else:
+            s8 = gold[f"{name}_s8_g64"]
+        prepared = gold[f"{name}_int8_prepared"].view(np.int8)
+        assert np.array_equal(prepared, O.int8_prepare(O.prepare_weight(q8, tiled=False)))
+        xf = x.float().double().reshape(3, k // 64, 64)
+        sx = torch.clamp(xf.abs().amax(dim=2, keepdim=True).float() / 127.0, min=1e-20).double()
+        xhat = (torch.round(xf / sx) * sx).reshape(3, k)  # torch.round is half-even, as rint
+        what = (torch.from_numpy(q8.astype(np.float64)) - 128.0) * torch.from_numpy(
+            O.f16_to_f32(s8).astype(np.float64)).repeat_interleave(64, dim=1)
+        want = (xhat @ what.T).numpy()
+        got = O.linear_w8a8_int8(bits16(x), prepared, s8)
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12), name
+        # planted mistake: the activation codes left in natural order (no fragment permutation)
+        wrong = prepared.reshape(rows, k // 64, 64)[:, :, np.argsort(O.int8_natural())].reshape(rows, k)
+        assert not np.allclose(O.linear_w8a8_int8(bits16(x), wrong, s8), want, rtol=1e-6), name
+    # closed form: every activation 127/128 -> s_x = 2^-7 exactly, codes 127, so the product is
+    # 127/128 times the row sums of the dequantized weight
+    q8, s8 = gold["a_q8_g64"], gold["a_s8_g64"]
+    prepared = gold["a_int8_prepared"].view(np.int8)
+    x = np.full((1, 256), O.f32_to_bf16(np.array([127.0 / 128.0], np.float32))[0], np.uint16)
+    rowsum = ((q8.astype(np.float64) - 128.0) * np.repeat(O.f16_to_f32(s8).astype(np.float64), 64, axis=1)).sum(1)
+    assert np.allclose(O.linear_w8a8_int8(x, prepared, s8)[0], 127.0 / 128.0 * rowsum, rtol=1e-12, atol=1e-15)
