@@ -72,6 +72,7 @@ SIGNATURES = {
     "qlx_linear_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_plan_skinny": ([_I, _I, _I, _I, _I, _PLAN], _I),
     "qlx_linear_skinny": ([_I, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
+    "qlx_linear_skinny_noalloc": ([_I, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
     "qlx_linear_fp8_w8a8_q": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),

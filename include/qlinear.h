@@ -162,6 +162,17 @@ int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan);
 int qlx_linear_skinny(int fmt, const void* w, const void* w_scale, const void* x, void* y, int m, int n, int k,
                       const qlx_plan* plan, void* stream);
 
+/* qlx_linear_skinny for callers that cannot allocate (code under graph capture, serving
+ * loops, harnesses that forbid hipMalloc): no counterpart in the reference. It plans the call
+ * itself (qlx_plan_skinny) and keeps the K-slice planes and ticket counters in the library's
+ * own static device array (8 MiB of planes + 16384 counters per GPU, held until the process
+ * ends) instead of caller memory; it calls no hipMalloc/hipFree. Rejects (QLX_EINVAL) shapes
+ * whose planes (splits * m * n * 4 bytes) exceed 8 MiB or with n > 262144. Every call on one
+ * GPU shares that array: calls that overlap on one GPU (other streams, other threads) race.
+ * Same output as qlx_linear_skinny with the same plan, bit for bit. */
+int qlx_linear_skinny_noalloc(int fmt, const void* w, const void* w_scale, const void* x, void* y, int m, int n,
+                              int k, int mode, void* stream);
+
 /* FP8 e4m3 W8A8: per-channel bf16 weight scales, activation quantized per token inside the
  * kernel (same arithmetic as qlx_quantize_fp8_act). Replaces cuda_int8.matmul's role
  * (engine/kernels/cuda_int8.py:251-281) for the north-star FP8 format. */
