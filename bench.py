@@ -35,7 +35,10 @@ LAYERS = 36
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
-EXECUTOR_SHAPES = ((8, 0), (4, 4))  # (compute waves, poller waves)
+#: Executors timed per stack: the stream executor, and the first one with 8 compute waves.
+EXECUTOR_SHAPES = (("stream", 0), (8, 0))
+#: Largest batch the stream executor takes per format (its staged activation must fit LDS).
+STREAM_MAX_M = {"fp8": 2, "w8a16": 1, "w4a16": 1}
 
 
 def log(*a):
@@ -100,10 +103,12 @@ class Stack:
             else:  # down, lm_head
                 q = h = self.linear(h if name == "lm_head" else q, packed)
 
-    def executor(self, waves=8, lanes=1, pollers=0):
-        """The same chain as one decode-step executor launch (outputs preallocated)."""
-        from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, pollers=pollers)
+    def executor(self, waves=8, lanes=1, pollers=0, stream=False):
+        """The same chain as one decode-step executor launch (outputs preallocated): the first
+        executor, or with ``stream`` the stream executor."""
+        from kernels.decode_stack import DecodeStack, StreamStack
+        chain = StreamStack(self.fmt, self.m) if stream else DecodeStack(self.fmt, self.m, waves=waves,
+                                                                           groups_per_cu=lanes, pollers=pollers)
         self.outs = []
         h = self.x[2560]
         q = None
@@ -282,15 +287,24 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
         # The executor in each workgroup shape: 8 compute waves, or 4 with 0, 2 or 4 poller waves
         # (waves that only read and stage the published activations).
         for waves, pollers in EXECUTOR_SHAPES:
-            chain = stack.executor(waves=waves, pollers=pollers)
+            stream = waves == "stream"
+            if stream and m > STREAM_MAX_M.get(fmt, 0):
+                continue
+            chain = stack.executor(waves=waves, pollers=pollers, stream=stream)
             ms_exec = time_fn(chain.run, steps, warmup)
             if chain.failed():
-                raise RuntimeError(f"decode executor ({waves}c{pollers}p): a wait gave up")
-            out.setdefault("shapes_us", {})[f"{waves}c{pollers}p"] = round(ms_exec * 1e3, 2)
+                raise RuntimeError(f"decode executor ({waves}, {pollers}): a wait gave up")
+            key = "stream" if stream else f"{waves}c{pollers}p"
+            out.setdefault("shapes_us", {})[key] = round(ms_exec * 1e3, 2)
             if ms_exec * 1e3 < out.get("executor_us", 1e30):
                 out["executor_us"] = ms_exec * 1e3
-                out["executor_launch"] = {"grid": chain.grid, "lds": chain.lds, "waves": waves, "pollers": pollers,
-                                          "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
+                if stream:
+                    out["executor_launch"] = {"kind": "stream", "grid": chain.grid, "lds": chain.lds,
+                                              "ring_lines": chain.launch.ring_lines}
+                else:
+                    out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": waves,
+                                              "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
+                                              "pieces": chain.launch.pieces != 0}
             del chain
     cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
@@ -392,12 +406,15 @@ def main():
     if head["path"] == "executor":
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
         el = head["executor_launch"]
-        kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
-                 f"{str(el['pieces']).lower()}>")
+        if el["kind"] == "stream":
+            kname = f"stream_kernel<{fmt_name}>"
+        else:
+            kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
+                     f"{str(el['pieces']).lower()}>")
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
-            "traffic": profiled_traffic(args.workload, args.m, "stack"),
+            "traffic": profiled_traffic(args.workload, args.m, el["kind"]),
             "kernel": f"{kname} (the whole chain, M={args.m})",
             "us_per_launch": round(head["us"], 2), "alg_MB_per_launch": round(head["alg_GB"] * 1e3, 3),
         }

@@ -605,10 +605,11 @@ struct BlockTeam {
   __device__ void sync() const { __syncthreads(); }
 };
 
-template <class F, class XS, class Team = BlockTeam>
+// UNROLL (0: stage_unroll's choice) sets the chunks each thread keeps in flight.
+template <class F, class XS, class Team = BlockTeam, int UNROLL = 0>
 __device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {}) {
   const int tid = team.tid(), nthr = team.size();
-  constexpr int U_ = stage_unroll<XS, false>();
+  constexpr int U_ = UNROLL ? UNROLL : stage_unroll<XS, false>();
   constexpr int CPS = F::KSTEP / 8;  // 16-byte chunks per step
   const int cpr = nst * CPS;
   const int total = a.m * cpr;
@@ -684,11 +685,11 @@ __device__ __forceinline__ uint32_t* fp8_amax(const GemmArgs& a, char* lds) {
 // one batch of loads covers the rows, the values stay in registers for the codes (one pass
 // over x); otherwise the slice is read again. With `zeroed_amax`, the per-token maxima live
 // there, already cleared and visible to the team.
-template <class XS, class Team = BlockTeam>
+template <class XS, class Team = BlockTeam, int UNROLL = 0>
 __device__ __forceinline__ void stage_fp8_act(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst, const Team& team = {},
                               uint32_t* zeroed_amax = nullptr) {
   const int tid = team.tid(), nthr = team.size();
-  constexpr int U_ = stage_unroll<XS, true>();
+  constexpr int U_ = UNROLL ? UNROLL : stage_unroll<XS, true>();
   float* sx = reinterpret_cast<float*>(lds + a.off_sx);
   uint32_t* amax = zeroed_amax ? zeroed_amax : fp8_amax(a, lds);
   if (!zeroed_amax) {

@@ -48,6 +48,14 @@ class StackLaunch(ctypes.Structure):
                                             "pieces")]
 
 
+class StreamLaunch(ctypes.Structure):
+    """``qlx_stream_launch``: grid, LDS bytes, ring lines per compute wave, and the kernel's
+    LDS layout (opaque words)."""
+
+    _fields_ = [("grid", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("ring_lines", ctypes.c_int),
+                ("layout_words", ctypes.c_int), ("layout", ctypes.c_int * 32)]
+
+
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
 _PLAN = ctypes.POINTER(Plan)
 _PI, _PLL = ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_longlong)
@@ -88,6 +96,9 @@ SIGNATURES = {
     "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
                          ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
+    "qlx_stream_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _P, _PLL, _P, _PLL, ctypes.POINTER(StreamLaunch)],
+                         _I),
+    "qlx_stream_run": ([_I, _P, ctypes.POINTER(StreamLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 
