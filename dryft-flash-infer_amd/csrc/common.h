@@ -75,6 +75,62 @@ __device__ __forceinline__ float clamp_keep_nan(float v, float lim) {
   return v < -lim ? -lim : (v > lim ? lim : v);
 }
 
+// The FP8 quantizers' code for x / sc, the reference's way: IEEE division, clamp to +-448,
+// RNE cast (engine/kernels/fp8.py:20-28).
+__device__ __forceinline__ uint32_t e4m3_of_quotient(float x, float sc) {
+  return f32_to_e4m3(clamp_keep_nan(x / sc, 448.f));
+}
+
+// x / sc as IEEE division rounds it, from y = 1 / sc (IEEE-rounded): the product x * y is
+// within an ulp of the quotient, and one correction with its exact residual (fma) lands on the
+// correctly rounded quotient (Markstein's theorem for a correctly rounded reciprocal). The sign
+// is taken from x so that -0 stays -0 (the residual of -0 is +0).
+__device__ __forceinline__ float quotient_by_reciprocal(float x, float sc, float y) {
+  const float q0 = x * y;
+  const float r = __builtin_fmaf(-q0, sc, x);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+}
+
+// e4m3 codes of 8 bf16 values (pairs in v) over the scale sc, y = 1 / sc, natural byte order:
+// the same codes as e4m3_of_quotient, at about a seventh of its instructions. The quotient comes
+// from quotient_by_reciprocal and the cast from the hardware's RNE conversion (v_cvt_pk_fp8_f32,
+// OCP e4m3 on gfx950). Both hold for every input the quantizers can see, a bf16 value no larger
+// in magnitude than the bf16 maximum its scale was taken from: qlx_fp8_selfcheck compares the two
+// paths on all of them. The clamp is not needed there: |x / sc| <= 448 (1 + 2^-23) rounds to 448.
+// A chunk holding a NaN, or a non-finite scale, takes e4m3_of_quotient (the hardware gives 0xFF
+// for every NaN; torch keeps the sign).
+__device__ __forceinline__ uint2 e4m3_chunk(uint4 v, float sc, float y) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  // bit 15 / 31 of (h & 0x7fff) + 0x7f per half: set when that bf16 half is a NaN (> 0x7f80)
+  const uint32_t nan = (((d[0] & 0x7fff7fffu) + 0x007f007fu) | ((d[1] & 0x7fff7fffu) + 0x007f007fu) |
+                        ((d[2] & 0x7fff7fffu) + 0x007f007fu) | ((d[3] & 0x7fff7fffu) + 0x007f007fu)) &
+                       0x80008000u;
+  uint32_t o[2];
+  if (nan != 0u || !(sc <= 3.40282347e38f)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t c = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t bits = (e & 1) ? d[2 * h + (e >> 1)] >> 16 : d[2 * h + (e >> 1)] & 0xffffu;
+        c |= e4m3_of_quotient(bf2f(bits), sc) << (8 * e);
+      }
+      o[h] = c;
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float q0 = quotient_by_reciprocal(bf2f(d[2 * h] & 0xffffu), sc, y);
+      const float q1 = quotient_by_reciprocal(bf2f(d[2 * h] >> 16), sc, y);
+      const float q2 = quotient_by_reciprocal(bf2f(d[2 * h + 1] & 0xffffu), sc, y);
+      const float q3 = quotient_by_reciprocal(bf2f(d[2 * h + 1] >> 16), sc, y);
+      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false);
+      o[h] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q2, q3, lo, true);
+    }
+  }
+  return uint2{o[0], o[1]};
+}
+
 // ---- wave reductions (64 lanes) ----------------------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {

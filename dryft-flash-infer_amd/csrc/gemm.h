@@ -663,17 +663,7 @@ __device__ void stage_bias(const GemmArgs& a, char* lds, int nst) {
 
 // e4m3 codes of 8 activation values (bf16 pairs in v) at per-token scale sc, to LDS.
 __device__ __forceinline__ void store_e4m3_chunk(char* dst, uint4 v, float sc) {
-  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-  uint32_t c[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
-    c[e] = f32_to_e4m3(clamp_keep_nan(xv / sc, 448.f));
-  }
-  uint2 o;
-  o.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-  o.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-  *reinterpret_cast<uint2*>(dst) = o;
+  *reinterpret_cast<uint2*>(dst) = e4m3_chunk(v, sc, 1.f / sc);
 }
 
 // The per-token bf16 maxima (as uint bits) of the FP8 prologue, after the token scales.

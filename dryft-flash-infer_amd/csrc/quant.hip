@@ -215,22 +215,10 @@ quantize_fp8_weight_kernel(const uint16_t* __restrict__ w, uint8_t* __restrict__
     }
   }
   amax = wave_max(amax);
-  const float s = fmaxf(amax / 448.f, 1e-12f);
+  const float s = fmaxf(amax / 448.f, 1e-12f), y = 1.f / s;
   if (lane == 0) scale[(size_t)row * groups + g] = f2bf(s);
-  for (int o = lane; o < octets; o += 64) {
-    const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * o);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-    uint32_t c[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
-      c[e] = f32_to_e4m3(clamp_keep_nan(x / s, 448.f));
-    }
-    uint2 out;
-    out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    *reinterpret_cast<uint2*>(dst + 8 * o) = out;
-  }
+  for (int o = lane; o < octets; o += 64)
+    *reinterpret_cast<uint2*>(dst + 8 * o) = e4m3_chunk(*reinterpret_cast<const uint4*>(src + 8 * o), s, y);
 }
 
 // Per-token activation quantize: one block of 256 threads per row.
@@ -255,22 +243,51 @@ quantize_fp8_act_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ co
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-  const float s = fmaxf(amax / 448.f, 1e-12f);
+  const float s = fmaxf(amax / 448.f, 1e-12f), y = 1.f / s;
   if (threadIdx.x == 0) scale[row] = s;
-  for (int o = threadIdx.x; o < octets; o += 256) {
-    const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * o);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-    uint32_t c[8];
+  for (int o = threadIdx.x; o < octets; o += 256)
+    *reinterpret_cast<uint2*>(code + (size_t)row * k + 8 * o) =
+        e4m3_chunk(*reinterpret_cast<const uint4*>(src + 8 * o), s, y);
+}
+
+// Every input the FP8 quantizers can see, through e4m3_chunk and through e4m3_of_quotient: a
+// finite or infinite bf16 maximum `amax` (block y), its scale max(amax / 448, 1e-12), and each
+// bf16 x with |x| <= amax, plus every NaN x. counts[0] = codes that differ, counts[2 + i] the
+// first 64 of them as (amax bits << 48 | x bits << 32 | fast code << 8 | reference code).
+__global__ void __launch_bounds__(256) fp8_selfcheck_kernel(unsigned long long* counts) {
+  const uint32_t ab = blockIdx.y;  // 0 .. 0x7f80 (+inf)
+  const float amax = bf2f(ab);
+  const float s = fmaxf(amax / 448.f, 1e-12f), y = 1.f / s;
+  unsigned long long bad = 0;
+  // 8 consecutive x bit patterns per thread: one chunk
+  for (uint32_t x0 = (blockIdx.x * 256 + threadIdx.x) * 8; x0 < 0x10000u; x0 += gridDim.x * 256 * 8) {
+    uint32_t pk[4];
+    bool live[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float xv = bf2f(e & 1 ? d[e >> 1] >> 16 : d[e >> 1] & 0xffffu);
-      c[e] = f32_to_e4m3(clamp_keep_nan(xv / s, 448.f));
+      const uint32_t xb = x0 + e, mag = xb & 0x7fffu;
+      live[e] = mag <= ab || mag > 0x7f80u;
     }
-    uint2 out;
-    out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    *reinterpret_cast<uint2*>(code + (size_t)row * k + 8 * o) = out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // values outside the domain are replaced by 0 so that the chunk stays a possible input
+      const uint32_t lo = live[2 * i] ? x0 + 2 * i : 0u, hi = live[2 * i + 1] ? x0 + 2 * i + 1 : 0u;
+      pk[i] = lo | (hi << 16);
+    }
+    const uint2 f = e4m3_chunk(uint4{pk[0], pk[1], pk[2], pk[3]}, s, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t bits = e & 1 ? pk[e >> 1] >> 16 : pk[e >> 1] & 0xffffu;
+      const uint32_t r = e4m3_of_quotient(bf2f(bits), s);
+      const uint32_t fc = ((e < 4 ? f.x : f.y) >> (8 * (e & 3))) & 0xffu;
+      if (fc != r) {
+        ++bad;
+        const unsigned long long i = atomicAdd(&counts[1], 1ull);
+        if (i < 64) counts[2 + i] = ((unsigned long long)ab << 48) | ((unsigned long long)bits << 32) | (fc << 8) | r;
+      }
+    }
   }
+  if (bad) atomicAdd(&counts[0], bad);
 }
 
 // ---- INT8 W8A8 (cuda_int8.py) ---------------------------------------------------------------
@@ -388,6 +405,12 @@ int qlx_quantize_fp8_act(const void* x, void* code, float* scale, int m, int k, 
   quantize_fp8_act_kernel<<<m, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint8_t*)code,
                                                               scale, k);
   QLX_LAUNCH_CHECK("quantize_fp8_act");
+}
+
+int qlx_fp8_selfcheck(unsigned long long* counts, void* stream) {
+  QLX_REQUIRE(counts != nullptr, "counts is null");
+  fp8_selfcheck_kernel<<<dim3(32, 0x7f81), 256, 0, (hipStream_t)stream>>>(counts);
+  QLX_LAUNCH_CHECK("fp8_selfcheck");
 }
 
 int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void* stream) {

@@ -18,9 +18,11 @@
 //     -- across projections, while inputs are still being produced. (Measured on MI355X: four
 //     such waves per CU stream 6.9 TB/s; one wave draws at most ~9 GB/s, so fewer waves cannot.)
 //   * kSxIo IO waves poll the published activation of the next projection this workgroup has
-//     work in, stage it into LDS (bf16, or the per-token FP8 codes), signal the compute waves
-//     through an LDS word, then reduce each tile's partial sums from the compute waves, apply
-//     the epilogue and publish the outputs.
+//     work in, copy it into LDS as bf16 (FP8: with the per-token maxima), signal the compute
+//     waves through an LDS word each, then reduce each tile's partial sums from the compute
+//     waves, apply the epilogue and publish the outputs. The per-step work on the staged
+//     activation (FP8 codes, W8A16/W4A16 bias sums) is done by the compute wave that owns the
+//     step, for itself: the link from one projection to the next is a poll and a copy.
 //
 // Work: each projection's 16-row tiles are dealt to workgroups whole (all of K), in
 // contiguous ranges chosen so that every workgroup's running total of weight bytes stays
@@ -90,8 +92,7 @@ struct SxLayout {
 // Control words (uint32 each, at ctl_off).
 enum SxCtl {
   kCtlStaged = 0,  // [2][kSxIo]: IO wave i's part of staging buffer b holds work entry k: word = k + 1
-  kCtlIoBar = 2 * kSxIo,  // IO-team barrier counter
-  kCtlPart = 2 * kSxIo + 4,  // [kSxSlots][kSxCompute]: generation of the partial sums compute wave c left in the slot
+  kCtlPart = 2 * kSxIo,  // [kSxSlots][kSxCompute]: generation of the partial sums compute wave c left in the slot
   kCtlFree = kCtlPart + kSxSlots * kSxCompute,  // [kSxSlots]: generations of the slot consumed by the IO waves
   kCtlAmax = kCtlFree + kSxSlots,  // [3][16]: FP8 per-token maxima of entries e % 3 (zeroed between uses)
   kCtlWords = kCtlAmax + 48,
@@ -281,9 +282,10 @@ struct SxRing {
   int pending;       // ops issued and not yet freed
   SxCursor<F> cur;
 
-  __device__ void fill(int lane) {
+  // Issue loads into free slots, up to the end of work entry `last` (every entry: INT_MAX).
+  __device__ void fill(int lane, int last) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the freed slots' reads are done
-    while (!cur.done && pending < R) {
+    while (!cur.done && pending < R && cur.e <= last) {
       cur.issue(base + islot * 1024, lane);
       islot = islot + 1 == R ? 0 : islot + 1;
       ++pending;
@@ -340,13 +342,15 @@ __device__ __forceinline__ void sx_w4_step(f32x4& acc, const uint4 (&c)[2], cons
   }
 }
 
-// Staging geometry of a projection with k inputs (the staged slice is all of K).
+// Staging geometry of a projection with k inputs (the staged slice is all of K). Every format
+// stages the bf16 activation (FP8: the compute wave that owns a step turns its 256 bytes per
+// token into the step's 128 e4m3 codes in place, at the start of the region).
 __device__ __host__ inline void sx_stage_args(const FmtInfo& fi, int m, int k, GemmArgs& a) {
   a.m = m;
   a.k = k;
   a.nsteps = k / fi.kstep;
   a.sps = a.nsteps;
-  a.xstride = ((k * fi.xbytes + 16) + 15) & ~15;
+  a.xstride = ((k * 2 + 16) + 15) & ~15;
   a.off_sx = (m * a.xstride + 15) & ~15;
   a.off_xb = a.off_sx + 64 + 64;  // after the token scales (16 floats) and spare
   a.xb_stride = fi.nsc > 1 ? a.nsteps * fi.nsc : a.nsteps;
@@ -357,19 +361,68 @@ __host__ inline int sx_stage_bytes(const FmtInfo& fi, int m, int k) {
   return a.off_xb + (fi.bias ? m * a.xb_stride * 4 : 0);
 }
 
+// FP8 per-token scale from the token's maximum |x| (bits of a non-negative float), as the
+// reference takes it: max(amax / 448, 1e-12) (engine/kernels/fp8.py:20-28).
+__device__ __forceinline__ float sx_token_scale(uint32_t amax_bits) {
+  return fmaxf(__uint_as_float(amax_bits) / 448.f, 1e-12f);
+}
+
+// Per-step prologue of compute wave cw for its own steps s = cw, cw + kSxCompute, ... of a
+// staged entry; only this wave reads what it writes, so no other wave waits for it.
+//   FP8: the e4m3 codes of each token's 128 values of step s (per-token scale from the
+//        entry's maxima), written over the first half of the step's bf16 region. Items are
+//        (step, token, 16-byte chunk), 16 chunks per region and 64 lanes per pass, so every
+//        region is read whole by one instruction before the codes overwrite it.
+//   W8A16 / W4A16: the bias sums of the step's scale groups (stage_bias's work).
+template <class F>
+__device__ __forceinline__ void sx_own_steps_prologue(const GemmArgs& a, char* stage, const uint32_t* amax, int ns,
+                                                      int cw, int lane, int m) {
+  if constexpr (std::is_same<F, FmtFP8>::value) {
+    // lane r < m holds token r's scale and its IEEE reciprocal; items fetch theirs by shuffle
+    const int mr = min(lane & 15, m - 1);
+    const float scr = sx_token_scale(lds_vload(&amax[mr]));
+    const float yr = 1.f / scr;
+    const int items = ns * m * 16;
+    for (int i0 = 0; i0 < items; i0 += 64) {
+      const int it = i0 + lane;
+      const int c = it & 15, rs = it >> 4;
+      const int mm = it < items ? rs % m : 0;
+      const float sc = __shfl(scr, mm, 64), y = __shfl(yr, mm, 64);
+      if (it < items) {
+        char* p = stage + mm * a.xstride + (cw + (rs / m) * kSxCompute) * 256;
+        const uint4 v = *reinterpret_cast<const uint4*>(p + c * 16);
+        *reinterpret_cast<uint2*>(p + c * 8) = e4m3_chunk(v, sc, y);
+      }
+    }
+  } else if constexpr (F::BIAS != 0.f) {
+    constexpr int NJ = F::NSC > 1 ? F::NSC : 1;
+    const int mm = lane & 15, mrow = min(mm, m - 1);
+    float* xb = reinterpret_cast<float*>(stage + a.off_xb);
+    for (int jj = 0; jj < ns; ++jj) {
+      const int s = cw + jj * kSxCompute;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 d = F::bias_chain(stage, s, j, lane, mrow * a.xstride);
+        if ((lane >> 4) == 0 && mm < m) xb[mm * a.xb_stride + s * NJ + j] = d[0];
+      }
+    }
+  }
+}
+
 // The compute waves: stream the ring, run each tile's MFMAs over this wave's steps, hand the
 // tile's partial sums to the IO waves.
 template <class F, int R>
 __device__ __forceinline__ void sx_compute(const SxLayout& L, char* lds, const SxWork* work, int nwork,
                                            const SxComp* comp, const Waits& w) {
   constexpr bool W4 = std::is_same<F, FmtW4>::value;
+  constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63, cw = uni((int)threadIdx.x >> 6);
   uint32_t* ctl = reinterpret_cast<uint32_t*>(lds + L.ctl_off);
   SxRing<F, R> rg;
   rg.base = lds + L.ring_off + cw * R * 1024;
   rg.islot = rg.cslot = rg.pending = 0;
   rg.cur.start(work, comp, nwork, cw, lane);
-  rg.fill(lane);
+  rg.fill(lane, 0x7fffffff);
   const FmtInfo fi = info<F>();
   const int mrow = min(lane & 15, L.m - 1);
   const int rowl = 4 * (lane >> 4);
@@ -385,6 +438,7 @@ __device__ __forceinline__ void sx_compute(const SxLayout& L, char* lds, const S
     const int xoff = mrow * a.xstride;
 #pragma unroll
     for (int i = 0; i < kSxIo; ++i) lds_wait_ge_quiet(&ctl[kCtlStaged + (e & 1) * kSxIo + i], (uint32_t)e + 1, w);
+    if (ntile > 0) sx_own_steps_prologue<F>(a, const_cast<char*>(stage), &ctl[kCtlAmax + 16 * (e % 3)], ns, cw, lane, L.m);
     for (int t = 0; t < ntile; ++t, ++q) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       // Groups of up to four of this wave's steps (the step within the group is a compile-time
@@ -416,12 +470,16 @@ __device__ __forceinline__ void sx_compute(const SxLayout& L, char* lds, const S
             } else {
               f32x4 accs[1] = {acc};
               const int xo[1] = {xoff}, mr[1] = {mrow};
-              F::template compute<1>(accs, c[u], stage, a, s, lane, xo, mr, rowl);
+              // FP8: the step's codes sit at the start of its 256-byte bf16 region
+              F::template compute<1>(accs, c[u], stage, a, FP8 ? 2 * s : s, lane, xo, mr, rowl);
               acc = accs[0];
             }
           }
         }
-        rg.fill(lane);
+        // While computing entry e, refill only with entry e's loads: a load issue occupies the
+        // wave (about 1 KB per 110 ns), and later entries' loads can wait for the time this wave
+        // spends waiting for the next entry's input.
+        rg.fill(lane, e);
       }
       // Partial sums of tile q to its slot, once the IO waves are done with the slot's
       // previous tile; then the flag that says they are there.
@@ -435,42 +493,66 @@ __device__ __forceinline__ void sx_compute(const SxLayout& L, char* lds, const S
       asm volatile("" ::: "memory");
       if (lane == 0) lds_vstore(&ctl[kCtlPart + slot * kSxCompute + cw], (uint32_t)(q / kSxSlots + 1));
     }
+    rg.fill(lane, 0x7fffffff);  // the entry is done: stream ahead while the next input is produced
   }
   wait_vm<0>();  // no ring load may land after the workgroup's LDS is released
 }
 
 // ---- IO waves ---------------------------------------------------------------------------
 
-// The IO waves as a team: staging helpers take it in place of the whole workgroup; its
-// barrier is an LDS counter (the compute waves are never at the same point).
-struct SxIoTeam {
-  uint32_t* bar;
-  Waits w;
-  mutable uint32_t gen;  // barriers passed by this wave (the same in every IO wave)
-  __device__ int tid() const { return (int)threadIdx.x - kSxCompute * 64; }
-  __device__ int size() const { return kSxIo * 64; }
-  __device__ void sync() const {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    ++gen;
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(as_lds(bar), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    lds_wait_ge(bar, gen * kSxIo, w, kWaitInput);
+// The IO waves' staging of one entry: each thread fetches chunks of 8 values (U in flight),
+// waits until they have all been published, and stores them as bf16 (in the format's chunk
+// order) -- nothing else, so the link from the producers to the compute waves is a poll and a
+// copy. FP8: the per-token maxima |x| too: each thread keeps the maximum of its chunks of one
+// token and adds it with one LDS atomic at the end (a chunk of another token, where a token's
+// row ends inside the thread's chunks, takes its own). No barrier: the compute waves wait for
+// every IO wave's flag.
+template <class F, class XS, int U>
+__device__ __forceinline__ void sx_stage_raw(const GemmArgs& a, const XS& xs, char* stage, int tid, int nthr,
+                                             uint32_t* amax) {
+  constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
+  const int cpr = a.k >> 3;
+  const int total = a.m * cpr;
+  int row = -1;      // FP8: the token of this thread's running maximum
+  float rmax = 0.f;  // and the maximum
+  for (int q0 = tid; q0 < total; q0 += U * nthr) {
+    typename XS::Raw r[U];
+    auto chunk = [&](int u, int& mm, int& kabs) {
+      const int q = q0 + u * nthr;
+      mm = q / cpr;
+      kabs = (q - mm * cpr) * 8;
+      return q < total;
+    };
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
+    }
+    settle_batch<XS, U>(a, xs, r, chunk);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) {
+        const uint4 v = xs.value(r[u]);
+        if constexpr (FP8) {
+          *reinterpret_cast<uint4*>(stage + mm * a.xstride + kabs * 2) = v;
+          const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+          float mx = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
+          if (row < 0) row = mm;
+          if (mm == row)
+            rmax = fmaxf(rmax, mx);
+          else
+            atomicMax(&amax[mm], __float_as_uint(mx));
+        } else {
+          *reinterpret_cast<uint4*>(stage + mm * a.xstride + kabs * 2) = F::order(v);
+        }
+      }
+    }
   }
-};
-
-// Bias sums of the staged activation (W8A16, W4A16): one MFMA chain per (scale group, token
-// fragment), spread over the IO waves (stage_bias's work for the IO team).
-template <class F>
-__device__ void sx_stage_bias(const GemmArgs& a, char* stage, int iw) {
-  constexpr int NJ = F::NSC > 1 ? F::NSC : 1;
-  const int lane = threadIdx.x & 63;
-  const int frags = (a.m + 15) >> 4;
-  float* xb = reinterpret_cast<float*>(stage + a.off_xb);
-  for (int item = iw; item < a.nsteps * NJ * frags; item += kSxIo) {
-    const int mt = item % frags, sj = item / frags;
-    const int mm = 16 * mt + (lane & 15);
-    const int mrow = min(mm, a.m - 1);
-    const f32x4 dv = F::bias_chain(stage, sj / NJ, sj % NJ, lane, mrow * a.xstride);
-    if ((lane >> 4) == 0 && mm < a.m) xb[mm * a.xb_stride + sj] = dv[0];
+  if constexpr (FP8) {
+    if (row >= 0) atomicMax(&amax[row], __float_as_uint(rmax));
   }
 }
 
@@ -481,10 +563,12 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
   constexpr int UNROLL = 5;  // chunks per IO thread in flight: one pass over k <= 10240 at m = 1
   const int lane = threadIdx.x & 63, iw = ((int)threadIdx.x >> 6) - kSxCompute;
   uint32_t* ctl = reinterpret_cast<uint32_t*>(lds + L.ctl_off);
-  const SxIoTeam team{&ctl[kCtlIoBar], w, 0u};
+  const int tid = (int)threadIdx.x - kSxCompute * 64;  // within the IO waves
+  constexpr int nthr = kSxIo * 64;
   const FmtInfo fi = info<F>();
   float* sws = reinterpret_cast<float*>(lds + L.sws_off);
-  int q0 = 0;  // first tile (workgroup-wide count) of the entry
+  int q0 = 0;       // first tile (workgroup-wide count) of the entry
+  int q0_prev = 0;  // first tile of the previous entry
   for (int e = 0; e < nwork; ++e) {
     const SxWork wk = work[e];
     const SxProj& P = projs[wk.proj];
@@ -495,9 +579,20 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
     a.mode = P.sw ? QLX_MODE_SWIGLU : QLX_MODE_BF16;
     a.half = P.half;
     a.n = P.n;
-    // Staging buffer e & 1, the per-row scales e & 1 and the FP8 maxima e & 1 were last used
-    // by entry e - 2, which every IO wave finished before the barriers of entry e - 1's
-    // staging: they are free.
+    // Entry e reuses entry e - 2's buffers. Every IO wave has staged entry e - 1, so every IO
+    // wave is done with entry e - 2's epilogues (per-row scales e & 1, FP8 maxima (e + 1) % 3);
+    // the compute waves have left partial sums of entry e - 2's last tile, so they are done with
+    // its staged activation (buffer e & 1).
+    if (e >= 1) {
+#pragma unroll
+      for (int i = 0; i < kSxIo; ++i) lds_wait_ge(&ctl[kCtlStaged + ((e - 1) & 1) * kSxIo + i], (uint32_t)e, w, kWaitInput);
+    }
+    if (e >= 2) {
+      const int ql = q0_prev - 1, slot = ql % kSxSlots;
+#pragma unroll
+      for (int c = 0; c < kSxCompute; ++c)
+        lds_wait_ge(&ctl[kCtlPart + slot * kSxCompute + c], (uint32_t)(ql / kSxSlots + 1), w, kWaitPartial);
+    }
     // Per-row scales of the entry's tiles: loaded before the polls and stored after staging, so
     // their memory latency overlaps the wait for the input.
     constexpr int NSW = kSxMaxTilesPerEntry * 16 / (kSxIo * 64);
@@ -505,46 +600,35 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
     if constexpr (F::NSC == 0) {
 #pragma unroll
       for (int u = 0; u < NSW; ++u) {
-        const int i = team.tid() + u * team.size();
+        const int i = tid + u * nthr;
         swv[u] = 0u;
         if (i < wk.ntile * 16)
           swv[u] = gmem(reinterpret_cast<const uint16_t*>(P.ws))[weight_row(a, wk.tile0 + i / 16, i & 15)];
       }
     }
-    // FP8 maxima: entry e's buffer was cleared at the start of entry e - 1. Clear entry e + 1's
-    // now: it was last read by entry e - 2, which every IO wave finished before entry e - 1's
-    // staging barrier, and no IO wave can reach entry e + 1 before passing entry e's barrier,
-    // which waits for this wave.
+    // FP8 maxima: entry e's buffer was cleared at the start of entry e - 1, before IO wave 0
+    // raised its flag for entry e - 1, which every IO wave waited for above. Clear entry e + 1's:
+    // its last readers, entry e - 2's epilogues, are done.
     uint32_t* amax = &ctl[kCtlAmax + 16 * (e % 3)];
     if constexpr (FP8) {
-      if (team.tid() < 16) lds_store(&ctl[kCtlAmax + 16 * ((e + 1) % 3) + team.tid()], 0u);
+      if (tid < 16) lds_store(&ctl[kCtlAmax + 16 * ((e + 1) % 3) + tid], 0u);
     }
     float* swe = sws + (e & 1) * kSxMaxTilesPerEntry * 16;
     if (P.xwire) {
       const XWire xs(P.xwire, P.xpitch, L.m, w);
-      if constexpr (FP8)
-        stage_fp8_act<XWire, SxIoTeam, UNROLL>(a, xs, stage, 0, a.nsteps, team, amax);
-      else
-        stage_bf16<F, XWire, SxIoTeam, UNROLL>(a, xs, stage, 0, a.nsteps, team);
+      sx_stage_raw<F, XWire, UNROLL>(a, xs, stage, tid, nthr, amax);
     } else {
-      if constexpr (FP8)
-        stage_fp8_act<XPlain, SxIoTeam, UNROLL>(a, XPlain{}, stage, 0, a.nsteps, team, amax);
-      else
-        stage_bf16<F, XPlain, SxIoTeam, UNROLL>(a, XPlain{}, stage, 0, a.nsteps, team);
+      sx_stage_raw<F, XPlain, UNROLL>(a, XPlain{}, stage, tid, nthr, amax);
     }
     if constexpr (F::NSC == 0) {
 #pragma unroll
       for (int u = 0; u < NSW; ++u) {
-        const int i = team.tid() + u * team.size();
+        const int i = tid + u * nthr;
         if (i < wk.ntile * 16) swe[i] = bf2f(swv[u]);
       }
     }
-    if constexpr (!FP8) {
-      team.sync();  // the bias sums read the whole staged activation
-      if constexpr (F::BIAS != 0.f) sx_stage_bias<F>(a, stage, iw);
-    }
-    // This wave's part of the staged activation (FP8: codes and scales, final after the
-    // staging's barrier) is in place: its own flag.
+    // This wave's part of the staged activation (and of the maxima) is in place: its flag.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (lane == 0) lds_store(&ctl[kCtlStaged + (e & 1) * kSxIo + iw], (uint32_t)e + 1);
     // Epilogues: tile q of the workgroup goes to IO wave q % kSxIo.
     const int nout = P.sw ? P.half : P.n;
@@ -571,7 +655,7 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
 #pragma unroll
           for (int c = 0; c < kSxCompute; ++c) s += red[c * wstride + rl[i] * L.m + mm];
           if constexpr (F::NSC == 0) s *= swe[t * 16 + rl[i]];
-          if constexpr (FP8) s *= reinterpret_cast<const float*>(stage + a.off_sx)[mm];
+          if constexpr (FP8) s *= sx_token_scale(lds_load(&amax[mm]));
           v[i] = s;
         }
         float o0 = v[0], o1 = v[1];
@@ -588,6 +672,7 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's reads are done
       if (lane == 0) lds_store(&ctl[kCtlFree + slot], (uint32_t)(q / kSxSlots + 1));
     }
+    q0_prev = q0;
     q0 += wk.ntile;
   }
 }
@@ -622,15 +707,17 @@ stream_kernel(const char* __restrict__ desc, SxLayout L, uint32_t epoch, int* er
 }
 
 // Ring sizes the kernel is built for (1 KB lines per compute wave); a launch takes the largest
-// its LDS allows.
-// (At least 9: a W4A16 group takes 9 ops at once.)
-constexpr int kSxRings[] = {16, 14, 12};
+// its LDS allows. A group of four steps takes 8 lines at once, W4A16's 9 (8 is not built for it).
+constexpr int kSxRings[] = {16, 14, 12, 10, 8};
 
 template <class F>
 const void* sx_fn_r(int ring) {
   if (ring == 16) return reinterpret_cast<const void*>(&stream_kernel<F, 16>);
   if (ring == 14) return reinterpret_cast<const void*>(&stream_kernel<F, 14>);
   if (ring == 12) return reinterpret_cast<const void*>(&stream_kernel<F, 12>);
+  if (ring == 10) return reinterpret_cast<const void*>(&stream_kernel<F, 10>);
+  if constexpr (F::NSC == 0)
+    if (ring == 8) return reinterpret_cast<const void*>(&stream_kernel<F, 8>);
   return nullptr;
 }
 const void* sx_fn(int fmt, int ring) {
@@ -760,7 +847,7 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, vo
   const int room = (kLdsLimit - off) / (kSxCompute * 1024);
   L.ring_lines = 0;
   for (int r : kSxRings)
-    if (r <= room) {
+    if (r <= room && sx_fn(fmt, r) != nullptr) {
       L.ring_lines = r;
       break;
     }

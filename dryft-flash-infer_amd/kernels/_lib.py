@@ -70,6 +70,7 @@ SIGNATURES = {
     "qlx_row_major_ref": ([_P, _P, _I, _I, _P], _I),
     "qlx_quantize_fp8_weight": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "qlx_quantize_fp8_act": ([_P, _P, _P, _I, _I, _P], _I),
+    "qlx_fp8_selfcheck": ([_P, _P], _I),
     "qlx_int8_prepare": ([_P, _P, _I, _I, _P], _I),
     "qlx_quantize_act_int8": ([_P, _P, _P, _P, _P, _I, _I, _P], _I),
     "qlx_plan_linear": ([_I, _I, _I, _I, _I, _PLAN], _I),

@@ -97,6 +97,14 @@ int qlx_quantize_fp8_weight(const void* w, void* code, void* scale, int rows, in
  * (engine/kernels/cuda_int8.py:58-88) with the north star's FP8 per-token granularity. */
 int qlx_quantize_fp8_act(const void* x, void* code, float* scale, int m, int k, void* stream);
 
+/* Exhaustive check of the arithmetic every FP8 quantizer here shares (weights, activations,
+ * in-kernel prologues): for each bf16 maximum (finite or +inf), its scale max(amax/448, 1e-12)
+ * and every bf16 value of no larger magnitude (plus every NaN), the fast code path against
+ * IEEE division + clamp + RNE cast. No counterpart in the reference; a diagnostic for tests.
+ * counts: 66 zeroed uint64 in device memory; counts[0] = mismatches, counts[1] = recorded,
+ * counts[2..65] = (amax bits << 48 | x bits << 32 | fast code << 8 | reference code). */
+int qlx_fp8_selfcheck(unsigned long long* counts, void* stream);
+
 /* cuda_int8.Prepared weight (engine/kernels/cuda_int8.py:100-108) from the fragment-permuted
  * row-major bytes. */
 int qlx_int8_prepare(const void* row_major_ref, void* out, int rows, int k, void* stream);
