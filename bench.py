@@ -122,6 +122,37 @@ class Stack:
                 h = y
         return chain.build()
 
+    def norm_executor(self, eps=1e-6):
+        """The decode step with its residual adds and RMSNorms as input stages of the stream
+        executor: qkv <- rmsnorm(h), gate_up <- rmsnorm(h + o), the next qkv and the lm_head <-
+        rmsnorm(h + o + down) (FP8: the normed input quantized per token in the same stage)."""
+        from kernels.decode_stack import StreamStack
+        chain = StreamStack(self.fmt, self.m)
+        gen = torch.Generator(device="cuda").manual_seed(77)
+        new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
+        norm_w = lambda: (1.0 + 0.1 * torch.randn(2560, generator=gen, device="cuda")).to(torch.bfloat16)
+        self.norm_keep = []
+        resid, delta, q, h0 = self.x[2560], None, None, None
+        for name, packed, k, sw in self.calls:
+            y = new(packed.rows // 2 if sw else packed.rows)
+            if name in ("qkv", "lm_head"):
+                r_out, w = new(2560), norm_w()
+                chain.add_normed(packed, resid, y, w, eps, delta=delta, resid_out=r_out)
+                self.norm_keep += [r_out, w]
+                h0 = r_out
+            elif name == "gate_up":
+                r_out, w = new(2560), norm_w()
+                chain.add_normed(packed, h0, y, w, eps, delta=q, resid_out=r_out, swiglu=True)
+                self.norm_keep += [r_out, w]
+                resid = r_out
+            else:
+                chain.add(packed, q[:, :4096] if name == "o" else q, y)
+                if name == "down":
+                    delta = y
+            self.norm_keep.append(y)
+            q = y
+        return chain.build()
+
     def bytes_alg(self, which=None):
         """Algorithmic bytes: weight codes + scales + M*K*2 (x in) + M*N_out*2 (y out)."""
         total = 0
@@ -306,6 +337,15 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
                                               "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
                                               "pieces": chain.launch.pieces != 0}
             del chain
+    if m <= 2:
+        # the full decode step's linear path with its residual adds and RMSNorms fused into the
+        # projections' input stages (stream executor); not the headline, which is the linears alone
+        chain = stack.norm_executor()
+        ms_norm = time_fn(chain.run, steps, warmup)
+        if chain.failed():
+            raise RuntimeError("stream executor with norm stages: a wait gave up")
+        out["norm_chain_us"] = round(ms_norm * 1e3, 2)
+        del chain
     cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
     ms = cands[out["path"]] / 1e3
@@ -455,6 +495,7 @@ def main():
             if (fmt, m) == (args.workload, args.m):
                 continue
             st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=True)
+            per = res.pop("per_projection")
             if (fmt, m) == ("w4a16", 1) and not args.no_cpu:
                 res["cpu_baseline"] = cpu_baseline(st)
                 log(f"cpu baseline w4a16 M=1: {res['cpu_baseline']['value'] / 1e3:.1f} ms per step "
@@ -492,7 +533,9 @@ def main():
         },
         "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
                      "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
-                     "executor_shapes": head.get("shapes_us")},
+                     "executor_shapes": head.get("shapes_us"),
+                     # the step with its residual adds and RMSNorms fused into the input stages
+                     "stream_executor_with_norm_stages": head.get("norm_chain_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),
         "roofline": roofline,

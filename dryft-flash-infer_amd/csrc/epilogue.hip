@@ -7,6 +7,8 @@
 //   add_rms_norm      residual then rms_norm               engine/kernels/reference.py:19-28
 //   swiglu            bf16(bf16(silu(bf16 g)) * bf16 u)    engine/kernels/swiglu.py:37-53
 //   add_norm_quant    residual, rms_norm, INT8 quantize    engine/kernels/cuda_int8.py:17-44
+//   add_norm_fp8      residual, rms_norm, per-token e4m3 quantize (the FP8 W8A8 activation
+//                     of qlx_quantize_fp8_act, from the normed row held on chip)
 #include "common.h"
 #include "../../include/qlinear.h"
 
@@ -37,7 +39,8 @@ __global__ void __launch_bounds__(256)
 add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
                     const float* __restrict__ planes, int splits, const uint16_t* __restrict__ w,
                     uint16_t* __restrict__ res, uint16_t* __restrict__ y, int8_t* __restrict__ q,
-                    float* __restrict__ qs, int rows, int n, float eps) {
+                    float* __restrict__ qs, uint8_t* __restrict__ q8, float* __restrict__ q8s, int rows, int n,
+                    float eps) {
   extern __shared__ float rbuf[];  // the row's residual, fp32
   __shared__ double part[4];
   const int row = blockIdx.x;
@@ -74,6 +77,28 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
     const float v = round_bf(round_bf(rbuf[c] * scale) * bf2f(w[c]));
     rbuf[c] = v;
     if (y) y[base + c] = f2bf(v);
+  }
+  if (q8) {
+    // FP8 per-token activation quantize of the normed row (every value is a bf16 value):
+    // scale = max(amax / 448, 1e-12), codes e4m3(x / scale).
+    __shared__ float pmax[4];
+    __syncthreads();
+    float mx = 0.f;
+    for (int c = threadIdx.x; c < n; c += 256) mx = fmaxf(mx, fabsf(rbuf[c]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) pmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float sc = fmaxf(fmaxf(fmaxf(pmax[0], pmax[1]), fmaxf(pmax[2], pmax[3])) / 448.f, 1e-12f);
+    const float yr = 1.f / sc;
+    if (threadIdx.x == 0) q8s[row] = sc;
+    for (int c8 = threadIdx.x; c8 < (n >> 3); c8 += 256) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pk[i] = (uint32_t)f2bf(rbuf[8 * c8 + 2 * i]) | ((uint32_t)f2bf(rbuf[8 * c8 + 2 * i + 1]) << 16);
+      *reinterpret_cast<uint2*>(q8 + base + 8 * c8) = e4m3_chunk(uint4{pk[0], pk[1], pk[2], pk[3]}, sc, yr);
+    }
+    return;
   }
   if (!q) return;
   // INT8 activation quantize per 64-group, fragment order (cuda_int8.py:30-44).
@@ -146,7 +171,7 @@ int qlx_add_rms_norm(const void* x, const void* delta, const float* planes, int 
   QLX_REQUIRE(planes == nullptr || splits >= 1, "planes need splits >= 1");
   add_rms_norm_kernel<<<rows, 256, n * sizeof(float), (hipStream_t)stream>>>(
       (const uint16_t*)x, (const uint16_t*)delta, planes, splits, (const uint16_t*)w, (uint16_t*)res,
-      (uint16_t*)y, nullptr, nullptr, rows, n, eps);
+      (uint16_t*)y, nullptr, nullptr, nullptr, nullptr, rows, n, eps);
   QLX_LAUNCH_CHECK("add_rms_norm");
 }
 
@@ -157,8 +182,19 @@ int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* plane
   QLX_REQUIRE(planes == nullptr || splits >= 1, "planes need splits >= 1");
   add_rms_norm_kernel<<<rows, 256, n * sizeof(float), (hipStream_t)stream>>>(
       (const uint16_t*)x, (const uint16_t*)delta, planes, splits, (const uint16_t*)w, (uint16_t*)res,
-      nullptr, (int8_t*)q, q_scale, rows, n, eps);
+      nullptr, (int8_t*)q, q_scale, nullptr, nullptr, rows, n, eps);
   QLX_LAUNCH_CHECK("add_norm_quant_int8");
+}
+
+int qlx_add_norm_quant_fp8(const void* x, const void* delta, const float* planes, int splits, const void* w,
+                           void* res, void* y, void* code, float* scale, int rows, int n, float eps, void* stream) {
+  QLX_REQUIRE(rows > 0 && n > 0 && n <= 16384 && n % 8 == 0, "n=%d must be a multiple of 8 up to 16384", n);
+  QLX_REQUIRE(planes == nullptr || splits >= 1, "planes need splits >= 1");
+  QLX_REQUIRE(code != nullptr && scale != nullptr, "codes and scales are required");
+  add_rms_norm_kernel<<<rows, 256, n * sizeof(float), (hipStream_t)stream>>>(
+      (const uint16_t*)x, (const uint16_t*)delta, planes, splits, (const uint16_t*)w, (uint16_t*)res,
+      (uint16_t*)y, nullptr, nullptr, (uint8_t*)code, scale, rows, n, eps);
+  QLX_LAUNCH_CHECK("add_norm_quant_fp8");
 }
 
 int qlx_swiglu(const void* gate_up, const float* planes, int splits, void* out, int rows, int inter,

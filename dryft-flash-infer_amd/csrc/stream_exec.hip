@@ -42,6 +42,8 @@ constexpr int kSxCompute = 8;  // compute waves per workgroup
 constexpr int kSxIo = 4;       // IO waves per workgroup
 constexpr int kSxSlots = 8;    // tiles whose partial sums may be in flight between the two
 constexpr int kSxMaxTilesPerEntry = 48;         // per-row scales staged per work entry
+constexpr int kSxNormU = 3;    // chunks per IO thread of a residual + RMSNorm stage (one pass)
+constexpr int kSxNormMaxM = 2;  // tokens of such a stage: m * k / 8 <= kSxNormU * 256
 
 // One projection, as the IO waves read it (global memory).
 struct alignas(16) SxProj {
@@ -55,7 +57,17 @@ struct alignas(16) SxProj {
   int sw;                 // SwiGLU epilogue (tile = 8 gate + 8 up rows)
   int xpitch;             // values per token row of xwire
   int half;               // n / 2
-  int pad;
+  int norm;               // input stage: residual add + RMSNorm (xwire, if any, is the delta)
+  // Residual add + RMSNorm input stage (norm != 0): r = bf16(resid + delta), input =
+  // bf16(bf16(r * rsqrt(mean(r^2) + eps)) * nw).
+  const void* nw;         // RMSNorm weight, bf16 [k]
+  const void* rmem;       // residual in memory (bf16 [m][k]), or null
+  const uint64_t* rwire;  // residual published by an earlier projection's stage, or null
+  void* rout;             // r to memory (by the workgroup holding tile 0), or null
+  uint64_t* rwire_out;    // r published for later stages, or null
+  void* nout;             // the normed input to memory (tile 0's workgroup), or null
+  float eps;
+  int pad2;
 };
 
 // What the compute waves need of a projection (copied to LDS once per launch).
@@ -92,7 +104,8 @@ struct SxLayout {
 // Control words (uint32 each, at ctl_off).
 enum SxCtl {
   kCtlStaged = 0,  // [2][kSxIo]: IO wave i's part of staging buffer b holds work entry k: word = k + 1
-  kCtlPart = 2 * kSxIo,  // [kSxSlots][kSxCompute]: generation of the partial sums compute wave c left in the slot
+  kCtlIoBar = 2 * kSxIo,  // IO-team barrier counter (residual + RMSNorm stages)
+  kCtlPart = 2 * kSxIo + 4,  // [kSxSlots][kSxCompute]: generation of the partial sums compute wave c left in the slot
   kCtlFree = kCtlPart + kSxSlots * kSxCompute,  // [kSxSlots]: generations of the slot consumed by the IO waves
   kCtlAmax = kCtlFree + kSxSlots,  // [3][16]: FP8 per-token maxima of entries e % 3 (zeroed between uses)
   kCtlWords = kCtlAmax + 48,
@@ -355,10 +368,16 @@ __device__ __host__ inline void sx_stage_args(const FmtInfo& fi, int m, int k, G
   a.off_xb = a.off_sx + 64 + 64;  // after the token scales (16 floats) and spare
   a.xb_stride = fi.nsc > 1 ? a.nsteps * fi.nsc : a.nsteps;
 }
-__host__ inline int sx_stage_bytes(const FmtInfo& fi, int m, int k) {
+__host__ __device__ inline int sx_stage_bytes(const FmtInfo& fi, int m, int k) {
   GemmArgs a = {};
   sx_stage_args(fi, m, k, a);
   return a.off_xb + (fi.bias ? m * a.xb_stride * 4 : 0);
+}
+// A residual + RMSNorm stage keeps its sums of squares (one double per 8-value chunk, then the
+// token totals) in its staging buffer after what the compute waves read: kSxCssBytes from here.
+constexpr int kSxCssBytes = (kSxNormU * kSxIo * 64 + kSxNormMaxM) * 8;
+__host__ __device__ inline int sx_css_offset(const FmtInfo& fi, int m, int k) {
+  return (sx_stage_bytes(fi, m, k) + 15) & ~15;
 }
 
 // FP8 per-token scale from the token's maximum |x| (bits of a non-negative float), as the
@@ -556,6 +575,145 @@ __device__ __forceinline__ void sx_stage_raw(const GemmArgs& a, const XS& xs, ch
   }
 }
 
+// Barrier of the IO waves (residual + RMSNorm stages only): an LDS counter each IO wave adds
+// to; `gen` counts the barriers this wave has passed, the same number in every IO wave.
+__device__ __forceinline__ void sx_io_barrier(uint32_t* bar, uint32_t& gen, const Waits& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  ++gen;
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(as_lds(bar), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  lds_wait_ge(bar, gen * kSxIo, w, kWaitInput);
+}
+
+// Residual add + RMSNorm input stage (engine/kernels/reference.py:13-28, norm.py:125-139; the
+// arithmetic of qlx_add_rms_norm): r = bf16(resid + delta) with delta the published output of an
+// earlier projection (DELTA) and resid published by an earlier stage (RWIRE) or in memory; the
+// sum of r^2 per token in fp64 in a fixed order (per 8-value chunk, then chunk by chunk), the
+// mean rounded to fp32, scale = 1 / sqrt(mean + eps) in fp32; the input bf16(bf16(r * scale) * w)
+// goes to the staging buffer as bf16 like any other activation (FP8: with its per-token maxima,
+// so the compute waves' codes are the FP8 per-token quantization of the normed row). Every
+// workgroup with work in the projection computes the same r and input from the same words in the
+// same order; the one holding tile 0 also writes r (memory and published) and the input. One
+// pass: m * k / 8 <= kSxNormU * 256 and k a multiple of 512, checked on the host.
+template <class F, bool RWIRE, bool DELTA>
+__device__ __forceinline__ void sx_stage_norm(const GemmArgs& a, const SxProj& P, char* stage, int tid, int nthr,
+                                              uint32_t* amax, double* css, uint32_t* bar, uint32_t& gen, bool owner,
+                                              const Waits& w) {
+  constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
+  constexpr int U = kSxNormU;
+  const int lane = threadIdx.x & 63, iw = tid >> 6;
+  const int cpr = a.k >> 3, total = a.m * cpr;
+  const XWire dx(DELTA ? P.xwire : nullptr, DELTA ? P.xpitch : 0, a.m, w);
+  const XWire rx(RWIRE ? P.rwire : nullptr, RWIRE ? a.k : 0, a.m, w);
+  GemmArgs ar = a;  // the residual in memory, [m][k]
+  ar.x = P.rmem;
+  auto chunk = [&](int u, int& mm, int& kabs) {
+    const int q = tid + u * nthr;
+    mm = q / cpr;
+    kabs = (q - mm * cpr) * 8;
+    return q < total;
+  };
+  XWire::Raw rd[U], rr[U];
+  XPlain::Raw rp[U];
+  uint4 wv[U], rv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      if constexpr (DELTA) dx.fetch(a, mm, kabs, rd[u]);
+      if constexpr (RWIRE)
+        rx.fetch(a, mm, kabs, rr[u]);
+      else
+        XPlain{}.fetch(ar, mm, kabs, rp[u]);
+      const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(P.nw) + kabs));
+      wv[u] = uint4{t[0], t[1], t[2], t[3]};
+    }
+  }
+  if constexpr (DELTA) settle_batch<XWire, U>(a, dx, rd, chunk);
+  if constexpr (RWIRE) settle_batch<XWire, U>(a, rx, rr, chunk);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      const uint4 x = RWIRE ? rx.value(rr[u]) : rp[u].v;
+      uint4 r = x;
+      if constexpr (DELTA) {
+        const uint4 d = dx.value(rd[u]);
+        const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ds[4] = {d.x, d.y, d.z, d.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = bf16_pair(bf2f(xs[i] & 0xffffu) + bf2f(ds[i] & 0xffffu), bf2f(xs[i] >> 16) + bf2f(ds[i] >> 16));
+        r = uint4{o[0], o[1], o[2], o[3]};
+      }
+      rv[u] = r;
+      const uint32_t rs[4] = {r.x, r.y, r.z, r.w};
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double lo = bf2f(rs[i] & 0xffffu), hi = bf2f(rs[i] >> 16);
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+      css[tid + u * nthr] = ss;
+    }
+  }
+  sx_io_barrier(bar, gen, w);
+  // Token t's total, by IO wave t: lane l sums chunks l, l + 64, ... in order, then the wave's
+  // lanes pairwise (a fixed tree).
+  double* tot = css + kSxNormU * 256;
+  if (iw < a.m) {
+    double t = 0.0;
+    for (int c = lane; c < cpr; c += 64) t += css[iw * cpr + c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (lane == 0) tot[iw] = t;
+  }
+  sx_io_barrier(bar, gen, w);
+  int row = -1;
+  float rmax = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      // mean rounded to fp32, + eps and 1/sqrt in fp32, as torch's rsqrt(mean + eps)
+      const float scale = 1.0f / sqrtf((float)(tot[mm] / (double)a.k) + P.eps);
+      const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      uint32_t o[4];
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale) * bf2f(ws[i] & 0xffffu));
+        const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale) * bf2f(ws[i] >> 16));
+        o[i] = bf16_pair(y0, y1);
+        mx = fmaxf(mx, fmaxf(fabsf(y0), fabsf(y1)));
+      }
+      const uint4 y = uint4{o[0], o[1], o[2], o[3]};
+      if constexpr (FP8) {
+        *reinterpret_cast<uint4*>(stage + mm * a.xstride + kabs * 2) = y;
+        if (row < 0) row = mm;
+        if (mm == row)
+          rmax = fmaxf(rmax, mx);
+        else
+          atomicMax(&amax[mm], __float_as_uint(mx));
+      } else {
+        *reinterpret_cast<uint4*>(stage + mm * a.xstride + kabs * 2) = F::order(y);
+      }
+      if (owner) {
+        const size_t at = (size_t)mm * a.k + kabs;
+        if (P.rout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P.rout) + at)) = u32x4{rs[0], rs[1], rs[2], rs[3]};
+        if (P.nout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P.nout) + at)) = u32x4{o[0], o[1], o[2], o[3]};
+        if (P.rwire_out) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wire_store_pair(P.rwire_out + (at >> 1) + i, rs[i], w.epoch);
+        }
+      }
+    }
+  }
+  if constexpr (FP8) {
+    if (row >= 0) atomicMax(&amax[row], __float_as_uint(rmax));
+  }
+}
+
 template <class F>
 __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj* projs, const SxWork* work, int nwork,
                                       const Waits& w) {
@@ -569,6 +727,7 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
   float* sws = reinterpret_cast<float*>(lds + L.sws_off);
   int q0 = 0;       // first tile (workgroup-wide count) of the entry
   int q0_prev = 0;  // first tile of the previous entry
+  uint32_t bar_gen = 0;  // IO-team barriers passed
   for (int e = 0; e < nwork; ++e) {
     const SxWork wk = work[e];
     const SxProj& P = projs[wk.proj];
@@ -614,7 +773,21 @@ __device__ __forceinline__ void sx_io(const SxLayout& L, char* lds, const SxProj
       if (tid < 16) lds_store(&ctl[kCtlAmax + 16 * ((e + 1) % 3) + tid], 0u);
     }
     float* swe = sws + (e & 1) * kSxMaxTilesPerEntry * 16;
-    if (P.xwire) {
+    if (P.norm) {
+      double* css = reinterpret_cast<double*>(stage + sx_css_offset(fi, L.m, P.k));
+      const bool owner = wk.tile0 == 0;
+      if (P.rwire) {
+        if (P.xwire)
+          sx_stage_norm<F, true, true>(a, P, stage, tid, nthr, amax, css, &ctl[kCtlIoBar], bar_gen, owner, w);
+        else
+          sx_stage_norm<F, true, false>(a, P, stage, tid, nthr, amax, css, &ctl[kCtlIoBar], bar_gen, owner, w);
+      } else {
+        if (P.xwire)
+          sx_stage_norm<F, false, true>(a, P, stage, tid, nthr, amax, css, &ctl[kCtlIoBar], bar_gen, owner, w);
+        else
+          sx_stage_norm<F, false, false>(a, P, stage, tid, nthr, amax, css, &ctl[kCtlIoBar], bar_gen, owner, w);
+      }
+    } else if (P.xwire) {
       const XWire xs(P.xwire, P.xpitch, L.m, w);
       sx_stage_raw<F, XWire, UNROLL>(a, xs, stage, tid, nthr, amax);
     } else {
@@ -749,28 +922,75 @@ using namespace qlx;
 
 extern "C" {
 
-int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, void* desc, long long* desc_bytes,
-                     void* arena, long long* arena_bytes, qlx_stream_launch* launch) {
+int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                     void* desc, long long* desc_bytes, void* arena, long long* arena_bytes,
+                     qlx_stream_launch* launch) {
   QLX_REQUIRE(sx_fn(fmt, kSxRings[0]) != nullptr, "the stream executor serves W8A16, W4A16 and FP8 W8A8 (format %d)",
               fmt);
   QLX_REQUIRE(m >= 1 && m <= 16, "the stream executor serves m = 1..16 (got %d)", m);
   QLX_REQUIRE(calls != nullptr && ncalls >= 1, "no projections");
   const FmtInfo fi = sx_info(fmt);
-  std::vector<int> src(ncalls, -1), published(ncalls, 0);
+  auto normed = [&](int c) { return norms != nullptr && norms[c].norm_w != nullptr; };
+  std::vector<int> src(ncalls, -1), published(ncalls, 0), rsrc(ncalls, -1), rpublished(ncalls, 0);
+  int knorm = 0;  // widest residual + RMSNorm stage
   for (int c = 0; c < ncalls; ++c) {
     const qlx_stack_call& q = calls[c];
     QLX_REQUIRE(q.n >= 16 && q.n % 16 == 0 && q.k > 0 && q.k % fi.kstep == 0 && q.k % 8 == 0,
                 "projection %d: n=%d k=%d do not fit the tiled format", c, q.n, q.k);
     QLX_REQUIRE(q.mode == QLX_MODE_BF16 || q.mode == QLX_MODE_SWIGLU, "projection %d: mode %d", c, q.mode);
-    QLX_REQUIRE(q.w && q.w_scale && q.x && q.y, "projection %d: NULL pointer", c);
+    QLX_REQUIRE(q.w && q.w_scale && q.y && (normed(c) ? q.x == nullptr : q.x != nullptr),
+                "projection %d: NULL pointer (x must be NULL exactly when the input is a norm stage)", c);
+    if (normed(c)) {
+      QLX_REQUIRE(norms[c].resid != nullptr, "projection %d: a norm stage needs its residual", c);
+      QLX_REQUIRE(q.k % 512 == 0 && m <= kSxNormMaxM && m * (q.k / 8) <= kSxNormU * kSxIo * 64,
+                  "projection %d: a norm stage takes k a multiple of 512 and m * k <= %d (m=%d, k=%d)", c,
+                  kSxNormU * kSxIo * 64 * 8, m, q.k);
+      knorm = std::max(knorm, q.k);
+    }
   }
   auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };
+  // memory a projection or a norm stage writes
+  auto written = [&](const void* p, long long bytes) {
+    for (int j = 0; j < ncalls; ++j) {
+      if (sx_overlaps(p, bytes, calls[j].y, 2LL * m * nout(j))) return true;
+      if (normed(j) && norms[j].resid_out && sx_overlaps(p, bytes, norms[j].resid_out, 2LL * m * calls[j].k))
+        return true;
+      if (normed(j) && norms[j].normed_out && sx_overlaps(p, bytes, norms[j].normed_out, 2LL * m * calls[j].k))
+        return true;
+    }
+    return false;
+  };
   for (int c = 0; c < ncalls; ++c) {
     const long long ybytes = 2LL * m * nout(c);
     for (int j = 0; j < ncalls; ++j)
       if (j != c)
         QLX_REQUIRE(!sx_overlaps(calls[c].y, ybytes, calls[j].y, 2LL * m * nout(j)),
                     "outputs of projections %d and %d overlap", c, j);
+    if (normed(c)) {
+      const qlx_norm_input& nd = norms[c];
+      if (nd.delta) {
+        for (int j = 0; j < c; ++j)
+          if (nd.delta == calls[j].y && calls[c].k == nout(j)) {
+            src[c] = j;
+            published[j] = 1;
+            break;
+          }
+        QLX_REQUIRE(src[c] >= 0, "projection %d: the delta of a norm stage is the whole output of an earlier "
+                    "projection", c);
+      }
+      for (int j = 0; j < c; ++j)
+        if (normed(j) && norms[j].resid_out && nd.resid == norms[j].resid_out && calls[j].k == calls[c].k) {
+          rsrc[c] = j;
+          rpublished[j] = 1;
+          break;
+        }
+      QLX_REQUIRE(rsrc[c] >= 0 || !written(nd.resid, 2LL * m * calls[c].k),
+                  "projection %d: the residual is memory the chain writes (only an earlier stage's resid_out can "
+                  "be)", c);
+      QLX_REQUIRE(!nd.resid_out || !sx_overlaps(nd.resid_out, 2LL * m * calls[c].k, nd.resid, 2LL * m * calls[c].k),
+                  "projection %d: resid_out overlaps the residual", c);
+      continue;
+    }
     for (int j = 0; j < c; ++j)
       if (calls[c].x == calls[j].y && calls[c].k <= nout(j)) {
         src[c] = j;
@@ -778,10 +998,9 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, vo
         break;
       }
     if (src[c] < 0)
-      for (int j = 0; j < ncalls; ++j)
-        QLX_REQUIRE(!sx_overlaps(calls[c].x, 2LL * m * calls[c].k, calls[j].y, 2LL * m * nout(j)),
-                    "projection %d reads memory that projection %d writes (only the whole output of an "
-                    "earlier projection can be an input)", c, j);
+      QLX_REQUIRE(!written(calls[c].x, 2LL * m * calls[c].k),
+                  "projection %d reads memory the chain writes (only the whole output of an earlier projection "
+                  "can be an input)", c);
   }
   int dev = 0, P = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -839,6 +1058,7 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, vo
   L.sws_off = off;
   off += 2 * kSxMaxTilesPerEntry * 16 * 4;
   L.stage_bytes = (sx_stage_bytes(fi, m, kmax) + 15) & ~15;
+  if (knorm > 0) L.stage_bytes = std::max(L.stage_bytes, sx_css_offset(fi, m, knorm) + kSxCssBytes);
   L.stage_off[0] = off;
   L.stage_off[1] = off + L.stage_bytes;
   off += 2 * L.stage_bytes;
@@ -864,12 +1084,17 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, vo
   }
   // Arena: published outputs.
   long long aoff = 0;
-  std::vector<long long> wire_off(ncalls, -1);
-  for (int c = 0; c < ncalls; ++c)
+  std::vector<long long> wire_off(ncalls, -1), rwire_off(ncalls, -1);
+  for (int c = 0; c < ncalls; ++c) {
     if (published[c]) {
       wire_off[c] = aoff;
       aoff += ((8LL * m * (nout(c) / 2)) + 255) & ~255LL;
     }
+    if (rpublished[c]) {
+      rwire_off[c] = aoff;
+      aoff += ((8LL * m * (calls[c].k / 2)) + 255) & ~255LL;
+    }
+  }
   // Descriptor image.
   SxHeader hd = {};
   hd.ncalls = ncalls;
@@ -914,6 +1139,19 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, vo
       pj.xpitch = nout(src[c]);
     } else {
       pj.x = q.x;
+    }
+    if (normed(c)) {
+      const qlx_norm_input& nd = norms[c];
+      pj.norm = 1;
+      pj.nw = nd.norm_w;
+      pj.eps = nd.eps;
+      if (rsrc[c] >= 0)
+        pj.rwire = reinterpret_cast<const uint64_t*>(base + rwire_off[rsrc[c]]);
+      else
+        pj.rmem = nd.resid;
+      pj.rout = nd.resid_out;
+      pj.nout = nd.normed_out;
+      pj.rwire_out = rwire_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + rwire_off[c]) : nullptr;
     }
     memcpy(out + hd.proj_off + c * sizeof(SxProj), &pj, sizeof(pj));
     SxComp cp = {};

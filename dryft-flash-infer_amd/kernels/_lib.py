@@ -48,6 +48,12 @@ class StackLaunch(ctypes.Structure):
                                             "pieces")]
 
 
+class NormInput(ctypes.Structure):
+    _fields_ = [("resid", ctypes.c_void_p), ("delta", ctypes.c_void_p), ("norm_w", ctypes.c_void_p),
+                ("resid_out", ctypes.c_void_p), ("normed_out", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("pad", ctypes.c_int)]
+
+
 class StreamLaunch(ctypes.Structure):
     """``qlx_stream_launch``: grid, LDS bytes, ring lines per compute wave, and the kernel's
     LDS layout (opaque words)."""
@@ -92,12 +98,14 @@ SIGNATURES = {
     "qlx_residual_planes": ([_P, _P, _P, _LL, _I, _P], _I),
     "qlx_add_rms_norm": ([_P, _P, _P, _I, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_add_norm_quant_int8": ([_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "qlx_add_norm_quant_fp8": ([_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
     "qlx_stack_desc_size": ([], _I),
     "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
                          ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
-    "qlx_stream_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _P, _PLL, _P, _PLL, ctypes.POINTER(StreamLaunch)],
+    "qlx_stream_build": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _P, _PLL, _P, _PLL,
+                          ctypes.POINTER(StreamLaunch)],
                          _I),
     "qlx_stream_run": ([_I, _P, ctypes.POINTER(StreamLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),

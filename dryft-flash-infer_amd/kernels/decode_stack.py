@@ -144,14 +144,60 @@ class DecodeStack:
 
 class StreamStack(DecodeStack):
     """The same chain on the stream executor (``qlx_stream_build`` / ``qlx_stream_run``): in
-    each workgroup four compute waves stream every projection's weights into LDS rings with
+    each workgroup eight compute waves stream every projection's weights into LDS rings with
     direct-to-LDS loads, running ahead across projections, while four IO waves poll, stage,
     reduce and publish, so no poll ever waits behind a weight load. Each projection's tiles go
-    whole to workgroups; a tile's output is the fixed-order sum of four K-interleaved partial
-    sums (deterministic). ``add`` takes the same arguments (``kw`` is ignored)."""
+    whole to workgroups; a tile's output is the fixed-order sum of eight K-interleaved partial
+    sums (deterministic). ``add`` takes the same arguments (``kw`` is ignored).
+
+    ``add_normed`` appends a projection whose input is a residual add + RMSNorm stage, so a
+    chain can be a whole decode layer's linear path:
+
+        chain.add_normed(qkv, h_in, y_qkv, w_in, eps, resid_out=h0)          # rmsnorm(h_in)
+        chain.add(o, y_qkv[:, :4096], y_o)
+        chain.add_normed(gate_up, h0, y_act, w_post, eps, delta=y_o, resid_out=h1, swiglu=True)
+        chain.add(down, y_act, y_down)
+        chain.add_normed(next_qkv, h1, ..., delta=y_down, resid_out=h2)      # the next layer
+    """
 
     def __init__(self, fmt, m):
         super().__init__(fmt, m)
+        self.norms = []
+
+    def add(self, weight, x, y, swiglu=False, kw=0):
+        super().add(weight, x, y, swiglu, kw)
+        self.norms.append(_lib.NormInput())
+        return self
+
+    def add_normed(self, weight, resid, y, norm_w, eps, delta=None, resid_out=None, normed_out=None,
+                   swiglu=False):
+        """Append a projection of bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
+        r = bf16(resid + delta) (r = resid without delta). ``resid`` is memory the chain does not
+        write or an earlier stage's ``resid_out``; ``delta`` the output tensor of an earlier
+        projection; ``resid_out`` / ``normed_out`` (optional) receive r and the normed input.
+        FP8 W8A8 quantizes the normed input per token inside the same stage."""
+        if not isinstance(weight, Tiled) or weight.fmt != self.fmt:
+            raise ValueError(f"the chain takes {self.fmt} weights in tile layout (qlinear.prepare)")
+        shape = (self.m, weight.k)
+        tensors = [resid, norm_w] + [t for t in (delta, resid_out, normed_out) if t is not None]
+        _lib.require_device(weight.weight, weight.scale, y, *tensors)
+        for name, t in (("resid", resid), ("delta", delta), ("resid_out", resid_out), ("normed_out", normed_out)):
+            if t is not None and (t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous bf16 [{self.m}, {weight.k}] tensor")
+        if norm_w.dtype != torch.bfloat16 or tuple(norm_w.shape) != (weight.k,):
+            raise ValueError(f"norm_w must be bf16 [{weight.k}]")
+        out_n = weight.rows // 2 if swiglu else weight.rows
+        if y.dtype != torch.bfloat16 or tuple(y.shape) != (self.m, out_n):
+            raise ValueError(f"y must be bf16 [{self.m}, {out_n}]")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self.calls.append(_lib.StackCall(weight.weight.data_ptr(), weight.scale.data_ptr(), None, y.data_ptr(),
+                                         weight.rows, weight.k, _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, 0))
+        self.norms.append(_lib.NormInput(ptr(resid), ptr(delta), ptr(norm_w), ptr(resid_out), ptr(normed_out),
+                                         float(eps), 0))
+        self._keep += [weight, resid, y]
+        self._extra = getattr(self, "_extra", []) + tensors
+        self.desc = None
+        return self
 
     def build(self):
         if not self.calls:
@@ -159,16 +205,18 @@ class StreamStack(DecodeStack):
         device = self._keep[0].weight.device
         lib = _lib.lib()
         arr = (_lib.StackCall * len(self.calls))(*self.calls)
+        norms = (_lib.NormInput * len(self.norms))(*self.norms)
         fmt = _FMTS[self.fmt]
         desc_bytes, arena_bytes, launch = ctypes.c_longlong(0), ctypes.c_longlong(0), _lib.StreamLaunch()
         with torch.cuda.device(device):
-            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), None, desc_bytes, None, arena_bytes,
-                                            launch), "qlx_stream_build")
+            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), norms, None, desc_bytes, None,
+                                            arena_bytes, launch), "qlx_stream_build")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
             self.error = torch.zeros(1, dtype=torch.int32, device=device)
             host = torch.zeros(desc_bytes.value, dtype=torch.uint8)
-            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), ctypes.c_void_p(host.data_ptr()),
-                                            desc_bytes, _lib.ptr(self.arena), arena_bytes, launch), "qlx_stream_build")
+            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), norms,
+                                            ctypes.c_void_p(host.data_ptr()), desc_bytes, _lib.ptr(self.arena),
+                                            arena_bytes, launch), "qlx_stream_build")
             self.desc = host.to(device)
         self.launch = launch
         self.grid, self.lds = launch.grid, launch.lds_bytes

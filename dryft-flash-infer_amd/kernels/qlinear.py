@@ -261,6 +261,51 @@ def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False, pre_quan
                        (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
+def linear_fp8_w8a8_quantized(xq, sx, packed, config=None, planes=False, swiglu=False):
+    """FP8 W8A8 linear of an activation quantized beforehand: e4m3 codes ``xq`` [m, k] with
+    fp32 per-token scales ``sx`` [m] (``quantize_fp8_activation`` or ``add_norm_quant_fp8``)."""
+    q, s, n, k, tiled = _unpack(packed, "fp8")
+    if xq.ndim != 2 or xq.shape[1] != k or xq.element_size() != 1:
+        raise ValueError("codes must be one byte each, [m, k] with k the weight's width")
+    if sx.dtype != torch.float32 or sx.numel() != xq.shape[0]:
+        raise ValueError("token scales are fp32 [m]")
+    if not 1 <= xq.shape[0] <= 64:
+        raise ValueError(f"batch {xq.shape[0]} exceeds 64 rows")
+    _lib.require_device(q, s, xq, sx)
+    return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8_q", xq, n, k,
+                       (_lib.ptr(q), _lib.ptr(s), _lib.ptr(xq), _lib.ptr(sx)), (tiled,),
+                       mode=_mode(swiglu, planes), config=config)
+
+
+def add_norm_quant_fp8(residual, delta, weight, eps, keep_normed=False):
+    """Residual + RMSNorm with the reference's bf16 casts, then the FP8 per-token activation of
+    the normed row, in one launch: the FP8 W8A8 counterpart of ``cuda_int8.add_norm_quant``
+    (engine/kernels/cuda_int8.py:17-55). ``delta`` is bf16 [m, n], fp32 planes [splits, m, n] or
+    None (plain RMSNorm). Returns (residual out or None, codes e4m3 [m, n], scales fp32 [m]) and,
+    with ``keep_normed``, the normed bf16 row too."""
+    _bf16_2d(residual, "residual")
+    m, n = residual.shape
+    if n % 8:
+        raise ValueError(f"width {n} is not a multiple of 8")
+    planes = delta is not None and delta.ndim == 3
+    if planes and delta.dtype != torch.float32:
+        raise ValueError("planes are fp32 [splits, rows, n]")
+    if delta is not None and tuple(delta.shape[-2:]) != (m, n):
+        raise ValueError("delta does not match the residual")
+    _lib.require_device(residual, weight, *(() if delta is None else (delta,)))
+    res = torch.empty_like(residual) if delta is not None else None
+    normed = torch.empty_like(residual) if keep_normed else None
+    code = torch.empty((m, n), dtype=torch.uint8, device=residual.device)
+    scale = torch.empty(m, dtype=torch.float32, device=residual.device)
+    _lib.call("qlx_add_norm_quant_fp8", _lib.ptr(residual),
+              None if (delta is None or planes) else _lib.ptr(delta), _lib.ptr(delta) if planes else None,
+              delta.shape[0] if planes else 0, _lib.ptr(weight), None if res is None else _lib.ptr(res),
+              None if normed is None else _lib.ptr(normed), _lib.ptr(code), _lib.ptr(scale), m, n, float(eps),
+              _lib.stream(residual.device))
+    out = (res, code.view(torch.float8_e4m3fn), scale)
+    return out + (normed,) if keep_normed else out
+
+
 def splits(fmt, m, n, k, config=None, swiglu=False):
     """How many fp32 planes a linear of this shape and config reduces."""
     return _linear.splits_for(fmt, _mode(swiglu), m, n, k, config)

@@ -249,6 +249,15 @@ int qlx_add_norm_quant_int8(const void* x, const void* delta, const float* plane
                             const void* w, void* res, void* q, float* q_scale, int rows, int n, float eps,
                             void* stream);
 
+/* Residual + RMSNorm + FP8 per-token activation quantize in one launch: r = bf16(x + delta)
+ * (delta bf16 [rows][n], or fp32 planes [splits][rows][n] reduced in plane order; both NULL: r = x,
+ * res not written), y = bf16(bf16(r * rsqrt(mean(r^2) + eps)) * w) (written if y != NULL), then
+ * scale[row] = max(amax(y)/448, 1e-12) and code = e4m3(y / scale) as qlx_quantize_fp8_act gives
+ * for y. The FP8 W8A8 counterpart of cuda_int8.add_norm_quant (engine/kernels/cuda_int8.py:17-55):
+ * the next projection's activation arrives quantized (qlx_linear_fp8_w8a8_q). */
+int qlx_add_norm_quant_fp8(const void* x, const void* delta, const float* planes, int splits, const void* w,
+                           void* res, void* y, void* code, float* scale, int rows, int n, float eps, void* stream);
+
 /* out[r][i] = bf16(bf16(silu(g)) * u) from bf16 gate_up [rows][2I] or fp32 planes
  * [splits][rows][2I] (g and u rounded to bf16 after the plane sum). Replaces swiglu.swiglu,
  * swiglu.swiglu_partials, cuda_small.swiglu_partials (engine/kernels/swiglu.py:12-64,
@@ -318,6 +327,24 @@ int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch*
 
 /* ---- decode-step stream executor ---------------------------------------------------- */
 
+/* Residual add + RMSNorm input stage of a stream-executor projection (the decode step's fused
+ * residual consumer, engine/kernels/norm.py:125-139 with reference.py:13-28's casts). With norm_w
+ * set, projection c's input is y = bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
+ * r = bf16(resid + delta) (r = resid when delta is NULL), and calls[c].x must be NULL. resid is
+ * bf16 [m][k] in memory the chain does not write, or the resid_out of an earlier stage; delta is
+ * NULL or the whole output y of an earlier projection. resid_out (optional) receives r and
+ * normed_out (optional) y. For FP8 W8A8 the staged y is quantized per token like any input: the
+ * norm -> FP8 activation quantize is fused. A stage takes k a multiple of 512 and m * k <= 6144 (m <= 2). */
+typedef struct qlx_norm_input {
+  const void* resid;
+  const void* delta;
+  const void* norm_w;
+  void* resid_out;
+  void* normed_out;
+  float eps;
+  int pad;
+} qlx_norm_input;
+
 /* Launch configuration of a stream-executor chain, filled by qlx_stream_build. */
 typedef struct qlx_stream_launch {
   int grid;          /* workgroups, one per CU (cooperative launch) */
@@ -339,8 +366,9 @@ typedef struct qlx_stream_launch {
  * *desc_bytes), to be copied to device memory as is; published outputs live in `arena`
  * (*arena_bytes, zeroed once before the first run). Same replacement as qlx_stack_build
  * (engine/kernels/cuda_fp8.py:47-50, 150-169; engine/kernels/cuda_jit.py:218-262). */
-int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, void* desc, long long* desc_bytes,
-                     void* arena, long long* arena_bytes, qlx_stream_launch* launch);
+int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                     void* desc, long long* desc_bytes, void* arena, long long* arena_bytes,
+                     qlx_stream_launch* launch);
 
 /* Run a stream-executor chain (device copy of the descriptor image); epoch, error and budget
  * as for qlx_stack_run: a new nonzero low-16-bit epoch per run on one arena, runs sharing an

@@ -89,6 +89,41 @@ def test_fp8_quantizer_fast_path_is_exact_on_every_input():
     assert c[0] == 0, [hex(v & (2 ** 64 - 1)) for v in c[2:2 + min(c[1], 8)]]
 
 
+@pytest.mark.parametrize("m", [1, 3, 16])
+def test_add_norm_quant_fp8_matches_oracle(m):
+    """Fused residual + RMSNorm + FP8 per-token quantize: residual, normed row, codes and scales
+    bit-exact against the oracle (add_rms_norm then quantize_fp8_activation), for a bf16 delta,
+    fp32 planes and no delta; the codes feed the FP8 GEMM exactly as its own prologue would."""
+    g = torch.Generator().manual_seed(101 + m)
+    n = 2560
+    x = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16)
+    d = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    planes = torch.randn(4, m, n, generator=g)
+    xd, wd = x.to(DEV), w.to(DEV)
+    for kind, delta in (("bf16", d), ("planes", planes), ("none", None)):
+        res, code, scale, normed = qlinear.add_norm_quant_fp8(
+            xd, None if delta is None else delta.to(DEV), wd, 1e-6, keep_normed=True)
+        if kind == "bf16":
+            o_res, o_norm = O.add_rms_norm(bits16(x), bits16(d), bits16(w), 1e-6)
+        elif kind == "planes":
+            o_res, o_norm = O.add_rms_norm_partials(bits16(x), planes.numpy(), bits16(w), 1e-6)
+        else:
+            o_res, o_norm = None, O.rms_norm(bits16(x), bits16(w), 1e-6)
+        if o_res is None:
+            assert res is None
+        else:
+            assert np.array_equal(bits16(res), o_res), (kind, "residual")
+        assert np.array_equal(bits16(normed), o_norm), (kind, "normed")
+        oq, os_ = O.quantize_fp8_activation(o_norm)
+        assert np.array_equal(code.view(torch.uint8).cpu().numpy(), oq), (kind, "codes")
+        assert np.array_equal(scale.cpu().numpy().view(np.uint32), os_.view(np.uint32)), (kind, "scales")
+    wq = qlinear.quantize_fp8(weights(1024, n, 7, edge=False).to(DEV))
+    pre = qlinear.linear_fp8_w8a8_quantized(code, scale, wq)
+    fused = qlinear.linear_fp8_w8a8(normed, wq, pre_quantize=False)
+    assert torch.equal(pre, fused), "pre-quantized codes = the GEMM's own prologue"
+
+
 @pytest.mark.parametrize("m,k", [(1, 2560), (3, 9728), (16, 256), (64, 4096)])
 def test_quantize_fp8_activation_bit_exact(m, k):
     x = acts(m, k, 11 + m)

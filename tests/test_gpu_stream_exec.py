@@ -8,9 +8,11 @@ K-interleaved partials added in wave order), against the CPU oracle to the north
 relative L2 bound, and for determinism.
 """
 
+import numpy as np
 import pytest
 import torch
 
+import oracle as O
 from kernels import qlinear
 from kernels.decode_stack import StreamStack
 from test_gpu_decode_stack import CHAIN, DEV, QWEN_LAYER, bits16, check_against_single_calls, oracle_check, rand, \
@@ -90,3 +92,89 @@ def test_stream_bounded_wait_gives_up_and_recovers():
     torch.cuda.synchronize()
     assert not chain.failed()
     check_against_single_calls("fp8", bufs, weights, "stream after reset")
+
+
+def build_norm_chain(fmt, m, seed, layers=2):
+    """`layers` Qwen3-4B layers with their residual adds and RMSNorms inside the chain, then a
+    final norm into a small head: qkv <- rmsnorm(h); o; gate_up <- rmsnorm(h + o); down; the next
+    qkv <- rmsnorm(h + o + down); ..."""
+    quant = qlinear.FORMATS[fmt][0]
+    chain = StreamStack(fmt, m)
+    bufs = {"h_in": rand((m, 2560), seed).to(DEV)}
+    weights, raw, stages = {}, {}, []
+    eps = 1e-6
+
+    def proj(name, n, k, idx):
+        packed = quant(rand((n, k), seed + 10 + idx, std=0.02).to(DEV))
+        raw[name] = packed
+        weights[name] = qlinear.prepare(packed)
+
+    def out(name, n):
+        bufs[name] = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        return bufs[name]
+
+    def norm_w(name, idx):
+        g = torch.Generator().manual_seed(seed + 500 + idx)
+        bufs[name] = (1.0 + 0.1 * torch.randn(2560, generator=g)).to(torch.bfloat16).to(DEV)
+        return bufs[name]
+
+    resid, delta = "h_in", None
+    for L in range(layers):
+        for i, (n, k) in enumerate(((6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728))):
+            proj(f"{('qkv', 'o', 'gu', 'dn')[i]}{L}", n, k, 4 * L + i)
+        chain.add_normed(weights[f"qkv{L}"], bufs[resid], out(f"qkv{L}", 6144), norm_w(f"win{L}", 2 * L), eps,
+                         delta=None if delta is None else bufs[delta], resid_out=out(f"h0_{L}", 2560),
+                         normed_out=out(f"nq{L}", 2560))
+        stages.append((resid, delta, f"win{L}", f"h0_{L}", f"nq{L}", f"qkv{L}", False))
+        chain.add(weights[f"o{L}"], bufs[f"qkv{L}"][:, :4096], out(f"o{L}", 2560))
+        chain.add_normed(weights[f"gu{L}"], bufs[f"h0_{L}"], out(f"gu{L}", 9728), norm_w(f"wpost{L}", 2 * L + 1), eps,
+                         delta=bufs[f"o{L}"], resid_out=out(f"h1_{L}", 2560), normed_out=out(f"ng{L}", 2560),
+                         swiglu=True)
+        stages.append((f"h0_{L}", f"o{L}", f"wpost{L}", f"h1_{L}", f"ng{L}", f"gu{L}", True))
+        chain.add(weights[f"dn{L}"], bufs[f"gu{L}"], out(f"dn{L}", 2560))
+        resid, delta = f"h1_{L}", f"dn{L}"
+    proj("head", 1024, 2560, 99)
+    chain.add_normed(weights["head"], bufs[resid], out("head", 1024), norm_w("wfin", 99), eps, delta=bufs[delta],
+                     resid_out=out("h_fin", 2560), normed_out=out("nfin", 2560))
+    stages.append((resid, delta, "wfin", "h_fin", "nfin", "head", False))
+    chain.build()
+    return chain, bufs, weights, raw, stages
+
+
+@pytest.mark.parametrize("fmt,m", [("fp8", 1), ("w4a16", 1), ("w8a16", 1), ("fp8", 2)])
+def test_stream_decode_layers_with_residual_and_norm(fmt, m):
+    """Residual add + RMSNorm (+ FP8 per-token quantize) as input stages of the stream executor:
+    every stage's residual and normed input are bit-exact against the oracle on the chain's own
+    inputs, every projection agrees with the single-call linear on its stage's normed input (and
+    o / down with the oracle), and two runs are bitwise equal."""
+    print(f"stream exec norm chain {fmt} m={m}", flush=True)
+    chain, bufs, weights, raw, stages = build_norm_chain(fmt, m, 700 + m)
+    linear = qlinear.FORMATS[fmt][1]
+    for run in range(2):
+        if run:
+            bufs["h_in"].copy_(rand((m, 2560), 7000 + m).to(DEV))
+        chain.run()
+        torch.cuda.synchronize()
+        assert not chain.failed(), chain.failed_waits()
+        snap = {k: v.clone() for k, v in bufs.items()}
+        chain.run()
+        torch.cuda.synchronize()
+        assert not chain.failed(), chain.failed_waits()
+        for k, v in bufs.items():
+            assert torch.equal(v, snap[k]), (fmt, m, run, k, "deterministic")
+        for resid, delta, w, r_out, n_out, y, sw in stages:
+            if delta is None:
+                o_r, o_n = bits16(bufs[resid]), O.rms_norm(bits16(bufs[resid]), bits16(bufs[w]), 1e-6)
+            else:
+                o_r, o_n = O.add_rms_norm(bits16(bufs[resid]), bits16(bufs[delta]), bits16(bufs[w]), 1e-6)
+            assert np.array_equal(bits16(bufs[r_out]), o_r), (fmt, m, run, r_out, "residual")
+            assert np.array_equal(bits16(bufs[n_out]), o_n), (fmt, m, run, n_out, "normed input")
+            want = linear(bufs[n_out], weights[y], swiglu=sw).float()
+            got = bufs[y].float()
+            rowmax = want.abs().amax(dim=1, keepdim=True)
+            tol = (2.0 ** -6 if sw else 2.0 ** -7) * want.abs() + 2.0 ** -9 * rowmax
+            assert ((got - want).abs() > tol).sum().item() == 0, (fmt, m, run, y)
+        for L in range(2):
+            assert oracle_check(fmt, bits16(bufs[f"qkv{L}"][:, :4096].contiguous()), raw[f"o{L}"],
+                                bufs[f"o{L}"]) < 1e-2
+            assert oracle_check(fmt, bits16(bufs[f"gu{L}"]), raw[f"dn{L}"], bufs[f"dn{L}"]) < 1e-2
