@@ -59,7 +59,7 @@ __host__ __device__ inline SkinnyLayout skinny_layout(int m, int waves, int rw) 
 // x chunks (16 bytes, 8 values) of one K step that each thread stages: 16 MT rows.
 template <class F, int WAVES, int MT>
 struct SkinnyStage {
-  static constexpr int PER_ROW = F::KSTEP / 8;
+  static constexpr int PER_ROW = F::KSTEP * F::XBYTES / 16;
   static constexpr int CHUNKS = 16 * MT * PER_ROW;
   static constexpr int MAX = (CHUNKS + WAVES * 64 - 1) / (WAVES * 64);
 };
@@ -113,8 +113,28 @@ __device__ __forceinline__ void skinny_step(f32x4 (&acc)[RW][MT], const uint4 (&
           for (int i = 0; i < 4; ++i) acc[r][mt][i] = fmaf(s4[i], tmp[r][mt][i] - tb[mt][i], acc[r][mt][i]);
       }
     }
+  } else if constexpr (std::is_same<F, FmtFP8>::value) {
+    // FP8 W8A8: e4m3 weights against the e4m3 codes of the activation (quantized per token
+    // beforehand); both scales come in the epilogue. Chunk bytes 64 j + 16 c of a row hold the
+    // codes of k 64 j + 16 c .., as the weight bytes of lane 16 c + r.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kb = j * 64 + (lane >> 4) * 16;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(ch + xoff[mt] + kb);
+        const long b0 = (long)(((unsigned long)bv.y << 32) | bv.x), b1 = (long)(((unsigned long)bv.w << 32) | bv.z);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const long a0 = (long)(((unsigned long)c[r][j].y << 32) | c[r][j].x);
+          const long a1 = (long)(((unsigned long)c[r][j].w << 32) | c[r][j].z);
+          acc[r][mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a0, b0, acc[r][mt], 0, 0, 0);
+          acc[r][mt] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a1, b1, acc[r][mt], 0, 0, 0);
+        }
+      }
+    }
   } else {
-    static_assert(std::is_same<F, FmtW8>::value, "skinny_step: W4A16 or W8A16");
+    static_assert(std::is_same<F, FmtW8>::value, "skinny_step: W4A16, W8A16 or FP8 W8A8");
     const uint4 ab = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
     f32x4 tmp[RW][MT], tb[MT];
 #pragma unroll
@@ -194,7 +214,8 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
     // (ids 8 apart share an XCD, so the second block finds the weights in that XCD's L2)
     const int b = (bid >> 3) & 1;
     bid = 8 * (bid >> 4) + (bid & 7);
-    a.x = static_cast<const char*>(a.x) + (size_t)b * 32 * a.k * 2;
+    a.x = static_cast<const char*>(a.x) + (size_t)b * 32 * a.k * F::XBYTES;
+    if (a.xs) a.xs += b * 32;
     a.y = static_cast<char*>(a.y) + (size_t)b * 32 * (SW ? a.half : a.n) * 2;
     a.work += (size_t)b * 32 * a.n;  // K-slice planes keep the whole batch's rows (a.pm)
     a.m = min(32, a.m - 32 * b);
@@ -235,14 +256,16 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   // step is a scalar offset), and rows past m read as zeros (the resource's bounds check).
   constexpr int XROWS = WAVES * 64 / SPR;
   static_assert(WAVES * 64 % SPR == 0, "a thread's chunks share their column");
-  const __amdgpu_buffer_rsrc_t xr = skinny_rsrc(a.x, (unsigned)a.m * (unsigned)a.k * 2u);
+  // (FP8: the e4m3 codes, one byte per value.)
+  constexpr unsigned XB = F::XBYTES;
+  const __amdgpu_buffer_rsrc_t xr = skinny_rsrc(a.x, (unsigned)a.m * (unsigned)a.k * XB);
   const int xrow0 = threadIdx.x / SPR, xcol = threadIdx.x - xrow0 * SPR;
-  const unsigned xoff0 = ((unsigned)xrow0 * (unsigned)a.k + (unsigned)xcol * 8u) * 2u;
+  const unsigned xoff0 = (unsigned)xrow0 * (unsigned)a.k * XB + (unsigned)xcol * 16u;
   auto fetch_x = [&](int step, Staged& st) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < SMAX; ++u) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(xoff0 + (unsigned)step * (F::KSTEP * 2)),
-                                                            u * XROWS * a.k * 2, 0);
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(xoff0 + (unsigned)step * (F::KSTEP * XB)),
+                                                            u * XROWS * a.k * (int)XB, 0);
       st.x[u] = uint4{v[0], v[1], v[2], v[3]};
     }
     if constexpr (F::NSC > 0) {
@@ -261,8 +284,12 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
 #pragma unroll
     for (int u = 0; u < SMAX; ++u) {
       const int mm = xrow0 + u * XROWS;  // rows past m hold zeros and are never read
-      if (CHUNKS % (WAVES * 64) == 0 || mm < 16 * MT)
-        *reinterpret_cast<uint4*>(ch + mm * L.xstride + xcol * 16) = F::order(st.x[u]);
+      if (CHUNKS % (WAVES * 64) == 0 || mm < 16 * MT) {
+        if constexpr (std::is_same<F, FmtFP8>::value)
+          *reinterpret_cast<uint4*>(ch + mm * L.xstride + xcol * 16) = st.x[u];  // codes in k order
+        else
+          *reinterpret_cast<uint4*>(ch + mm * L.xstride + xcol * 16) = F::order(st.x[u]);
+      }
     }
     if constexpr (F::NSC > 0) {
       float* sc = reinterpret_cast<float*>(ch + L.off_sc);
@@ -338,6 +365,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
         // per-channel formats scale once here; group formats scaled every group in the step
         v[i] = acc[r][mt][i];
         if constexpr (F::NSC == 0) v[i] *= bf2f(gmem(ws)[weight_row(a, tile[r], r0 + i)]);
+        if constexpr (std::is_same<F, FmtFP8>::value) v[i] *= a.xs[min(mm, a.m - 1)];  // the token's scale
       }
       if (a.splits > 1) {  // fp32 plane s, rows in natural order
         if (mm < a.m) {
@@ -461,8 +489,12 @@ hipError_t skinny_mt(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStrea
 // Waves, tiles per wave and K slices: 4 waves per workgroup, one tile per wave (two, which reuse
 // each activation fragment read from LDS twice, measured no faster on any config-4 shape: gate_up
 // 12.6 vs 12.7 us at 16 tokens, 17.4 vs 16.6 at 32; down 13.1 vs 11.0 at 16), and K slices until
-// about 240 workgroups (gate_up: 304 whole-K workgroups; down: 40 row groups x 6 slices), each
-// slice at least 2 steps. Measured on the Qwen3 config-4 shapes over every slice count.
+// about 240 workgroups (down: 40 row groups x 6 slices), each slice at least 2 steps. A shape with
+// row groups for at least 256 whole-K workgroups (gate_up: 1216 tiles) at up to 32 tokens runs 8
+// waves per workgroup instead, one per CU: every staged activation chunk then serves 8 tiles, half
+// the activation reads from L2 (gate_up 12.7 -> 11.7 us at 16 tokens, 17.1 -> 15.7 at 32; taking
+// a tile's steps two waves at a time, which doubles them, measured 13.6 and 21.6). Measured on the
+// Qwen3 config-4 shapes over every slice count, waves per workgroup and tiles per wave.
 template <class F>
 void skinny_plan(int m, int n, int k, int* waves, int* rw, int* splits) {
   const int nsteps = k / F::KSTEP;
@@ -476,6 +508,7 @@ void skinny_plan(int m, int n, int k, int* waves, int* rw, int* splits) {
   if (s > most) s = most;
   if (s < 1) s = 1;
   *splits = s;
+  if (s == 1 && m <= 32 && groups >= 256) *waves = 8;
 }
 
 template <class F>
@@ -567,8 +600,9 @@ extern "C" {
 
 int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan) {
   QLX_REQUIRE(plan != nullptr, "plan is NULL");
-  QLX_REQUIRE(fmt == QLX_FMT_W4A16 || fmt == QLX_FMT_W8A16, "the skinny GEMM serves W4A16 and W8A16 (format %d)", fmt);
-  const int kstep = fmt == QLX_FMT_W4A16 ? FmtW4::KSTEP : FmtW8::KSTEP;
+  QLX_REQUIRE(fmt == QLX_FMT_W4A16 || fmt == QLX_FMT_W8A16 || fmt == QLX_FMT_FP8,
+              "the skinny GEMM serves W4A16, W8A16 and FP8 W8A8 (format %d)", fmt);
+  const int kstep = fmt == QLX_FMT_W4A16 ? FmtW4::KSTEP : (fmt == QLX_FMT_W8A16 ? FmtW8::KSTEP : FmtFP8::KSTEP);
   QLX_REQUIRE(m >= 1 && m <= 64 && n >= 16 && n % 16 == 0 && k >= kstep && k % kstep == 0,
               "shape m=%d n=%d k=%d does not fit format %d", m, n, k, fmt);
   qlx_plan p = {};
@@ -576,8 +610,10 @@ int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan) {
   p.kw = 1;
   if (fmt == QLX_FMT_W4A16)
     skinny_plan<FmtW4>(m, n, k, &p.waves, &p.rw, &p.splits);
-  else
+  else if (fmt == QLX_FMT_W8A16)
     skinny_plan<FmtW8>(m, n, k, &p.waves, &p.rw, &p.splits);
+  else
+    skinny_plan<FmtFP8>(m, n, k, &p.waves, &p.rw, &p.splits);
   const int nsteps = k / kstep;
   const int sps = (nsteps + p.splits - 1) / p.splits;
   p.splits = (nsteps + sps - 1) / sps;
@@ -596,7 +632,20 @@ int qlx_linear_skinny(int fmt, const void* w, const void* w_scale, const void* x
   QLX_REQUIRE(plan != nullptr, "linear_skinny: plan is NULL");
   if (fmt == QLX_FMT_W4A16) return skinny_run<FmtW4>("linear_skinny", a, m, n, k, plan->mode, plan, stream);
   if (fmt == QLX_FMT_W8A16) return skinny_run<FmtW8>("linear_skinny", a, m, n, k, plan->mode, plan, stream);
-  QLX_REQUIRE(false, "the skinny GEMM serves W4A16 and W8A16 (format %d)", fmt);
+  QLX_REQUIRE(false, "qlx_linear_skinny serves W4A16 and W8A16 (format %d; FP8: qlx_linear_skinny_fp8)", fmt);
+}
+
+int qlx_linear_skinny_fp8(const void* w, const void* w_scale, const void* x_code, const float* x_scale, void* y,
+                          int m, int n, int k, const qlx_plan* plan, void* stream) {
+  GemmArgs a = {};
+  a.w = w;
+  a.ws = w_scale;
+  a.x = x_code;
+  a.xs = x_scale;
+  a.y = y;
+  QLX_REQUIRE(w && w_scale && x_code && x_scale && y, "linear_skinny_fp8: NULL pointer");
+  QLX_REQUIRE(plan != nullptr, "linear_skinny_fp8: plan is NULL");
+  return skinny_run<FmtFP8>("linear_skinny_fp8", a, m, n, k, plan->mode, plan, stream);
 }
 
 }  // extern "C"

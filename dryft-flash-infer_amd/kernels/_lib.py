@@ -88,6 +88,7 @@ SIGNATURES = {
     "qlx_plan_skinny": ([_I, _I, _I, _I, _I, _PLAN], _I),
     "qlx_linear_skinny": ([_I, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_skinny_noalloc": ([_I, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "qlx_linear_skinny_fp8": ([_P, _P, _P, _P, _P, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8_w8a8_q": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_fp8_w8a8": ([_P, _P, _P, _P, _I, _I, _I, _I, _PLAN, _P], _I),
     "qlx_linear_ref": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _PLAN, _P], _I),

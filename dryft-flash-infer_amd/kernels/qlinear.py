@@ -242,14 +242,44 @@ def linear_w4a16(x, packed, config=None, planes=False, swiglu=False, skinny=None
 FP8_QUANTIZE_FROM = 2
 
 
-def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False, pre_quantize=None):
+def _skinny_fp8(q, s, xq, sx, n, k, swiglu, fused_reduce=None):
+    """The FP8 W8A8 skinny GEMM (``qlx_linear_skinny_fp8``) on codes quantized beforehand; K
+    slices reduced as in ``_skinny``."""
+    m = xq.shape[0]
+    if fused_reduce is None:
+        fused_reduce = m <= 32
+    mode = _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16
+    plan = _lib.Plan()
+    _lib.check(_lib.lib().qlx_plan_skinny(_lib.FMT_FP8, mode, m, n, k, plan), "plan_skinny")
+    out = torch.empty((m, n // 2 if swiglu else n), dtype=torch.bfloat16, device=xq.device)
+    work = None
+    if plan.splits > 1:
+        work = torch.empty((plan.splits, m, n), dtype=torch.float32, device=xq.device)
+        plan.workspace = work.data_ptr()
+        if fused_reduce:
+            plan.tickets = _lib.tickets(xq.device, n // 16).data_ptr()
+    _lib.call("qlx_linear_skinny_fp8", _lib.ptr(q), _lib.ptr(s), _lib.ptr(xq), _lib.ptr(sx), _lib.ptr(out), m, n, k,
+              ctypes.byref(plan), _lib.stream(xq.device))
+    return out
+
+
+def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False, pre_quantize=None, skinny=None):
     """``(x_q s_x) @ (W_q s_w).T`` with the activation quantized per token (``pre_quantize``:
-    None = by its own kernel from 2 tokens, else inside the GEMM; the codes are the same)."""
+    None = by its own kernel from 2 tokens, else inside the GEMM; the codes are the same).
+    ``skinny`` (None: from 9 tokens on tile-layout weights) runs the skinny GEMM on the
+    quantized codes; False forces the decode kernel."""
     q, s, n, k, tiled = _unpack(packed, "fp8")
     _check_x(x, k)
     _lib.require_device(q, s)
     if s.numel() != n:
         raise ValueError("FP8 W8A8 weight scales are one bf16 per output channel")
+    if skinny is None and pre_quantize is not None:  # a decode-kernel variant was asked for
+        skinny = False
+    if _use_skinny(skinny, x, tiled, planes, config):
+        if pre_quantize is False:
+            raise ValueError("the FP8 skinny GEMM takes the activation quantized beforehand")
+        xq, sx = quantize_fp8_activation(x)
+        return _skinny_fp8(q, s, xq, sx, n, k, swiglu)
     if pre_quantize is None:
         pre_quantize = x.shape[0] >= FP8_QUANTIZE_FROM and k % 128 == 0
     if pre_quantize:
@@ -261,9 +291,10 @@ def linear_fp8_w8a8(x, packed, config=None, planes=False, swiglu=False, pre_quan
                        (_lib.ptr(q), _lib.ptr(s), _lib.ptr(x)), (tiled,), mode=_mode(swiglu, planes), config=config)
 
 
-def linear_fp8_w8a8_quantized(xq, sx, packed, config=None, planes=False, swiglu=False):
+def linear_fp8_w8a8_quantized(xq, sx, packed, config=None, planes=False, swiglu=False, skinny=None):
     """FP8 W8A8 linear of an activation quantized beforehand: e4m3 codes ``xq`` [m, k] with
-    fp32 per-token scales ``sx`` [m] (``quantize_fp8_activation`` or ``add_norm_quant_fp8``)."""
+    fp32 per-token scales ``sx`` [m] (``quantize_fp8_activation`` or ``add_norm_quant_fp8``).
+    ``skinny`` as for ``linear_fp8_w8a8``."""
     q, s, n, k, tiled = _unpack(packed, "fp8")
     if xq.ndim != 2 or xq.shape[1] != k or xq.element_size() != 1:
         raise ValueError("codes must be one byte each, [m, k] with k the weight's width")
@@ -272,6 +303,8 @@ def linear_fp8_w8a8_quantized(xq, sx, packed, config=None, planes=False, swiglu=
     if not 1 <= xq.shape[0] <= 64:
         raise ValueError(f"batch {xq.shape[0]} exceeds 64 rows")
     _lib.require_device(q, s, xq, sx)
+    if _use_skinny(skinny, xq, tiled, planes, config):
+        return _skinny_fp8(q, s, xq.view(torch.uint8), sx, n, k, swiglu)
     return _linear.run(_lib.FMT_FP8, "qlx_linear_fp8_w8a8_q", xq, n, k,
                        (_lib.ptr(q), _lib.ptr(s), _lib.ptr(xq), _lib.ptr(sx)), (tiled,),
                        mode=_mode(swiglu, planes), config=config)

@@ -171,6 +171,15 @@ int qlx_plan_skinny(int fmt, int mode, int m, int n, int k, qlx_plan* plan);
 int qlx_linear_skinny(int fmt, const void* w, const void* w_scale, const void* x, void* y, int m, int n, int k,
                       const qlx_plan* plan, void* stream);
 
+/* The skinny GEMM for FP8 W8A8 at 9..64 tokens: the activation quantized per token beforehand
+ * (qlx_quantize_fp8_act or qlx_add_norm_quant_fp8: e4m3 codes [m][k] and fp32 scales [m]), its
+ * codes streamed through LDS per K step against e4m3 weights on the fp8 MFMA; each output is
+ * the fp32 product times the channel's and the token's scale (qlx_plan_skinny with
+ * QLX_FMT_FP8 plans it). The W8A8 batches the reference serves through cuda_int8.matmul at
+ * b9-16 (engine/kernels/cuda_int8.py:251-281; engine/engine.py:623-625). */
+int qlx_linear_skinny_fp8(const void* w, const void* w_scale, const void* x_code, const float* x_scale, void* y,
+                          int m, int n, int k, const qlx_plan* plan, void* stream);
+
 /* qlx_linear_skinny for callers that cannot allocate (code under graph capture, serving
  * loops, harnesses that forbid hipMalloc): no counterpart in the reference. It plans the call
  * itself (qlx_plan_skinny) and keeps the K-slice planes and ticket counters in the library's

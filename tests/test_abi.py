@@ -79,7 +79,7 @@ def test_contract_violations_fail_before_any_launch():
     # skinny GEMM: W4A16/W8A16 only, m <= 64, whole 16-row tiles; NULL pointers; K slices
     # without a workspace
     sk = _lib.Plan()
-    assert lib.qlx_plan_skinny(_lib.FMT_FP8, 0, 16, 256, 512, sk) == _lib.QLX_EINVAL
+    assert lib.qlx_plan_skinny(_lib.FMT_INT8, 0, 16, 256, 512, sk) == _lib.QLX_EINVAL
     assert lib.qlx_plan_skinny(_lib.FMT_W4A16, 0, 65, 256, 512, sk) == _lib.QLX_EINVAL
     assert lib.qlx_plan_skinny(_lib.FMT_W4A16, 0, 16, 250, 512, sk) == _lib.QLX_EINVAL
     assert lib.qlx_plan_skinny(_lib.FMT_W8A16, 0, 16, 2560, 9728, sk) == 0 and sk.waves == 4 and sk.splits > 1

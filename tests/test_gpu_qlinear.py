@@ -294,7 +294,7 @@ def test_tiled_weights_match_oracle_and_row_major_bitwise(fmt):
     raw = packed[0].view(torch.uint8).cpu().numpy() if fmt == "fp8" else packed[0].cpu().numpy()
     want = O.tile_rows(raw)
     assert np.array_equal(tiled.weight.cpu().view(torch.uint8).numpy().reshape(want.shape), want)
-    same_kernel = {} if fmt == "fp8" else {"skinny": False}  # tiled batches > 8 default to the skinny GEMM
+    same_kernel = {"skinny": False}  # tiled batches > 8 default to the skinny GEMM
     for m in (1, 8, 33):
         x = acts(m, k, 600 + m).to(DEV)
         for cfg in (None, (4, 4, 1, 2), (8, 2, 2, 1)):
@@ -346,6 +346,35 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
         assert O.rel_l2(ys.float().cpu().numpy(), ref) <= 1e-2, (fmt, n, k, m)
         if not sw:
             assert not ys[:, 0].float().abs().sum().item(), "zero weight row must give zero"
+
+
+@pytest.mark.parametrize("n,k,sw", [(2 * 9728, 2560, True), (2560, 9728, False), (4112, 2560, False)])
+def test_fp8_skinny_gemm_matches_decode_kernel_and_oracle(n, k, sw):
+    """FP8 W8A8 from 9 tokens runs the skinny GEMM on the activation's e4m3 codes (quantized per
+    token by its own kernel): within one bf16 rounding step of the decode kernel on the same
+    codes, rel-L2 <= 1e-2 against the oracle's W8A8 product, K slices reduced by the last
+    workgroup bit-identical to the planes launch, and the same output from codes handed in."""
+    print(f"fp8 skinny n={n} k={k} swiglu={sw}", flush=True)
+    packed = qlinear.quantize_fp8(weights(n, k, 44).to(DEV))
+    tiled = qlinear.prepare(packed)
+    q, s = packed
+    for m in (9, 16, 17, 33, 64):
+        x = acts(m, k, 990 + m).to(DEV)
+        ys = qlinear.linear_fp8_w8a8(x, tiled, swiglu=sw)
+        yd = qlinear.linear_fp8_w8a8(x, tiled, swiglu=sw, pre_quantize=True).float()
+        xq, sx = qlinear.quantize_fp8_activation(x)
+        for fused in (True, False):
+            yu = qlinear._skinny_fp8(tiled.weight, tiled.scale, xq.view(torch.uint8), sx, n, k, sw, fused_reduce=fused)
+            assert torch.equal(ys, yu), (n, k, m, fused, "fused split-K reduction differs from the planes launch")
+        assert torch.equal(ys, qlinear.linear_fp8_w8a8_quantized(xq, sx, tiled, swiglu=sw)), (n, k, m)
+        diff = (ys.float() - yd).abs()
+        rowmax = yd.abs().amax(dim=1, keepdim=True)
+        tol = (2.0 ** -6 if sw else 2.0 ** -7) * yd.abs() + 2.0 ** -9 * rowmax
+        assert (diff > tol).sum().item() == 0, (n, k, m, diff.max().item())
+        ref = O.linear_fp8_w8a8(bits16(x), q.view(torch.uint8).cpu().numpy(), bits16(s))
+        if sw:
+            ref = O.bf16_to_f32(O.swiglu(O.f32_to_bf16(ref.astype(np.float32))))
+        assert O.rel_l2(ys.float().cpu().numpy(), ref) <= 1e-2, (n, k, m)
 
 
 @pytest.mark.parametrize("m", [33, 64])
