@@ -23,10 +23,13 @@ qlx::FmtInfo fmt_info(int fmt) {
   }
 }
 
-// Workgroups a streaming GEMV should at least have. Measured on MI355X at M = 1 over the
+// Workgroups a streaming GEMV should at least have. Measured on MI355X at M = 1..8 over the
 // Qwen3-4B shapes: fewer, larger workgroups win (each pays the activation staging and a
-// reduction once) as long as there are about 150 or more of them.
-constexpr int kMinGroups = 160;
+// reduction once) as long as there are about 150 or more of them (gate_up's 152 whole tiles
+// per 8 waves: 13.4 us against 16.9 with 304 half tiles, W4A16).
+constexpr int kMinGroups = 150;
+// Workgroups of 8 waves that run in one round (one per CU).
+constexpr int kOneRound = 256;
 
 }  // namespace
 
@@ -53,9 +56,36 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
       break;
     }
   }
+  qlx::GemmArgs a = {};
+  if (m <= 16) {
+    // Up to 16 tokens the staged activation slice may use the whole LDS while the workgroups
+    // fit one round (one per CU): o at 8 tokens whole-K 8.5 us against 13.0 with two K slices
+    // (W4A16). Where K must be sliced to fit, take fewer waves per tile and as many slices as
+    // still fit one round: down at 4-8 tokens (W4A16) 4 waves per tile x 3 slices (240
+    // workgroups) 12.0-12.7 us against 16.8-17.5 with 8 x 2-3 (320-480 workgroups).
+    const int kw0 = p.kw;
+    for (int kw = kw0; kw >= 1; kw /= 2) {
+      qlx_plan q = p;
+      q.kw = kw;
+      const int groups = (ntiles + (q.waves / kw) * q.rw - 1) / ((q.waves / kw) * q.rw);
+      if (kw < kw0 && groups * 2 > kOneRound) break;  // fewer waves per tile would not help
+      int smin = 1;  // the fewest K slices whose staged slice fits
+      for (; smin <= nsteps; ++smin) {
+        q.splits = smin;
+        if (qlx::layout(fi, q, m, n, k, a) <= qlx::kLdsLimit) break;
+      }
+      if (smin > nsteps) continue;
+      const int s = std::max(smin, smin > 1 ? kOneRound / groups : 1);
+      if (groups * s > kOneRound && !(s == 1 && kw == kw0)) continue;
+      q.splits = std::min(s, nsteps);
+      qlx::layout(fi, q, m, n, k, a);
+      q.splits = a.splits;
+      *plan = q;
+      return QLX_OK;
+    }
+  }
   // Large m stages a wide activation slice: split K until the workgroup's LDS fits the
   // 64 KB target; a plan whose reduction buffer alone is larger drops to 4 waves.
-  qlx::GemmArgs a = {};
   for (;;) {
     const int lds = qlx::layout(fi, p, m, n, k, a);
     if (lds <= qlx::kLdsTarget) break;

@@ -17,9 +17,9 @@ def make_plan(fmt, mode, m, n, k, config=None, fit=False, comp=1):
     library (every K slice non-empty); ``fit`` first grows the splits until the LDS fits.
     The library default always fits."""
     plan = _lib.Plan()
-    if config is None:
+    if config is None:  # the library's plan fits as it is (a second activation component may not)
         _lib.check(_lib.lib().qlx_plan_linear(fmt, mode, m, n, k, plan), "plan_linear")
-        fit = True
+        fit = comp > 1
     else:
         waves, kw, rw, splits = config
         plan.mode, plan.waves, plan.kw, plan.rw, plan.splits = mode, waves, kw, rw, splits

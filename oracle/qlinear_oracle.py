@@ -240,22 +240,31 @@ def int8_prepare(row_major_bytes):
     return (row_major_bytes[:, cols] ^ 128).astype(np.uint8).view(np.int8)
 
 
-def int8_quantize_activation(x_bits):
+def int8_quantize_activation(x_bits, components=1):
     """Per-row, per-64-group INT8 activation quantize (cuda_int8.py:58-77).
 
     s = max(amax/127, 1e-20) in fp32; q = rint(x/s) (``nearbyint``, half-even)
     stored at fragment position p from natural ``int8_natural()[p]``. Returns
-    (q int8 [M,K], s fp32 [M,K/64]). Pinned by closed form and brute-force
-    tests (the reference's version is a Triton kernel that cannot run here).
+    (q int8 [M,K], s fp32 [M,K/64]). With ``components=2`` (cuda_int8.py:70-77) also the
+    second component of what q leaves: residual = x - fp32(q * s) (the kernel is compiled
+    without fp fusion, so the product is rounded before the subtraction), then
+    sr = max(amax(residual)/127, 1e-20) and qr = rint(residual/sr) in the same positions:
+    returns (q, s, qr, sr). Pinned by closed form and brute-force tests (the reference's
+    version is a Triton kernel that cannot run here).
     """
     x = bf16_to_f32(x_bits)
     m, k = x.shape
     nat = int8_natural()
     g = x.reshape(m, k // 64, 64)
     s = np.maximum(np.abs(g).max(axis=2) / F32(127.0), F32(1e-20)).astype(F32)
-    q = np.rint(g / s[:, :, None]).astype(np.int8)
-    q = q[:, :, nat]
-    return q.reshape(m, k), s
+    qf = np.rint(g / s[:, :, None]).astype(F32)
+    q = qf.astype(np.int8)[:, :, nat]
+    if components == 1:
+        return q.reshape(m, k), s
+    res = (g - (qf * s[:, :, None]).astype(F32)).astype(F32)
+    sr = np.maximum(np.abs(res).max(axis=2) / F32(127.0), F32(1e-20)).astype(F32)
+    qr = np.rint(res / sr[:, :, None]).astype(np.int8)[:, :, nat]
+    return q.reshape(m, k), s, qr.reshape(m, k), sr
 
 
 def linear_w8a8_int8(x_bits, prepared_i8, w_scale_f16):

@@ -200,6 +200,9 @@ def test_cuda_int8_quantize_matmul_add_norm_quant():
             assert np.array_equal(q.cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), os_)
             q1, s1, q2, s2 = cuda_int8.quantize_activation(x, components=2)
             assert torch.equal(q1, q) and torch.equal(s1, s)
+            _, _, oq2, os2 = O.int8_quantize_activation(bits16(x), components=2)
+            assert np.array_equal(q2.cpu().numpy(), oq2) and np.array_equal(s2.cpu().numpy(), os2), \
+                (n, k, m, "second component vs oracle")
             want = O.linear_w8a8_int8(bits16(x), prepared.weight.cpu().numpy(), bits16(prepared.scale))
             for config in ((4, 1), (8, 2), (4, 4)):
                 got = cuda_int8.matmul(x, prepared, config=config).float().cpu().numpy()

@@ -275,6 +275,43 @@ def test_int8_activation_quantize_closed_form():
                 assert q[r, grp * 64 + p] == np.int8(np.rint(xf[r, grp, nat[p]] / sc))
 
 
+def test_int8_second_component_closed_forms_and_bounds():
+    """The INT8 activation's second component (cuda_int8.py:70-77): whole-number groups are
+    taken exactly by the first component (residual 0: qr = 0, sr = 1e-20); otherwise the two
+    components reconstruct every value to within half a step of the second scale, the second
+    scale is the residual's max / 127, and each group's largest residual maps to +-127. A
+    planted mistake (the residual taken with a fused multiply-add, i.e. the product unrounded)
+    changes the codes of random data."""
+    g = torch.Generator().manual_seed(31)
+    # closed form: integers with a group maximum of 127 -> s = 1 exactly, nothing left over
+    ints = torch.randint(-127, 128, (2, 128), generator=g).float()
+    ints[:, 0] = 127.0
+    ints[:, 64] = -127.0
+    q, s, qr, sr = O.int8_quantize_activation(bits16(ints.to(torch.bfloat16)), components=2)
+    assert np.all(s == np.float32(1.0)) and not qr.any() and np.all(sr == np.float32(1e-20))
+    nat = O.int8_natural()
+    assert np.array_equal(q.reshape(2, 2, 64), ints.numpy().astype(np.int8).reshape(2, 2, 64)[:, :, nat])
+    # bounds on random data
+    x = bits16(torch.randn(4, 256, generator=g).to(torch.bfloat16))
+    q, s, qr, sr = O.int8_quantize_activation(x, components=2)
+    q1, s1 = O.int8_quantize_activation(x)
+    assert np.array_equal(q, q1) and np.array_equal(s, s1), "the first component is the plain quantize"
+    xf = O.bf16_to_f32(x).reshape(4, 4, 64)[:, :, nat].astype(np.float64)
+    qd = q.reshape(4, 4, 64).astype(np.float64)
+    rd = qr.reshape(4, 4, 64).astype(np.float64)
+    res = xf - qd * s[:, :, None].astype(np.float64)
+    assert np.all(np.abs(res - rd * sr[:, :, None]) <= 0.5 * sr[:, :, None] * (1 + 1e-6) + 1e-7 * np.abs(xf))
+    assert np.all(np.abs(rd).max(axis=2) == 127)
+    assert np.allclose(sr, np.abs(res).max(axis=2) / 127, rtol=1e-5)
+    # planted mistake: the residual with the product kept exact
+    xf32 = O.bf16_to_f32(x).reshape(4, 4, 64)
+    qf = np.rint(xf32 / s[:, :, None]).astype(np.float64)
+    fused = (xf32.astype(np.float64) - qf * s[:, :, None].astype(np.float64)).astype(np.float32)
+    sr_f = np.maximum(np.abs(fused).max(axis=2) / np.float32(127), np.float32(1e-20)).astype(np.float32)
+    qr_f = np.rint(fused / sr_f[:, :, None]).astype(np.int8)[:, :, nat].reshape(4, 256)
+    assert not (np.array_equal(qr_f, qr) and np.array_equal(sr_f, sr)), "an unrounded product must show"
+
+
 def test_int8_w8a8_product_pinned_by_golden_weights_and_fp64(gold):
     """oracle.linear_w8a8_int8 (the INT8 W8A8 GEMM's checker) against an fp64 torch product in
     natural column order: activation s_x * rint(x / s_x) per 64-group (torch ops), weight
