@@ -210,9 +210,12 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   GemmArgs a = a0;
   int bid = blockIdx.x;
+  int b = 0;      // token block
+  int prow = a.m;  // rows of one fp32 plane
   if (a.tblocks == 2) {  // token blocks: block ids 16 q + 8 b + x are row group 8 q + x, tokens 32 b..
     // (ids 8 apart share an XCD, so the second block finds the weights in that XCD's L2)
-    const int b = (bid >> 3) & 1;
+    b = (bid >> 3) & 1;
+    prow = a.pm;
     bid = 8 * (bid >> 4) + (bid & 7);
     a.x = static_cast<const char*>(a.x) + (size_t)b * 32 * a.k * F::XBYTES;
     if (a.xs) a.xs += b * 32;
@@ -348,8 +351,9 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
 
   // Epilogue: lane holds rows 4 (lane >> 4) + 0..3 of each tile for token 16 mt + (lane & 15).
   // K-slice planes shared through tickets go through a buffer resource at device scope.
-  const __amdgpu_buffer_rsrc_t wr =
-      skinny_rsrc(a.work, a.tickets != nullptr ? (unsigned)a.splits * (unsigned)a.m * (unsigned)a.n * 4u : 0u);
+  // (over this block's rows of every plane: planes are prow rows apart)
+  const __amdgpu_buffer_rsrc_t wr = skinny_rsrc(
+      a.work, a.tickets != nullptr ? ((unsigned)(a.splits - 1) * (unsigned)prow + (unsigned)a.m) * (unsigned)a.n * 4u : 0u);
   const int r0 = 4 * (lane >> 4);
   const uint16_t* ws = reinterpret_cast<const uint16_t*>(a.ws);
   uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
@@ -369,10 +373,10 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
       }
       if (a.splits > 1) {  // fp32 plane s, rows in natural order
         if (mm < a.m) {
-          float* plane = a.work + ((size_t)s * (a.tblocks == 2 ? a.pm : a.m) + mm) * a.n;
+          float* plane = a.work + ((size_t)s * prow + mm) * a.n;
           if (a.tickets != nullptr) {  // read by the row group's last workgroup below
             // rows r0 .. r0 + 3 of a tile are consecutive weight rows: one 16-byte store
-            const unsigned off = (unsigned)(((size_t)s * a.m + mm) * a.n + weight_row(a, tile[r], r0)) * 4u;
+            const unsigned off = (unsigned)(((size_t)s * prow + mm) * a.n + weight_row(a, tile[r], r0)) * 4u;
             __builtin_amdgcn_raw_buffer_store_b128(
                 u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
                 wr, (int)off, 0, kSc1);
@@ -408,9 +412,10 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   __shared__ int s_last;
   publish_stores();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.tickets[tg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int* ticket = &a.tickets[a.tblocks == 2 ? 2 * tg + b : tg];  // per (row group, token block)
+    const int prev = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == a.splits - 1;
-    if (s_last) __hip_atomic_store(&a.tickets[tg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (s_last) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
@@ -419,7 +424,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   // rows), each plane's chunk one 16-byte device-scope load, 4 planes in flight at a time.
   constexpr int RT = WAVES * RW, QUADS = SW ? 2 : 4;  // 4-row chunks per tile
   const int per_tok = RT * QUADS;
-  const unsigned pstride = (unsigned)a.m * (unsigned)a.n * 4u;
+  const unsigned pstride = (unsigned)prow * (unsigned)a.n * 4u;
   auto f4 = [](const u32x4& u) { return f32x4{__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]),
                                               __uint_as_float(u[3])}; };
   for (int idx = threadIdx.x; idx < per_tok * a.m; idx += WAVES * 64) {
@@ -545,15 +550,17 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
               "%s: %d planes of %d x %d floats exceed the 2 GiB a shared reduction addresses", name, splits, m, n);
   hipStream_t st = (hipStream_t)stream;
   const int wgs = a.tile_groups * splits;
-  if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && a.tickets == nullptr && splits > 1 &&
-      wgs % 8 == 0 && 2 * wgs <= 512) {
+  if (skinny_mt_of(m) == 4 && F::NSC > 0 && plan->waves == 4 && splits > 1 && wgs % 8 == 0 && 2 * wgs <= 512) {
     // K-sliced batches of 33..64 tokens whose two 32-token blocks still fit the two-per-CU
     // instance in one round (down: 40 row groups x 6 slices = 240 per block): one launch, a
-    // (row group, slice)'s two blocks on one XCD; each block writes its rows of the planes.
+    // (row group, slice)'s two blocks on one XCD; each block writes its rows of the planes, and
+    // with tickets the last workgroup of each (row group, block) reduces them (2 counters per
+    // row group).
     a.tblocks = 2;
     a.pm = m;
     const hipError_t e = skinny_launch<F, 2, 1, 4>(a, skinny_layout<F>(32, 4, plan->rw), sps, st);
     if (e != hipSuccess) return hip_status(e, name);
+    if (a.tickets != nullptr) return QLX_OK;
     if (mode == QLX_MODE_SWIGLU) return qlx_swiglu(nullptr, plan->workspace, splits, a.y, m, n / 2, stream);
     return qlx_reduce_planes(plan->workspace, a.y, (long long)m * n, splits, stream);
   }

@@ -179,8 +179,8 @@ def _skinny(fmt, q, s, x, n, k, swiglu, fused_reduce=None):
     K slices write fp32 planes that the row group's last workgroup reduces in slice order
     (``fused_reduce``: split-K tickets) or a second launch reduces (bit-identical)."""
     m = x.shape[0]
-    if fused_reduce is None:  # up to 32 tokens (33-64 token blocks need the planes launch)
-        fused_reduce = m <= 32
+    if fused_reduce is None:
+        fused_reduce = True
     mode = _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16
     plan = _lib.Plan()
     _lib.check(_lib.lib().qlx_plan_skinny(fmt, mode, m, n, k, plan), "plan_skinny")
@@ -247,7 +247,7 @@ def _skinny_fp8(q, s, xq, sx, n, k, swiglu, fused_reduce=None):
     slices reduced as in ``_skinny``."""
     m = xq.shape[0]
     if fused_reduce is None:
-        fused_reduce = m <= 32
+        fused_reduce = True
     mode = _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16
     plan = _lib.Plan()
     _lib.check(_lib.lib().qlx_plan_skinny(_lib.FMT_FP8, mode, m, n, k, plan), "plan_skinny")
