@@ -1,0 +1,550 @@
+// Grouped-query decode attention over the KV cache, split along the key length
+// (engine/kernels/attention.py:37-227: split kernel, merge kernel, DecodeAttention).
+//
+// One workgroup per (sequence x KV head, split); its four waves take 32-key blocks in turn.
+// The R = tokens x group query rows of a KV head share every key and value it reads:
+//
+//   S^T = K Q^T   on v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims (a lane's 16-byte load
+//                 of one key row), B = Q^T (the rows' query fragments, held in registers).
+//                 The C fragment leaves each lane 8 keys of one query row, which is exactly
+//                 the A fragment the P V product needs, so P never goes through LDS.
+//   O += P V      A = bf16(P) 16 rows x 32 keys, B = V. A lane loads 8 consecutive values of 8
+//                 keys (eight 16-byte loads) and transposes that 8 x 8 block in registers; the
+//                 8 products of a block take output columns d = 8 n + j (j = 0..7), which
+//                 covers the 128 dims with every lane's block used once.
+//
+// Softmax follows the reference: fp32 scores and running maximum, p = exp(s - max), the
+// row total summed from fp32 p, the P V product from bf16 p, acc / total at the end
+// (attention.py:102-137). Exponentials are base 2 on scores pre-multiplied by log2(e).
+// The split partials merge as in attention.py:144-178: weights exp(max_s - max), sum of
+// weighted accumulators over sum of weighted totals; the merge runs in the workgroup that
+// finishes a head last (a ticket), not in a second launch.
+//
+// Splits are a parallelism knob, not a fixed key range: the live length `end` = pos + tokens
+// is read on the device and divided into `splits` chunks of whole 32-key blocks, so every
+// workgroup has work whatever the capacity, and the grid stays fixed for graph capture.
+#include "common.h"
+#include "../../include/qlinear.h"
+
+#include <algorithm>
+
+namespace qlx {
+
+struct AttnArgs {
+  const uint16_t* q;   // bf16 [B*T][H*G*128]
+  const void* k;       // bf16 or int8 [B][H][cap][128]
+  const void* v;
+  const float* ks;     // fp32 [B][H][cap] (INT8 cache)
+  const float* vs;
+  const int* pos;      // base position of token 0
+  uint16_t* out;       // bf16 [B*T][H*G*128]
+  float* pacc;         // [B*H][S][R][128]
+  float* pm;           // [B*H][S][R]
+  float* pl;           // [B*H][S][R]
+  int* tickets;        // [B*H], zero before and after a launch
+  float scale2;        // head_dim^-0.5 * log2(e)
+  int cap, splits, T, G, H, R, heads;
+};
+
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Dim slot of MFMA k-step s for lane group g. The order inside a product is free as long as
+// the query and key fragments agree: bf16 keys take dims 32 s + 8 g (each load instruction
+// reads 64 consecutive bytes of 16 keys), INT8 keys 32 g + 8 s (a lane's four steps are 32
+// consecutive bytes, two 16-byte loads).
+template <bool Q8>
+__device__ __forceinline__ int kdim(int s, int g) { return Q8 ? 32 * g + 8 * s : 32 * s + 8 * g; }
+
+// Key of slot j (0..7) of lane group g in a 32-key block: the keys the S^T fragment leaves
+// in that lane (key tile j / 4, row 4 g + j % 4).
+__device__ __forceinline__ int slot_key(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
+
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+__device__ __forceinline__ bf16x8 bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Buffer resource over `bytes` of device memory (base uniform across the workgroup); loads and
+// stores through it with kSc1 go past this XCD's L2, so another XCD's workgroup sees them.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const void* p, unsigned bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr int kSc1 = 16;
+
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+template <bool Q8>
+struct KVBlock;
+
+template <>
+struct KVBlock<false> {
+  u32x4 k[2][4];  // [key tile][k-step]: 8 dims of key 16 kt + n
+  u32x4 v[8];     // [slot]: V[key(slot)][8 n .. 8 n + 7]
+  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int stop, int n, int g) {
+    const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + hb;
+    const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + hb;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = min(kb + 16 * kt + n, stop - 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) k[kt][s] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + kdim<false>(s, g)));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = min(kb + slot_key(g, j), stop - 1);
+      v[j] = *gmem(reinterpret_cast<const u32x4*>(V + (size_t)key * 128 + 8 * n));
+    }
+  }
+  __device__ __forceinline__ u32x4 kfrag(int kt, int s) const { return k[kt][s]; }
+  // Column c (0..7) of the lane's 8 keys x 8 dims block: 8 keys of dim 8 n + c, slot order.
+  __device__ __forceinline__ u32x4 vfrag(int c) const {
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = reinterpret_cast<const uint32_t*>(&v[2 * q])[c >> 1];
+      const uint32_t hi = reinterpret_cast<const uint32_t*>(&v[2 * q + 1])[c >> 1];
+      d[q] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+    return u32x4{d[0], d[1], d[2], d[3]};
+  }
+};
+
+// INT8 cache: codes with one fp32 scale per (token, head); each value is dequantised to
+// bf16(code * scale) as it is loaded (attention.py:94-99).
+template <>
+struct KVBlock<true> {
+  u32x4 k[2][2];  // [key tile][half]: dims 32 g .. 32 g + 31 of key 16 kt + n
+  u32x2 v[8];     // [slot]: codes of V[key(slot)][8 n .. 8 n + 7]
+  float ksc[2], vsc[8];
+  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int stop, int n, int g) {
+    const int8_t* K = reinterpret_cast<const int8_t*>(a.k) + hb;
+    const int8_t* V = reinterpret_cast<const int8_t*>(a.v) + hb;
+    const size_t sb = hb >> 7;  // scale index of key 0 of this head
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = min(kb + 16 * kt + n, stop - 1);
+      k[kt][0] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g));
+      k[kt][1] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g + 16));
+      ksc[kt] = gmem(a.ks)[sb + key];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = min(kb + slot_key(g, j), stop - 1);
+      v[j] = *gmem(reinterpret_cast<const u32x2*>(V + (size_t)key * 128 + 8 * n));
+      vsc[j] = gmem(a.vs)[sb + key];
+    }
+  }
+  static __device__ __forceinline__ float deq(uint32_t w, int b, float sc) {
+    return round_bf((float)(int)(int8_t)(w >> (8 * b)) * sc);
+  }
+  __device__ __forceinline__ u32x4 kfrag(int kt, int s) const {
+    const uint32_t* c = reinterpret_cast<const uint32_t*>(&k[kt][s >> 1]) + 2 * (s & 1);
+    const float sc = ksc[kt];
+    return u32x4{pack_bf(deq(c[0], 0, sc), deq(c[0], 1, sc)), pack_bf(deq(c[0], 2, sc), deq(c[0], 3, sc)),
+                 pack_bf(deq(c[1], 0, sc), deq(c[1], 1, sc)), pack_bf(deq(c[1], 2, sc), deq(c[1], 3, sc))};
+  }
+  __device__ __forceinline__ u32x4 vfrag(int c) const {
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w0 = reinterpret_cast<const uint32_t*>(&v[2 * q])[c >> 2];
+      const uint32_t w1 = reinterpret_cast<const uint32_t*>(&v[2 * q + 1])[c >> 2];
+      d[q] = pack_bf(deq(w0, c & 3, vsc[2 * q]), deq(w1, c & 3, vsc[2 * q + 1]));
+    }
+    return u32x4{d[0], d[1], d[2], d[3]};
+  }
+};
+
+// RT tiles of 16 query rows (R <= 16 RT). 256 threads; dynamic LDS 4 x R x 128 fp32.
+template <int RT, bool Q8>
+__global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
+  extern __shared__ float wacc[];  // [4 waves][R][128]
+  __shared__ float wm[4][64], wl[4][64];
+  __shared__ int s_last;
+  const int head = blockIdx.x, part = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int seq = head / a.H, kvh = head - seq * a.H;
+  const int NQ = a.H * a.G;
+  const int base = a.pos[0];
+  const int end = min(base + a.T, a.cap);  // keys at or past end are live for no row
+  // at least one 32-key block per wave, so a short context does not spread over idle splits
+  const int chunk = end > 0 ? max(128, ((end + a.splits - 1) / a.splits + 31) & ~31) : 128;
+  const int start = part * chunk;
+  const int stop = min(start + chunk, end);
+  const size_t hb = (size_t)head * a.cap * 128;
+
+  // Query fragments (B operand of S^T = K Q^T): row 16 rt + n, dims kdim(s, g). Up to two row
+  // tiles live in registers; more are read from LDS each block (the four waves share them),
+  // which with no prefetched block keeps the wave within its registers.
+  constexpr bool QLDS = RT >= 3;
+  __shared__ u32x4 qlds[QLDS ? RT * 4 * 64 : 1];
+  u32x4 qf[QLDS ? 1 : RT][4];
+  auto qload = [&](int rt, int s) -> u32x4 {
+    const int r = 16 * rt + n;
+    if (r >= a.R) return u32x4{0u, 0u, 0u, 0u};
+    const int t = r / a.G, gi = r - t * a.G;
+    const uint16_t* qp = a.q + ((size_t)(seq * a.T + t) * NQ + kvh * a.G + gi) * 128 + kdim<Q8>(s, g);
+    return *gmem(reinterpret_cast<const u32x4*>(qp));
+  };
+  if constexpr (QLDS) {
+    for (int i = w; i < RT * 4; i += 4) qlds[i * 64 + lane] = qload(i >> 2, i & 3);
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qf[rt][s] = qload(rt, s);
+  }
+  auto qfrag = [&](int rt, int s) -> u32x4 {
+    if constexpr (QLDS) return qlds[(rt * 4 + s) * 64 + lane];
+    else return qf[rt][s];
+  };
+  // Last live key + 1 of row 16 rt + n (padding rows: every key of the split).
+  int lim[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = 16 * rt + n;
+    lim[rt] = r < a.R ? min(base + r / a.G + 1, stop) : stop;
+  }
+
+  float m[RT], l[RT];
+  f32x4 acc[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = kNegInf;
+    l[rt] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto compute = [&](const KVBlock<Q8>& b, int kb) __attribute__((always_inline)) {
+    u32x4 kf[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[kt][s] = b.kfrag(kt, s);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      f32x4 st[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf8(kf[kt][s]), bf8(qfrag(rt, s)), st[kt], 0, 0, 0);
+      }
+      // lane: row 16 rt + n, keys kb + 16 kt + 4 g + i
+      float sc[8];
+      float bm = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 16 * kt + 4 * g + i;
+          sc[4 * kt + i] = key < lim[rt] ? st[kt][i] * a.scale2 : kNegInf;
+          bm = fmaxf(bm, sc[4 * kt + i]);
+        }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m[rt], bm);
+      const float mu = mn == kNegInf ? 0.f : mn;  // a row with no live key yet keeps p = 0
+      const float carry = ex2(m[rt] - mu);
+      m[rt] = mn;
+      float p[8], ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = ex2(sc[j] - mu);
+        ps += p[j];
+      }
+      l[rt] = l[rt] * carry + ps;
+      const u32x4 pf = u32x4{pack_bf(p[0], p[1]), pack_bf(p[2], p[3]), pack_bf(p[4], p[5]), pack_bf(p[6], p[7])};
+      // acc rows 4 g + i of this tile take the carry of the lane holding that row
+      float cr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cr[i] = __shfl(carry, 4 * g + i, 64);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        f32x4 t = acc[rt][c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] *= cr[i];
+        acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf8(pf), bf8(b.vfrag(c)), t, 0, 0, 0);
+      }
+    }
+  };
+
+  // The wave's blocks start + 32 (w + 4 i). With up to two row tiles the next block's loads
+  // are issued before the current block is computed.
+  int kb = start + 32 * w;
+  if constexpr (RT <= 2) {
+    if (kb < stop) {
+      KVBlock<Q8> cur, nxt;
+      cur.load(a, hb, kb, stop, n, g);
+      for (;;) {
+        const int kn = kb + 128;
+        if (kn < stop) {
+          nxt.load(a, hb, kn, stop, n, g);
+          compute(cur, kb);
+          kb = kn;
+          const int k2 = kb + 128;
+          if (k2 < stop) {
+            cur.load(a, hb, k2, stop, n, g);
+            compute(nxt, kb);
+            kb = k2;
+            continue;
+          }
+          compute(nxt, kb);
+          break;
+        }
+        compute(cur, kb);
+        break;
+      }
+    }
+  } else {
+    for (; kb < stop; kb += 128) {
+      KVBlock<Q8> cur;
+      cur.load(a, hb, kb, stop, n, g);
+      compute(cur, kb);
+    }
+  }
+
+  // Merge the four waves: wave maxima and totals, then each wave's accumulator rescaled to
+  // the workgroup maximum, summed over waves in order.
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float lt = l[rt] + __shfl_xor(l[rt], 16, 64);
+    lt = lt + __shfl_xor(lt, 32, 64);
+    const int r = 16 * rt + n;
+    if (g == 0 && r < a.R) {
+      wm[w][r] = m[rt];
+      wl[w][r] = lt;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * rt + 4 * g + i;
+      if (r >= a.R) continue;
+      const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+      const float f = wm[w][r] == kNegInf ? 0.f : ex2(wm[w][r] - M);
+      float* dst = wacc + ((size_t)w * a.R + r) * 128 + 8 * n;
+      f32x4 lo, hi;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        lo[c] = acc[rt][c][i] * f;
+        hi[c] = acc[rt][c + 4][i] * f;
+      }
+      *reinterpret_cast<f32x4*>(dst) = lo;
+      *reinterpret_cast<f32x4*>(dst + 4) = hi;
+    }
+  }
+  __syncthreads();
+
+  // Workgroup result per (row, 4 dims): maximum M, total L, accumulator A (waves in order).
+  auto wg_result = [&](int r, int d4, float& M, float& L) -> f32x4 {
+    M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float f = wm[q][r] == kNegInf ? 0.f : ex2(wm[q][r] - M);
+      L += wl[q][r] * f;
+      A += *reinterpret_cast<const f32x4*>(wacc + ((size_t)q * a.R + r) * 128 + d4);
+    }
+    return A;
+  };
+  auto store_out = [&](int r, int d4, f32x4 A, float L) {
+    const int t = r / a.G, gi = r - t * a.G;
+    uint16_t* o = a.out + ((size_t)(seq * a.T + t) * NQ + kvh * a.G + gi) * 128 + d4;
+    *gmem(reinterpret_cast<u32x2*>(o)) = u32x2{pack_bf(A[0] / L, A[1] / L), pack_bf(A[2] / L, A[3] / L)};
+  };
+  const int items = a.R * 32;
+  if (a.splits == 1) {
+    for (int idx = threadIdx.x; idx < items; idx += 256) {
+      const int r = idx >> 5, d4 = (idx & 31) * 4;
+      float M, L;
+      const f32x4 A = wg_result(r, d4, M, L);
+      store_out(r, d4, A, L);
+    }
+    return;
+  }
+
+  // Several splits: publish this split's partial (splits holding live keys only) with
+  // device-scope stores, take the head's ticket; the last workgroup merges the live splits in
+  // split order. Partials: acc [heads][S][R][128], then maxima and totals [heads][S][R].
+  const unsigned pbytes = (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 130u * 4u;
+  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(a.pacc, pbytes);
+  const unsigned mbase = (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 512u;  // bytes to maxima
+  const unsigned lbase = mbase + (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 4u;
+  const unsigned pb = ((unsigned)head * (unsigned)a.splits + (unsigned)part) * (unsigned)a.R;
+  if (start < end) {
+    for (int idx = threadIdx.x; idx < items; idx += 256) {
+      const int r = idx >> 5, d4 = (idx & 31) * 4;
+      float M, L;
+      const f32x4 A = wg_result(r, d4, M, L);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, A), rs, (int)(((pb + r) * 128u + d4) * 4u), 0,
+                                             kSc1);
+      if (d4 == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), rs, (int)(mbase + (pb + r) * 4u), 0, kSc1);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), rs, (int)(lbase + (pb + r) * 4u), 0, kSc1);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&a.tickets[head], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == a.splits - 1;
+    if (s_last) __hip_atomic_store(&a.tickets[head], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const int live = end > 0 ? min(a.splits, (end + chunk - 1) / chunk) : 0;
+  const unsigned hb0 = (unsigned)head * (unsigned)a.splits * (unsigned)a.R;
+  // ng thread groups share an item's splits (contiguous ranges); each thread issues the loads of
+  // a batch of up to 16 splits at once (maxima, totals, accumulators: one memory round trip),
+  // merges them, and the groups' results combine in group order through LDS.
+  const int ng = items >= 256 ? 1 : 256 / items;
+  const int per = (live + ng - 1) / ng;
+  const int slots = items * ng;
+  f32x4* ga = reinterpret_cast<f32x4*>(wacc);
+  float* gm = wacc + 4 * slots;
+  float* gl = gm + slots;
+  for (int w0 = threadIdx.x; w0 < slots; w0 += 256) {
+    const int item = w0 % items, sg = w0 / items;
+    const int r = item >> 5, d4 = (item & 31) * 4;
+    const int s_lo = sg * per, s_hi = min(live, s_lo + per);
+    float Mt = kNegInf, Lt = 0.f;
+    f32x4 At = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = s_lo; b0 < s_hi; b0 += 16) {
+      float mv[16], lv[16];
+      u32x4 av[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const unsigned o = hb0 + (unsigned)min(b0 + j, s_hi - 1) * a.R + r;
+        mv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(mbase + o * 4u), 0, kSc1));
+        lv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(lbase + o * 4u), 0, kSc1));
+        av[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((o * 128u + d4) * 4u), 0, kSc1);
+      }
+      float Mb = Mt;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (b0 + j < s_hi) Mb = fmaxf(Mb, mv[j]);
+      const float Mu = Mb == kNegInf ? 0.f : Mb;
+      const float c = Mt == kNegInf ? 0.f : ex2(Mt - Mu);
+      At *= c;
+      Lt *= c;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (b0 + j >= s_hi || mv[j] == kNegInf) continue;
+        const float f = ex2(mv[j] - Mu);
+        At += f * __builtin_bit_cast(f32x4, av[j]);
+        Lt += f * lv[j];
+      }
+      Mt = Mb;
+    }
+    ga[w0] = At;
+    gm[w0] = Mt;
+    gl[w0] = Lt;
+  }
+  __syncthreads();
+  for (int item = threadIdx.x; item < items; item += 256) {
+    float M = kNegInf;
+    for (int g2 = 0; g2 < ng; ++g2) M = fmaxf(M, gm[g2 * items + item]);
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+    for (int g2 = 0; g2 < ng; ++g2) {
+      const float mg = gm[g2 * items + item];
+      if (mg == kNegInf) continue;
+      const float f = ex2(mg - M);
+      A += f * ga[g2 * items + item];
+      L += f * gl[g2 * items + item];
+    }
+    store_out(item >> 5, (item & 31) * 4, A, L);
+  }
+}
+
+template <int RT, bool Q8>
+static int launch_attn(const AttnArgs& a, int heads, hipStream_t st) {
+  // wave partials [4][R][128], later the merge's group results (6 floats per slot)
+  const size_t items = (size_t)a.R * 32, slots = items >= 256 ? items : 256;
+  const size_t lds = std::max((size_t)4 * a.R * 128, 6 * slots) * sizeof(float);
+  attn_kernel<RT, Q8><<<dim3(heads, a.splits), 256, lds, st>>>(a);
+  QLX_LAUNCH_CHECK("decode attention");
+}
+
+}  // namespace qlx
+
+using namespace qlx;
+
+extern "C" int qlx_attention_workspace(int batch, int n_kv, int group, int tokens, int splits, size_t* bytes) {
+  QLX_REQUIRE(bytes != nullptr, "attention workspace: null size pointer");
+  QLX_REQUIRE(batch > 0 && n_kv > 0 && group > 0 && tokens > 0 && splits > 0, "attention workspace: sizes must be positive");
+  const size_t heads = (size_t)batch * n_kv, rows = (size_t)tokens * group;
+  // tickets first (zeroed by the caller once; every launch leaves them zero), then the partials
+  const size_t tick = (heads * sizeof(int) + 255) & ~(size_t)255;
+  *bytes = splits == 1 ? 0 : tick + heads * splits * rows * (128 + 2) * sizeof(float);
+  return QLX_OK;
+}
+
+extern "C" int qlx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+                                    const float* v_scale, const int* pos, void* out, void* workspace,
+                                    size_t workspace_bytes, int batch, int n_kv, int group, int head_dim, int tokens,
+                                    int capacity, int splits, float scale, void* stream) {
+  QLX_REQUIRE(head_dim == 128, "decode attention: head_dim must be 128 (got %d)", head_dim);
+  QLX_REQUIRE(batch > 0 && n_kv > 0 && group > 0 && tokens > 0 && capacity > 0, "decode attention: sizes must be positive");
+  QLX_REQUIRE(tokens * group <= 64, "decode attention: tokens x group must be <= 64 (got %d)", tokens * group);
+  QLX_REQUIRE(splits >= 1 && splits <= 256, "decode attention: splits must be in 1..256 (got %d)", splits);
+  QLX_REQUIRE(q && k_cache && v_cache && pos && out, "decode attention: null pointer");
+  QLX_REQUIRE((k_scale == nullptr) == (v_scale == nullptr), "decode attention: give both scales or neither");
+  QLX_REQUIRE((size_t)batch * n_kv * capacity * 128 < (1ull << 40), "decode attention: cache too large");
+  size_t need = 0;
+  qlx_attention_workspace(batch, n_kv, group, tokens, splits, &need);
+  QLX_REQUIRE(splits == 1 || (workspace != nullptr && workspace_bytes >= need),
+              "decode attention: workspace of %zu bytes needed for %d splits", need, splits);
+  AttnArgs a{};
+  a.q = reinterpret_cast<const uint16_t*>(q);
+  a.k = k_cache;
+  a.v = v_cache;
+  a.ks = k_scale;
+  a.vs = v_scale;
+  a.pos = pos;
+  a.out = reinterpret_cast<uint16_t*>(out);
+  const int heads = batch * n_kv;
+  a.R = tokens * group;
+  a.heads = heads;
+  QLX_REQUIRE(need < (1ull << 31), "decode attention: split workspace beyond 2 GiB (%zu bytes)", need);
+  if (splits > 1) {
+    const size_t tick = ((size_t)heads * sizeof(int) + 255) & ~(size_t)255;
+    char* ws = reinterpret_cast<char*>(workspace);
+    a.tickets = reinterpret_cast<int*>(ws);
+    a.pacc = reinterpret_cast<float*>(ws + tick);
+    a.pm = a.pacc + (size_t)heads * splits * a.R * 128;
+    a.pl = a.pm + (size_t)heads * splits * a.R;
+  }
+  a.scale2 = scale * 1.4426950408889634f;
+  a.cap = capacity;
+  a.splits = splits;
+  a.T = tokens;
+  a.G = group;
+  a.H = n_kv;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool q8 = k_scale != nullptr;
+  const int rt = (a.R + 15) / 16;
+  switch (rt) {
+    case 1: return q8 ? launch_attn<1, true>(a, heads, st) : launch_attn<1, false>(a, heads, st);
+    case 2: return q8 ? launch_attn<2, true>(a, heads, st) : launch_attn<2, false>(a, heads, st);
+    case 3: return q8 ? launch_attn<3, true>(a, heads, st) : launch_attn<3, false>(a, heads, st);
+    default: return q8 ? launch_attn<4, true>(a, heads, st) : launch_attn<4, false>(a, heads, st);
+  }
+}

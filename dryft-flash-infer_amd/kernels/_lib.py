@@ -62,6 +62,20 @@ class StreamLaunch(ctypes.Structure):
                 ("layout_words", ctypes.c_int), ("layout", ctypes.c_int * 32)]
 
 
+class RopeArgs(ctypes.Structure):
+    """``qlx_rope_args``: the fused QKV head-norm + RoPE + cache write."""
+
+    _fields_ = [("qkv", ctypes.c_void_p), ("planes", ctypes.c_void_p), ("stride", ctypes.c_longlong),
+                ("splits", ctypes.c_int), ("rows", ctypes.c_int), ("n_q", ctypes.c_int), ("n_kv", ctypes.c_int),
+                ("q_col", ctypes.c_int), ("k_col", ctypes.c_int), ("v_col", ctypes.c_int),
+                ("seq_len", ctypes.c_int), ("capacity", ctypes.c_int), ("table_rows", ctypes.c_int),
+                ("pos_int64", ctypes.c_int), ("eps", ctypes.c_float),
+                ("q_norm_w", ctypes.c_void_p), ("k_norm_w", ctypes.c_void_p), ("cos", ctypes.c_void_p),
+                ("sin", ctypes.c_void_p), ("positions", ctypes.c_void_p), ("q_out", ctypes.c_void_p),
+                ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("k_copy", ctypes.c_void_p), ("v_copy", ctypes.c_void_p)]
+
+
 _P, _I, _F, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
 _PLAN = ctypes.POINTER(Plan)
 _PI, _PLL = ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_longlong)
@@ -110,6 +124,10 @@ SIGNATURES = {
                          _I),
     "qlx_stream_run": ([_I, _P, ctypes.POINTER(StreamLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
+    "qlx_qkv_norm_rope": ([ctypes.POINTER(RopeArgs), _P], _I),
+    "qlx_attention_workspace": ([_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_size_t)], _I),
+    "qlx_decode_attention": ([_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+                             _I),
 }
 
 _lib = None

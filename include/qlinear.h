@@ -20,6 +20,7 @@
 #ifndef QLINEAR_H
 #define QLINEAR_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -385,6 +386,60 @@ int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, co
  * epoch). */
 int qlx_stream_run(int fmt, const void* desc, const qlx_stream_launch* launch, unsigned epoch, int* error,
                    long long budget_us, void* stream);
+
+/* ---- QKV consumer and decode attention ----------------------------------------------- */
+
+/* Arguments of qlx_qkv_norm_rope. Head dim is 128. Row r of the projection is token
+ * r % seq_len of sequence r / seq_len; that token's position is positions[r % seq_len]. */
+typedef struct qlx_rope_args {
+  const void* qkv;        /* bf16 [rows][stride], or NULL when planes are given */
+  const float* planes;    /* fp32 split-K planes [splits][rows][stride], or NULL */
+  long long stride;       /* row width of qkv / planes, elements (multiple of 8) */
+  int splits;
+  int rows;
+  int n_q;                /* Q heads normed and rotated into q_out (0: none) */
+  int n_kv;               /* K heads normed, rotated and cached, V heads cached (0: none) */
+  int q_col, k_col, v_col;/* column of head 0 of Q, K and V (multiples of 8) */
+  int seq_len;
+  int capacity;           /* cache slots per (sequence, KV head) */
+  int table_rows;         /* rows of cos / sin */
+  int pos_int64;          /* positions are int64 (else int32) */
+  float eps;
+  const void* q_norm_w;   /* bf16 [128] */
+  const void* k_norm_w;   /* bf16 [128] */
+  const void* cos;        /* bf16 [table_rows][128] */
+  const void* sin;
+  const void* positions;  /* [seq_len] */
+  void* q_out;            /* bf16 [rows][n_q * 128] */
+  void* k_cache;          /* bf16, or int8 with scales, [batch][n_kv][capacity][128] */
+  void* v_cache;
+  float* k_scale;         /* fp32 [batch][n_kv][capacity]: INT8 cache when non-NULL */
+  float* v_scale;
+  void* k_copy;           /* bf16 [batch][n_kv][seq_len][128] or NULL (prefill's SDPA input) */
+  void* v_copy;
+} qlx_rope_args;
+
+/* Per-head RMSNorm + RoPE of Q and K, V copied, K/V written to cache slot positions[t]:
+ * engine/kernels/rope.py:221-240 (qkv_norm_rope_to_cache), :200-218 (the split-K planes form),
+ * :243-263 (q_norm_rope: n_kv = 0) and :266-297 (kv_norm_rope_to_cache: n_q = 0). One launch.
+ * A position outside [0, table_rows) writes NaN to that row's Q heads and nothing to the
+ * cache, as does one outside [0, capacity) for the cache. */
+int qlx_qkv_norm_rope(const qlx_rope_args* args, void* stream);
+
+/* Workspace bytes qlx_decode_attention needs for `splits` > 1 (0 for one split): ticket
+ * counters (zero them once; every call leaves them zero) and the per-split partials. */
+int qlx_attention_workspace(int batch, int n_kv, int group, int tokens, int splits, size_t* bytes);
+
+/* Grouped-query decode attention: engine/kernels/attention.py:282-315 (DecodeAttention.__call__,
+ * the split and merge kernels :37-178) in one launch. q bf16 [batch * tokens][n_kv * group *
+ * 128]; caches [batch][n_kv][capacity][128] bf16, or int8 with fp32 scales [batch][n_kv]
+ * [capacity]; pos (int32, device) is token 0's position: token t attends to keys 0 .. pos + t.
+ * out bf16 like q. The live length is divided among `splits` workgroups per KV head on the
+ * device, so the grid is fixed (capturable). tokens * group <= 64, head_dim 128. */
+int qlx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+                         const float* v_scale, const int* pos, void* out, void* workspace, size_t workspace_bytes,
+                         int batch, int n_kv, int group, int head_dim, int tokens, int capacity, int splits,
+                         float scale, void* stream);
 
 /* ---- measurement ------------------------------------------------------------------- */
 
