@@ -20,9 +20,12 @@
 // weighted accumulators over sum of weighted totals; the merge runs in the workgroup that
 // finishes a head last (a ticket), not in a second launch.
 //
-// Splits are a parallelism knob, not a fixed key range: the live length `end` = pos + tokens
-// is read on the device and divided into `splits` chunks of whole 32-key blocks, so every
-// workgroup has work whatever the capacity, and the grid stays fixed for graph capture.
+// Splits are a parallelism knob, not a fixed key range: 32-key blocks are dealt round-robin
+// (block j to split j % S, then to wave (j / S) % 4), so the live blocks -- the live length
+// pos + tokens is read on the device -- spread over the splits whatever the capacity, a
+// wave's first block can be fetched before the position arrives, and the grid stays fixed for
+// graph capture. A short context uses fewer splits (one block per wave at least); with one,
+// the workgroup writes the output itself.
 #include "common.h"
 #include "../../include/qlinear.h"
 
@@ -86,20 +89,25 @@ template <>
 struct KVBlock<false> {
   u32x4 k[2][4];  // [key tile][k-step]: 8 dims of key 16 kt + n
   u32x4 v[8];     // [slot]: V[key(slot)][8 n .. 8 n + 7]
-  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int stop, int n, int g) {
+  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int kcap, int n, int g) {
     const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + hb;
     const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + hb;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const int key = min(kb + 16 * kt + n, stop - 1);
+      const int key = min(kb + 16 * kt + n, kcap - 1);
 #pragma unroll
       for (int s = 0; s < 4; ++s) k[kt][s] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + kdim<false>(s, g)));
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int key = min(kb + slot_key(g, j), stop - 1);
+      const int key = min(kb + slot_key(g, j), kcap - 1);
       v[j] = *gmem(reinterpret_cast<const u32x4*>(V + (size_t)key * 128 + 8 * n));
     }
+  }
+  __device__ __forceinline__ void zero_from(int kb, int end, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (kb + slot_key(g, j) >= end) v[j] = u32x4{0u, 0u, 0u, 0u};
   }
   __device__ __forceinline__ u32x4 kfrag(int kt, int s) const { return k[kt][s]; }
   // Column c (0..7) of the lane's 8 keys x 8 dims block: 8 keys of dim 8 n + c, slot order.
@@ -122,23 +130,31 @@ struct KVBlock<true> {
   u32x4 k[2][2];  // [key tile][half]: dims 32 g .. 32 g + 31 of key 16 kt + n
   u32x2 v[8];     // [slot]: codes of V[key(slot)][8 n .. 8 n + 7]
   float ksc[2], vsc[8];
-  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int stop, int n, int g) {
+  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int kcap, int n, int g) {
     const int8_t* K = reinterpret_cast<const int8_t*>(a.k) + hb;
     const int8_t* V = reinterpret_cast<const int8_t*>(a.v) + hb;
     const size_t sb = hb >> 7;  // scale index of key 0 of this head
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const int key = min(kb + 16 * kt + n, stop - 1);
+      const int key = min(kb + 16 * kt + n, kcap - 1);
       k[kt][0] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g));
       k[kt][1] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g + 16));
       ksc[kt] = gmem(a.ks)[sb + key];
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int key = min(kb + slot_key(g, j), stop - 1);
+      const int key = min(kb + slot_key(g, j), kcap - 1);
       v[j] = *gmem(reinterpret_cast<const u32x2*>(V + (size_t)key * 128 + 8 * n));
       vsc[j] = gmem(a.vs)[sb + key];
     }
+  }
+  __device__ __forceinline__ void zero_from(int kb, int end, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (kb + slot_key(g, j) >= end) {
+        v[j] = u32x2{0u, 0u};
+        vsc[j] = 0.f;
+      }
   }
   static __device__ __forceinline__ float deq(uint32_t w, int b, float sc) {
     return round_bf((float)(int)(int8_t)(w >> (8 * b)) * sc);
@@ -168,17 +184,20 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   __shared__ float wm[4][64], wl[4][64];
   __shared__ int s_last;
   const int head = blockIdx.x, part = blockIdx.y;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index and position in scalar registers: block bounds and loop trips are wave-uniform
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = head / a.H, kvh = head - seq * a.H;
   const int NQ = a.H * a.G;
-  const int base = a.pos[0];
-  const int end = min(base + a.T, a.cap);  // keys at or past end are live for no row
-  // at least one 32-key block per wave, so a short context does not spread over idle splits
-  const int chunk = end > 0 ? max(128, ((end + a.splits - 1) / a.splits + 31) & ~31) : 128;
-  const int start = part * chunk;
-  const int stop = min(start + chunk, end);
   const size_t hb = (size_t)head * a.cap * 128;
+  // Key blocks of 32 are dealt round-robin: block j to split j % S, and within the split to
+  // wave (j / S) % 4. A wave's first block is then known before the position is: its K/V loads
+  // (clamped to the capacity, always valid memory) and the query loads go out at entry, and
+  // the position read overlaps them.
+  const int j0 = part + a.splits * w;
+  constexpr bool PF = RT <= 2;  // prefetch the next block (registers allow it up to 2 row tiles)
+  KVBlock<Q8> cur, nxt;
+  if (PF && 32 * j0 < a.cap) cur.load(a, hb, 32 * j0, a.cap, n, g);
 
   // Query fragments (B operand of S^T = K Q^T): row 16 rt + n, dims kdim(s, g). Up to two row
   // tiles live in registers; more are read from LDS each block (the four waves share them),
@@ -206,12 +225,23 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
     if constexpr (QLDS) return qlds[(rt * 4 + s) * 64 + lane];
     else return qf[rt][s];
   };
-  // Last live key + 1 of row 16 rt + n (padding rows: every key of the split).
+  const int base = __builtin_amdgcn_readfirstlane(a.pos[0]);
+  const int end = min(base + a.T, a.cap);  // keys at or past end are live for no row
+  const int nblk = end > 0 ? (end + 31) >> 5 : 0;
+  // Splits in use: at least one block per wave each (a short context on many splits would
+  // only add partials and ticket traffic). Workgroups past them leave now; when fewer splits
+  // are used than launched, waves past the first fetch their first block again.
+  const int se = max(1, min(a.splits, (nblk + 3) >> 2));
+  if (part >= se) return;
+  const int j1 = part + se * w, jstep1 = 4 * se;
+  const int nb = j1 < nblk ? (nblk - j1 + jstep1 - 1) / jstep1 : 0;  // this wave's blocks
+  if (PF && j1 != j0 && nb > 0) cur.load(a, hb, 32 * j1, a.cap, n, g);
+  // Last live key + 1 of row 16 rt + n (padding rows: every live key).
   int lim[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int r = 16 * rt + n;
-    lim[rt] = r < a.R ? min(base + r / a.G + 1, stop) : stop;
+    lim[rt] = r < a.R ? min(base + r / a.G + 1, end) : end;
   }
 
   float m[RT], l[RT];
@@ -279,38 +309,39 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
     }
   };
 
-  // The wave's blocks start + 32 (w + 4 i). With up to two row tiles the next block's loads
-  // are issued before the current block is computed.
-  int kb = start + 32 * w;
-  if constexpr (RT <= 2) {
-    if (kb < stop) {
-      KVBlock<Q8> cur, nxt;
-      cur.load(a, hb, kb, stop, n, g);
-      for (;;) {
-        const int kn = kb + 128;
-        if (kn < stop) {
-          nxt.load(a, hb, kn, stop, n, g);
-          compute(cur, kb);
-          kb = kn;
-          const int k2 = kb + 128;
-          if (k2 < stop) {
-            cur.load(a, hb, k2, stop, n, g);
-            compute(nxt, kb);
-            kb = k2;
-            continue;
-          }
-          compute(nxt, kb);
-          break;
-        }
-        compute(cur, kb);
-        break;
+  // The last block may run past `end`: its values there are zeroed (P is 0 there, and 0 times
+  // whatever the cache holds past the live keys could be NaN).
+  auto run = [&](KVBlock<Q8>& b, int j) __attribute__((always_inline)) {
+    const int kb = 32 * j;
+    if (kb + 32 > end) b.zero_from(kb, end, g);
+    compute(b, kb);
+  };
+  if constexpr (PF) {
+    if (nb > 0) {
+      int i = 0;
+      // (sched_barrier: the scheduler would otherwise sink the prefetch below the first
+      // products of the current block, behind a wait for every load in flight)
+      for (; i + 2 < nb; i += 2) {
+        nxt.load(a, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
+        __builtin_amdgcn_sched_barrier(0);
+        run(cur, j1 + jstep1 * i);
+        cur.load(a, hb, 32 * (j1 + jstep1 * (i + 2)), a.cap, n, g);
+        __builtin_amdgcn_sched_barrier(0);
+        run(nxt, j1 + jstep1 * (i + 1));
+      }
+      if (i + 1 < nb) {
+        nxt.load(a, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
+        __builtin_amdgcn_sched_barrier(0);
+        run(cur, j1 + jstep1 * i);
+        run(nxt, j1 + jstep1 * (i + 1));
+      } else {
+        run(cur, j1 + jstep1 * i);
       }
     }
   } else {
-    for (; kb < stop; kb += 128) {
-      KVBlock<Q8> cur;
-      cur.load(a, hb, kb, stop, n, g);
-      compute(cur, kb);
+    for (int i = 0; i < nb; ++i) {
+      cur.load(a, hb, 32 * (j1 + jstep1 * i), a.cap, n, g);
+      run(cur, j1 + jstep1 * i);
     }
   }
 
@@ -367,7 +398,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
     *gmem(reinterpret_cast<u32x2*>(o)) = u32x2{pack_bf(A[0] / L, A[1] / L), pack_bf(A[2] / L, A[3] / L)};
   };
   const int items = a.R * 32;
-  if (a.splits == 1) {
+  if (se == 1) {
     for (int idx = threadIdx.x; idx < items; idx += 256) {
       const int r = idx >> 5, d4 = (idx & 31) * 4;
       float M, L;
@@ -385,7 +416,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   const unsigned mbase = (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 512u;  // bytes to maxima
   const unsigned lbase = mbase + (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 4u;
   const unsigned pb = ((unsigned)head * (unsigned)a.splits + (unsigned)part) * (unsigned)a.R;
-  if (start < end) {
+  {
     for (int idx = threadIdx.x; idx < items; idx += 256) {
       const int r = idx >> 5, d4 = (idx & 31) * 4;
       float M, L;
@@ -403,13 +434,13 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&a.tickets[head], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == a.splits - 1;
+    s_last = prev == se - 1;
     if (s_last) __hip_atomic_store(&a.tickets[head], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  const int live = end > 0 ? min(a.splits, (end + chunk - 1) / chunk) : 0;
+  const int live = se;
   const unsigned hb0 = (unsigned)head * (unsigned)a.splits * (unsigned)a.R;
   // ng thread groups share an item's splits (contiguous ranges); each thread issues the loads of
   // a batch of up to 16 splits at once (maxima, totals, accumulators: one memory round trip),
