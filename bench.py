@@ -410,6 +410,88 @@ def measure_config4(reps, layers=LAYERS):
     return out
 
 
+#: Decode attention cases (Qwen3-4B: 8 KV heads x 4 query heads, head_dim 128): batch, cache
+#: capacity, live keys. Batch 32 at 576 keys is config 5's last step (prompt 512 + 64 tokens).
+ATTENTION_CASES = ((1, 4096, 4096), (1, 32768, 32768), (32, 640, 576))
+
+
+def measure_attention(reps=10):
+    """The QKV consumer and decode attention of a Qwen3-4B decode step (the path after qkv):
+    ``qkv_norm_rope_to_cache`` at 1 and 32 rows, and ``DecodeAttention`` at ATTENTION_CASES.
+    Each is replayed over enough distinct caches (up to one per layer) to cover >= 1 GiB, so
+    the Infinity Cache serves nothing hot. Algorithmic bytes of attention: the live K and V
+    (live x 8 heads x 128 x 2 bytes each, per sequence) plus q in and the output."""
+    import math
+    from kernels import DecodeAttention, qkv_norm_rope_to_cache
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    out = {}
+    for batch, cap, live in ATTENTION_CASES:
+        per_layer = batch * 8 * cap * 128 * 2 * 2
+        n = min(LAYERS, max(1, math.ceil((1 << 30) / per_layer)))
+        caches = [(torch.randn(batch, 8, cap, 128, generator=gen, device="cuda").bfloat16(),
+                   torch.randn(batch, 8, cap, 128, generator=gen, device="cuda").bfloat16()) for _ in range(n)]
+        q = torch.randn(batch, 32 * 128, generator=gen, device="cuda").bfloat16()
+        pos = torch.tensor([live - 1], dtype=torch.int32, device="cuda")
+        att = DecodeAttention(batch, 8, 4, 128, cap, "cuda")
+
+        def run():
+            for k, v in caches:
+                att(q, k, v, pos)
+        g = graph_of(run)
+        us = median_graph_ms(g, reps, 2, trials=3) / n * 1e3
+        del g
+        alg = batch * 8 * live * 128 * 2 * 2 + 2 * q.numel() * 2
+        key = f"B{batch}_ctx{live}"
+        out[key] = {"us": round(us, 2), "alg_MB": round(alg / 1e6, 3), "GBps": round(alg / us / 1e3, 1),
+                    "hbm_frac": round(alg / us / 1e3 / (PEAK_HBM / 1e9), 4), "splits": att.splits,
+                    "kernel": f"attn_kernel<1, false> (grid {batch * 8} x {att.splits})"}
+        log(f"decode attention batch {batch}, {live} live keys: {us:.2f} us, {alg / us / 1e3:.0f} GB/s "
+            f"({att.splits} splits)")
+        del caches
+        torch.cuda.empty_cache()
+    # The reference's CPU path for the same call (engine/engine.py:988-1005, its fallback: the
+    # group's query heads as query positions against the whole cache with a live-key mask),
+    # torch on the host cores, batch 1 at 4096 keys, median of 5 after 2.
+    import torch.nn.functional as F
+    kc = torch.randn(1, 8, 4096, 128).bfloat16()
+    vc = torch.randn(1, 8, 4096, 128).bfloat16()
+    qc = torch.randn(1, 8, 4, 128).bfloat16()
+    mask = torch.ones(4096, dtype=torch.bool)
+    times = []
+    for i in range(7):
+        t0 = time.perf_counter()
+        F.scaled_dot_product_attention(qc, kc, vc, attn_mask=mask.view(1, 1, 1, -1))
+        if i >= 2:
+            times.append(time.perf_counter() - t0)
+    out["cpu_baseline_B1_ctx4096"] = {"us": round(statistics.median(times) * 1e6, 1), "kind": "port",
+                                      "cores": torch.get_num_threads(),
+                                      "sample": "torch CPU scaled_dot_product_attention as the reference's fallback "
+                                                "calls it, batch 1, 4096 keys, median of 5 after 2"}
+    for rows in (1, 32):
+        cap = 1024
+        n = LAYERS
+        qkv = torch.randn(rows, 6144, generator=gen, device="cuda").bfloat16()
+        qn = torch.randn(128, generator=gen, device="cuda").bfloat16()
+        kn = torch.randn(128, generator=gen, device="cuda").bfloat16()
+        ang = torch.randn(cap, 128, generator=gen, device="cuda")
+        cos, sin = ang.cos().bfloat16(), ang.sin().bfloat16()
+        positions = torch.tensor([700], dtype=torch.int32, device="cuda")
+        caches = [(torch.zeros(rows, 8, cap, 128, device="cuda", dtype=torch.bfloat16),
+                   torch.zeros(rows, 8, cap, 128, device="cuda", dtype=torch.bfloat16)) for _ in range(n)]
+
+        def run():
+            for k, v in caches:
+                qkv_norm_rope_to_cache(qkv, 32, 8, qn, kn, cos, sin, positions, 1, k, v, 1e-6)
+        g = graph_of(run)
+        us = median_graph_ms(g, reps, 2, trials=3) / n * 1e3
+        del g, caches
+        alg = rows * (6144 + 4096 + 2048) * 2 + 2 * 256 * 2
+        out[f"norm_rope_rows{rows}"] = {"us": round(us, 2), "alg_KB": round(alg / 1e3, 1)}
+        log(f"qkv head norm + RoPE + cache write, {rows} rows: {us:.2f} us")
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,6 +504,9 @@ def main():
     ap.add_argument("--only-config4", action="store_true",
                     help="only BASELINE config 4 (W4 gate_up+SwiGLU then down, M = 16, 32, 64): one JSON line "
                          "of its figures, for profiling the skinny GEMM (not the driver's line)")
+    ap.add_argument("--only-attention", action="store_true",
+                    help="only the QKV consumer and decode attention figures: one JSON line, for profiling "
+                         "(not the driver's line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
@@ -435,6 +520,10 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.only_config4:
         print(json.dumps({"config4_w4_gate_up_swiglu_down": measure_config4(max(3, args.steps // 4))}), flush=True)
+        return
+    if args.only_attention:
+        print(json.dumps({"qkv_consumer_and_decode_attention": measure_attention(max(3, args.steps // 2))}),
+              flush=True)
         return
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
@@ -510,6 +599,7 @@ def main():
             torch.cuda.empty_cache()
         extra["per_projection_single_calls"] = per_cfg
         extra["config4_w4_gate_up_swiglu_down"] = measure_config4(max(3, args.steps // 4))
+        extra["qkv_consumer_and_decode_attention"] = measure_attention(max(3, args.steps // 2))
 
     line = {
         "metric": METRIC,
