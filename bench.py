@@ -226,20 +226,28 @@ def untile(tiled):
 
 
 def cpu_model_name():
-    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
-    import subprocess
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for ln in out.splitlines():
-            if ln.startswith("Model name:"):
-                return ln.split(":", 1)[1].strip()
-    except (OSError, subprocess.SubprocessError):
-        pass
+    """The host CPU's model name with its family / model / stepping numbers (/proc/cpuinfo;
+    a virtual machine may report only a short name such as "AMD EPYC"), else lscpu's."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
-            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+            for ln in f:
+                if not ln.strip():
+                    break  # first processor only
+                key, _, val = ln.partition(":")
+                fields[key.strip()] = val.strip()
     except OSError:
-        return platform.processor()
+        pass
+    name = fields.get("model name", "")
+    if not name:
+        import subprocess
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            name = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name:")), "")
+        except (OSError, subprocess.SubprocessError):
+            name = platform.processor()
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_baseline(stack, reps=5, warmup=2):

@@ -244,3 +244,51 @@ def test_stream_norm_stage_contract_on_host():
     assert build(3, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
     odd = _lib.StackCall(W, S, None, 1 << 36, 256, 2304, _lib.MODE_BF16, 0)
     assert build(1, [odd], [_lib.NormInput(R, None, NW, None, None, 1e-6, 0)]) == _lib.QLX_EINVAL
+
+
+def test_qkv_consumer_and_attention_contract_on_host():
+    """The rope and attention entry points reject bad arguments before any launch; the Python
+    ops keep the reference's names and refuse CPU tensors; plan_splits follows its rule."""
+    import ctypes
+    from kernels import _lib, attention, rope
+    import kernels
+    lib = _lib.lib()
+    a = _lib.RopeArgs()
+    a.rows, a.n_q, a.n_kv, a.seq_len, a.stride = 2, 32, 8, 3, 6144   # rows not a multiple of seq_len
+    assert lib.qlx_qkv_norm_rope(ctypes.byref(a), None) == _lib.QLX_EINVAL and "seq_len" in _lib.last_error()
+    a.seq_len, a.qkv, a.planes = 1, 1 << 20, 1 << 20                   # both inputs given
+    assert lib.qlx_qkv_norm_rope(ctypes.byref(a), None) == _lib.QLX_EINVAL
+    a.planes, a.cos, a.sin, a.positions, a.table_rows = None, 1 << 20, 1 << 20, 1 << 20, 8
+    a.q_out, a.q_norm_w, a.k_norm_w, a.k_cache, a.v_cache, a.capacity = (1 << 20,) * 5 + (8,)
+    a.q_col, a.k_col, a.v_col = 0, 4096, 5120
+    a.stride = 6000                                                     # V heads past the row
+    assert lib.qlx_qkv_norm_rope(ctypes.byref(a), None) == _lib.QLX_EINVAL and "columns" in _lib.last_error()
+    a.stride, a.k_scale = 6144, 1 << 20                                 # one cache scale only
+    assert lib.qlx_qkv_norm_rope(ctypes.byref(a), None) == _lib.QLX_EINVAL
+    size = ctypes.c_size_t()
+    assert lib.qlx_attention_workspace(1, 8, 4, 1, 1, ctypes.byref(size)) == 0 and size.value == 0
+    assert lib.qlx_attention_workspace(2, 8, 4, 3, 16, ctypes.byref(size)) == 0
+    assert size.value >= 2 * 8 * 16 * 12 * 130 * 4 + 2 * 8 * 4
+    p = 1 << 20
+    args = [p, p, p, None, None, p, p, None, 0, 1, 8, 4, 128, 1, 4096, 16, 0.088, None]
+    assert lib.qlx_decode_attention(*args) == _lib.QLX_EINVAL and "workspace" in _lib.last_error()
+    args[12] = 64                                                        # head_dim
+    assert lib.qlx_decode_attention(*args) == _lib.QLX_EINVAL and "head_dim" in _lib.last_error()
+    args[12], args[13] = 128, 17                                         # 17 tokens x 4 > 64 rows
+    assert lib.qlx_decode_attention(*args) == _lib.QLX_EINVAL
+    args[13], args[3] = 1, p                                             # k_scale without v_scale
+    assert lib.qlx_decode_attention(*args) == _lib.QLX_EINVAL
+
+    for name in ("DecodeAttention", "qkv_norm_rope_to_cache", "qkv_planes_norm_rope_to_cache", "q_norm_rope",
+                 "kv_norm_rope_to_cache"):
+        assert hasattr(kernels, name), name
+    assert hasattr(attention, "plan_splits") and hasattr(attention.DecodeAttention, "tuned")
+    # plan_splits: double while the grid is under one workgroup per CU and a split keeps >= 128 keys
+    assert attention.plan_splits(4096, 1, 8) == (32, 128) and attention.plan_splits(32768, 1, 8) == (32, 1024)
+    assert attention.plan_splits(640, 32, 8) == (1, 640) and attention.plan_splits(640, 1, 8) == (4, 160)
+    assert attention.plan_splits(100000, 1, 1)[0] == 64
+    qkv = torch.randn(1, 6144).to(torch.bfloat16)
+    cos = torch.randn(8, 128).to(torch.bfloat16)
+    pos = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        rope.q_norm_rope(qkv, 32, torch.ones(128, dtype=torch.bfloat16), cos, cos, pos, 1, 1e-6)
