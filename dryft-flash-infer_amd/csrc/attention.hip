@@ -17,8 +17,10 @@
 // row total summed from fp32 p, the P V product from bf16 p, acc / total at the end
 // (attention.py:102-137). Exponentials are base 2 on scores pre-multiplied by log2(e).
 // The split partials merge as in attention.py:144-178: weights exp(max_s - max), sum of
-// weighted accumulators over sum of weighted totals; the merge runs in the workgroup that
-// finishes a head last (a ticket), not in a second launch.
+// weighted accumulators over sum of weighted totals, in a small second kernel (one workgroup per
+// head). Merging in the attention launch itself -- the last workgroup of a head, found with a
+// ticket -- measured slower: the partial stores' acknowledgement, the ticket and the merge's
+// loads are three device-scope round trips (6 us of 12.9 at batch 1, 4096 keys, 32 splits).
 //
 // Splits are a parallelism knob, not a fixed key range: 32-key blocks are dealt round-robin
 // (block j to split j % S, then to wave (j / S) % 4), so the live blocks -- the live length
@@ -41,10 +43,7 @@ struct AttnArgs {
   const float* vs;
   const int* pos;      // base position of token 0
   uint16_t* out;       // bf16 [B*T][H*G*128]
-  float* pacc;         // [B*H][S][R][128]
-  float* pm;           // [B*H][S][R]
-  float* pl;           // [B*H][S][R]
-  int* tickets;        // [B*H], zero before and after a launch
+  float* pacc;         // split partials: [B*H][S][R][128], then maxima and totals [B*H][S][R]
   float scale2;        // head_dim^-0.5 * log2(e)
   int cap, splits, T, G, H, R, heads;
 };
@@ -67,16 +66,6 @@ __device__ __forceinline__ int slot_key(int g, int j) { return 16 * (j >> 2) + 4
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 
 __device__ __forceinline__ bf16x8 bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// Buffer resource over `bytes` of device memory (base uniform across the workgroup); loads and
-// stores through it with kSc1 go past this XCD's L2, so another XCD's workgroup sees them.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const void* p, unsigned bytes) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)bytes,
-                                           0x00020000);
-}
-constexpr int kSc1 = 16;
 
 __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
@@ -182,7 +171,6 @@ template <int RT, bool Q8>
 __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   extern __shared__ float wacc[];  // [4 waves][R][128]
   __shared__ float wm[4][64], wl[4][64];
-  __shared__ int s_last;
   const int head = blockIdx.x, part = blockIdx.y;
   // wave index and position in scalar registers: block bounds and loop trips are wave-uniform
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -229,7 +217,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   const int end = min(base + a.T, a.cap);  // keys at or past end are live for no row
   const int nblk = end > 0 ? (end + 31) >> 5 : 0;
   // Splits in use: at least one block per wave each (a short context on many splits would
-  // only add partials and ticket traffic). Workgroups past them leave now; when fewer splits
+  // only add partials and merge work). Workgroups past them leave now; when fewer splits
   // are used than launched, waves past the first fetch their first block again.
   const int se = max(1, min(a.splits, (nblk + 3) >> 2));
   if (part >= se) return;
@@ -408,64 +396,64 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
     return;
   }
 
-  // Several splits: publish this split's partial (splits holding live keys only) with
-  // device-scope stores, take the head's ticket; the last workgroup merges the live splits in
-  // split order. Partials: acc [heads][S][R][128], then maxima and totals [heads][S][R].
-  const unsigned pbytes = (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 130u * 4u;
-  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(a.pacc, pbytes);
-  const unsigned mbase = (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 512u;  // bytes to maxima
-  const unsigned lbase = mbase + (unsigned)a.heads * (unsigned)a.splits * (unsigned)a.R * 4u;
-  const unsigned pb = ((unsigned)head * (unsigned)a.splits + (unsigned)part) * (unsigned)a.R;
-  {
-    for (int idx = threadIdx.x; idx < items; idx += 256) {
-      const int r = idx >> 5, d4 = (idx & 31) * 4;
-      float M, L;
-      const f32x4 A = wg_result(r, d4, M, L);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, A), rs, (int)(((pb + r) * 128u + d4) * 4u), 0,
-                                             kSc1);
-      if (d4 == 0) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), rs, (int)(mbase + (pb + r) * 4u), 0, kSc1);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), rs, (int)(lbase + (pb + r) * 4u), 0, kSc1);
-      }
+  // Several splits: this split's partial goes out with plain stores; the merge kernel that
+  // follows on the stream (the kernel boundary makes them visible) combines the live splits.
+  // Partials: acc [heads][S][R][128], then maxima and totals [heads][S][R].
+  const size_t pb = ((size_t)head * a.splits + part) * a.R;
+  const size_t nslot = (size_t)a.heads * a.splits * a.R;
+  for (int idx = threadIdx.x; idx < items; idx += 256) {
+    const int r = idx >> 5, d4 = (idx & 31) * 4;
+    float M, L;
+    const f32x4 A = wg_result(r, d4, M, L);
+    *gmem(reinterpret_cast<f32x4*>(a.pacc + (pb + r) * 128 + d4)) = A;
+    if (d4 == 0) {
+      gmem(a.pacc)[nslot * 128 + pb + r] = M;
+      gmem(a.pacc)[nslot * 129 + pb + r] = L;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.tickets[head], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == se - 1;
-    if (s_last) __hip_atomic_store(&a.tickets[head], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  const int live = se;
-  const unsigned hb0 = (unsigned)head * (unsigned)a.splits * (unsigned)a.R;
-  // ng thread groups share an item's splits (contiguous ranges); each thread issues the loads of
-  // a batch of up to 16 splits at once (maxima, totals, accumulators: one memory round trip),
-  // merges them, and the groups' results combine in group order through LDS.
+}
+
+// Merge of the split partials of one head (one workgroup per sequence x KV head): the splits in
+// use (se, from the same position) combine as in attention.py:144-178 -- weights
+// exp(max_s - max), weighted accumulators over weighted totals -- in a fixed order. ng thread
+// groups share an item's splits (contiguous ranges); a thread issues the loads of up to 16
+// splits at once (one memory round trip), merges them, and the groups' results combine in group
+// order through LDS. With one split in use the attention kernel wrote the output itself.
+__global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
+  extern __shared__ float gbuf[];  // the groups' results: 6 floats per slot
+  const int head = blockIdx.x;
+  const int seq = head / a.H, kvh = head - seq * a.H;
+  const int NQ = a.H * a.G;
+  const int base = __builtin_amdgcn_readfirstlane(a.pos[0]);
+  const int end = min(base + a.T, a.cap);
+  const int nblk = end > 0 ? (end + 31) >> 5 : 0;
+  const int se = max(1, min(a.splits, (nblk + 3) >> 2));
+  if (se == 1) return;
+  const int items = a.R * 32;
   const int ng = items >= 256 ? 1 : 256 / items;
-  const int per = (live + ng - 1) / ng;
+  const int per = (se + ng - 1) / ng;
   const int slots = items * ng;
-  f32x4* ga = reinterpret_cast<f32x4*>(wacc);
-  float* gm = wacc + 4 * slots;
+  const size_t nslot = (size_t)a.heads * a.splits * a.R;
+  const size_t hb0 = (size_t)head * a.splits * a.R;
+  const float* P = a.pacc;
+  f32x4* ga = reinterpret_cast<f32x4*>(gbuf);
+  float* gm = gbuf + 4 * slots;
   float* gl = gm + slots;
   for (int w0 = threadIdx.x; w0 < slots; w0 += 256) {
     const int item = w0 % items, sg = w0 / items;
     const int r = item >> 5, d4 = (item & 31) * 4;
-    const int s_lo = sg * per, s_hi = min(live, s_lo + per);
+    const int s_lo = sg * per, s_hi = min(se, s_lo + per);
     float Mt = kNegInf, Lt = 0.f;
     f32x4 At = {0.f, 0.f, 0.f, 0.f};
     for (int b0 = s_lo; b0 < s_hi; b0 += 16) {
       float mv[16], lv[16];
-      u32x4 av[16];
+      f32x4 av[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const unsigned o = hb0 + (unsigned)min(b0 + j, s_hi - 1) * a.R + r;
-        mv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(mbase + o * 4u), 0, kSc1));
-        lv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(lbase + o * 4u), 0, kSc1));
-        av[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((o * 128u + d4) * 4u), 0, kSc1);
+        const size_t o = hb0 + (size_t)min(b0 + j, s_hi - 1) * a.R + r;
+        mv[j] = gmem(P)[nslot * 128 + o];
+        lv[j] = gmem(P)[nslot * 129 + o];
+        av[j] = *gmem(reinterpret_cast<const f32x4*>(P + o * 128 + d4));
       }
       float Mb = Mt;
 #pragma unroll
@@ -479,7 +467,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
       for (int j = 0; j < 16; ++j) {
         if (b0 + j >= s_hi || mv[j] == kNegInf) continue;
         const float f = ex2(mv[j] - Mu);
-        At += f * __builtin_bit_cast(f32x4, av[j]);
+        At += f * av[j];
         Lt += f * lv[j];
       }
       Mt = Mb;
@@ -501,16 +489,20 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
       A += f * ga[g2 * items + item];
       L += f * gl[g2 * items + item];
     }
-    store_out(item >> 5, (item & 31) * 4, A, L);
+    const int r = item >> 5, d4 = (item & 31) * 4;
+    const int t = r / a.G, gi = r - t * a.G;
+    uint16_t* o = a.out + ((size_t)(seq * a.T + t) * NQ + kvh * a.G + gi) * 128 + d4;
+    *gmem(reinterpret_cast<u32x2*>(o)) = u32x2{pack_bf(A[0] / L, A[1] / L), pack_bf(A[2] / L, A[3] / L)};
   }
 }
 
 template <int RT, bool Q8>
 static int launch_attn(const AttnArgs& a, int heads, hipStream_t st) {
-  // wave partials [4][R][128], later the merge's group results (6 floats per slot)
-  const size_t items = (size_t)a.R * 32, slots = items >= 256 ? items : 256;
-  const size_t lds = std::max((size_t)4 * a.R * 128, 6 * slots) * sizeof(float);
-  attn_kernel<RT, Q8><<<dim3(heads, a.splits), 256, lds, st>>>(a);
+  attn_kernel<RT, Q8><<<dim3(heads, a.splits), 256, (size_t)4 * a.R * 128 * sizeof(float), st>>>(a);
+  if (a.splits > 1) {
+    const size_t items = (size_t)a.R * 32, slots = items >= 256 ? items : 256;
+    attn_merge_kernel<<<heads, 256, 6 * slots * sizeof(float), st>>>(a);
+  }
   QLX_LAUNCH_CHECK("decode attention");
 }
 
@@ -522,9 +514,8 @@ extern "C" int qlx_attention_workspace(int batch, int n_kv, int group, int token
   QLX_REQUIRE(bytes != nullptr, "attention workspace: null size pointer");
   QLX_REQUIRE(batch > 0 && n_kv > 0 && group > 0 && tokens > 0 && splits > 0, "attention workspace: sizes must be positive");
   const size_t heads = (size_t)batch * n_kv, rows = (size_t)tokens * group;
-  // tickets first (zeroed by the caller once; every launch leaves them zero), then the partials
-  const size_t tick = (heads * sizeof(int) + 255) & ~(size_t)255;
-  *bytes = splits == 1 ? 0 : tick + heads * splits * rows * (128 + 2) * sizeof(float);
+  // the split partials: accumulators [heads][S][R][128], maxima and totals [heads][S][R]
+  *bytes = splits == 1 ? 0 : heads * splits * rows * (128 + 2) * sizeof(float);
   return QLX_OK;
 }
 
@@ -555,14 +546,7 @@ extern "C" int qlx_decode_attention(const void* q, const void* k_cache, const vo
   a.R = tokens * group;
   a.heads = heads;
   QLX_REQUIRE(need < (1ull << 31), "decode attention: split workspace beyond 2 GiB (%zu bytes)", need);
-  if (splits > 1) {
-    const size_t tick = ((size_t)heads * sizeof(int) + 255) & ~(size_t)255;
-    char* ws = reinterpret_cast<char*>(workspace);
-    a.tickets = reinterpret_cast<int*>(ws);
-    a.pacc = reinterpret_cast<float*>(ws + tick);
-    a.pm = a.pacc + (size_t)heads * splits * a.R * 128;
-    a.pl = a.pm + (size_t)heads * splits * a.R;
-  }
+  if (splits > 1) a.pacc = reinterpret_cast<float*>(workspace);
   a.scale2 = scale * 1.4426950408889634f;
   a.cap = capacity;
   a.splits = splits;

@@ -2,11 +2,11 @@
 ``kernels.attention`` (engine/kernels/attention.py:181-318).
 
 ``DecodeAttention`` keeps the reference's constructor, call and ``tuned`` race. The work is
-one HIP launch (``qlx_decode_attention``, csrc/attention.hip): a workgroup per (sequence x KV
-head, split) runs S^T = K Q^T and P V on bf16 MFMA for all ``tokens x group`` query rows of
-its KV head, and the workgroup that finishes a head last merges the splits -- the reference's
-split and merge kernels in one launch. The live length is read from ``pos`` on the device and
-shared among the splits, so the grid is fixed and the call captures into a HIP graph.
+``qlx_decode_attention`` (csrc/attention.hip): a workgroup per (sequence x KV head, split) runs
+S^T = K Q^T and P V on bf16 MFMA for all ``tokens x group`` query rows of its KV head, and with
+several splits a small second kernel merges them, like the reference's split and merge kernels.
+The live length is read from ``pos`` on the device and shared among the splits, so the grids
+are fixed and the call captures into a HIP graph.
 """
 
 import ctypes
@@ -69,8 +69,7 @@ class DecodeAttention:
         self.device = torch.device(device)
         size = ctypes.c_size_t()
         _lib.call("qlx_attention_workspace", batch, n_kv, group, tokens, self.splits, ctypes.byref(size))
-        # tickets must start at zero; every call leaves them zero again
-        self.workspace = torch.zeros(max(size.value, 1), dtype=torch.uint8, device=self.device)
+        self.workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=self.device)
         self.out = torch.empty(batch * tokens, self.n_q * head_dim, dtype=torch.bfloat16, device=self.device)
 
     def __call__(self, q, k_cache, v_cache, pos, k_scale=None, v_scale=None):

@@ -426,16 +426,17 @@ typedef struct qlx_rope_args {
  * cache, as does one outside [0, capacity) for the cache. */
 int qlx_qkv_norm_rope(const qlx_rope_args* args, void* stream);
 
-/* Workspace bytes qlx_decode_attention needs for `splits` > 1 (0 for one split): ticket
- * counters (zero them once; every call leaves them zero) and the per-split partials. */
+/* Workspace bytes qlx_decode_attention needs for `splits` > 1 (0 for one split): the per-split
+ * partials (no initial contents needed). */
 int qlx_attention_workspace(int batch, int n_kv, int group, int tokens, int splits, size_t* bytes);
 
 /* Grouped-query decode attention: engine/kernels/attention.py:282-315 (DecodeAttention.__call__,
- * the split and merge kernels :37-178) in one launch. q bf16 [batch * tokens][n_kv * group *
+ * the split and merge kernels :37-178). q bf16 [batch * tokens][n_kv * group *
  * 128]; caches [batch][n_kv][capacity][128] bf16, or int8 with fp32 scales [batch][n_kv]
  * [capacity]; pos (int32, device) is token 0's position: token t attends to keys 0 .. pos + t.
  * out bf16 like q. The live length is divided among `splits` workgroups per KV head on the
- * device, so the grid is fixed (capturable). tokens * group <= 64, head_dim 128. */
+ * device, so the grid is fixed (capturable); with splits > 1 a second small kernel merges the
+ * partials. Calls sharing a workspace must not overlap. tokens * group <= 64, head_dim 128. */
 int qlx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
                          const float* v_scale, const int* pos, void* out, void* workspace, size_t workspace_bytes,
                          int batch, int n_kv, int group, int head_dim, int tokens, int capacity, int splits,
