@@ -1,13 +1,15 @@
 """A seeded random-init Qwen3-4B-shaped model for the greedy-decode parity check.
 
-The quantized projections of every decode step run through the gfx950 library (the
-drop-in path); everything around them -- embedding, RMSNorm, q/k head norms, RoPE, GQA
-attention, residual adds -- is plain torch shared by both sides, in fp32 where it
-computes. The reference side is the reference engine's CPU-expressible linear path,
-dequantize-then-``F.linear`` (engine/kernels/cuda_fp8.py:1154-1161 followed by F.linear,
-as bench/gpu_checks.py:141-144 checks it), here in fp32 on the GPU; for FP8 W8A8 it is
-(x_q s_x)(w_q s_w)^T with the dynamic per-token activation scale. Prefill (512 prompt
-tokens) is out of the product's scope and uses the reference linears on both sides.
+Every op of a decode step runs through the gfx950 library (the drop-in path): RMSNorm and the
+residual add + RMSNorm, the quantized projections (SwiGLU fused into gate_up), the q/k head
+norm + RoPE + KV-cache write, and decode attention over the cache. The reference side is torch:
+the reference engine's CPU-expressible linear path, dequantize-then-``F.linear``
+(engine/kernels/cuda_fp8.py:1154-1161 followed by F.linear, as bench/gpu_checks.py:141-144 checks
+it), here in fp32 on the GPU (for FP8 W8A8: (x_q s_x)(w_q s_w)^T with the dynamic per-token
+activation scale); its head norm + RoPE as the reference's torch statement
+(engine/kernels/reference.py:31-46) with bf16 cos/sin tables built as the engine builds them
+(engine/engine.py:350-358); fp32 softmax attention; Qwen3RMSNorm. Prefill (512 prompt tokens)
+is out of the product's scope: it runs the reference side and fills the cache both sides read.
 
 The comparison is the reference harness's rule (bench/harness.py:136-152): the emitted
 tokens are replayed teacher-forced through the reference model; at every step the gap
@@ -24,6 +26,8 @@ import torch
 
 HIDDEN, INTER, HEADS, KV_HEADS, HEAD_DIM = 2560, 9728, 32, 8, 128
 VOCAB, LAYERS, EPS, THETA = 151936, 36, 1e-6, 5e6
+#: KV-cache slots per sequence: the 512-token prompt and 64 decode steps fit.
+CAPACITY = 640
 
 
 # ---- reference linears (torch fp32) ------------------------------------------------------
@@ -99,8 +103,14 @@ class RandomQwen3:
         self.final_norm = norm(HIDDEN)
         lm = quant(self.embed)  # tied: the lm_head is the quantized embedding
         self.lm_head = (lm, qlinear.prepare(lm, fmt), dequantize(fmt, lm) if fmt != "fp8" else None)
-        inv = 1.0 / (THETA ** (torch.arange(0, HEAD_DIM, 2, device=device, dtype=torch.float32) / HEAD_DIM))
-        self.inv_freq = inv
+        # cos/sin tables (bf16 [positions, 128]) as engine/engine.py:350-358 builds them
+        half = HEAD_DIM // 2
+        steps = torch.arange(0, half, dtype=torch.int64, device=device).float()
+        inv_freq = 1.0 / (THETA ** (steps / half))
+        positions = torch.arange(CAPACITY, dtype=torch.int64, device=device).float()
+        emb = torch.cat([positions[:, None] * inv_freq[None, :]] * 2, dim=-1)
+        self.cos = emb.cos().to(torch.bfloat16).contiguous()
+        self.sin = emb.sin().to(torch.bfloat16).contiguous()
 
     # -- pieces shared by both sides --------------------------------------------------------
 
@@ -111,15 +121,19 @@ class RandomQwen3:
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + EPS)
         return w * xf.to(torch.bfloat16)
 
-    def rope(self, x, pos):
-        """Rotate-half RoPE of [B, H, T, D] at integer positions [T]."""
-        f = pos.float()[:, None] * self.inv_freq[None, :]
-        emb = torch.cat([f, f], dim=-1)
-        cos, sin = emb.cos(), emb.sin()
-        xf = x.float()
+    def head_norm_rope(self, x, w, pos):
+        """Per-head RMSNorm then RoPE of [B, T, H, D] at positions [T]: the reference's torch
+        statement (engine/kernels/reference.py:31-46), three bf16 roundings."""
+        f = x.float()
+        scale = torch.rsqrt(f.pow(2).mean(-1, keepdim=True) + EPS)
+        normed = ((f * scale).to(torch.bfloat16).float() * w.float()).to(torch.bfloat16).float()
         half = HEAD_DIM // 2
-        rot = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
-        return (xf * cos + rot * sin).to(torch.bfloat16)
+        rotated = torch.cat([-normed[..., half:], normed[..., :half]], dim=-1)
+        c = self.cos[pos].float()[:, None, :]
+        s = self.sin[pos].float()[:, None, :]
+        left = (normed * c).to(torch.bfloat16).float()
+        right = (rotated * s).to(torch.bfloat16).float()
+        return (left + right).to(torch.bfloat16)
 
     @staticmethod
     def attention(q, k, v, causal_offset):
@@ -144,10 +158,16 @@ class RandomQwen3:
             return ref_linear(self.fmt, x, packed, deq, self.ref_dtype)
         return self.linear_fn(x, tiled, swiglu=which == "gate_up")
 
-    def forward(self, ids, cache, reference):
-        """Run [B, T] token ids after the cached positions; returns bf16 logits of the last token
-        (or of every token when ``reference`` replays), appending to the KV cache. With
-        ``reference`` False the projections are the library's (decode: T = 1)."""
+    def new_cache(self, batch, device="cuda"):
+        """Per-layer bf16 K/V caches [B, 8, CAPACITY, 128] (the layout the library's head-norm +
+        RoPE kernel writes and its decode attention reads) and the filled length."""
+        shape = (batch, KV_HEADS, CAPACITY, HEAD_DIM)
+        return {"len": 0, "k": [torch.zeros(shape, dtype=torch.bfloat16, device=device) for _ in range(self.layers)],
+                "v": [torch.zeros(shape, dtype=torch.bfloat16, device=device) for _ in range(self.layers)]}
+
+    def forward(self, ids, cache, reference=True):
+        """The torch reference (``reference``: its linears) over [B, T] token ids after the cached
+        positions: bf16 logits of every token, K/V written into the cache's slots."""
         b, t = ids.shape
         start = cache["len"]
         pos = torch.arange(start, start + t, device=ids.device)
@@ -158,15 +178,11 @@ class RandomQwen3:
             q = qkv[..., :HEADS * HEAD_DIM].reshape(b, t, HEADS, HEAD_DIM)
             k = qkv[..., HEADS * HEAD_DIM:(HEADS + KV_HEADS) * HEAD_DIM].reshape(b, t, KV_HEADS, HEAD_DIM)
             v = qkv[..., (HEADS + KV_HEADS) * HEAD_DIM:].reshape(b, t, KV_HEADS, HEAD_DIM)
-            q = self.rope(self.rms_norm(q, blk["q_norm"]).transpose(1, 2), pos)
-            k = self.rope(self.rms_norm(k, blk["k_norm"]).transpose(1, 2), pos)
-            v = v.transpose(1, 2)
-            if li not in cache["k"]:
-                cache["k"][li], cache["v"][li] = k, v
-            else:
-                cache["k"][li] = torch.cat([cache["k"][li], k], dim=2)
-                cache["v"][li] = torch.cat([cache["v"][li], v], dim=2)
-            a = self.attention(q, cache["k"][li], cache["v"][li], start)
+            q = self.head_norm_rope(q, blk["q_norm"], pos).transpose(1, 2)
+            k = self.head_norm_rope(k, blk["k_norm"], pos).transpose(1, 2)
+            cache["k"][li][:, :, start:start + t] = k
+            cache["v"][li][:, :, start:start + t] = v.transpose(1, 2)
+            a = self.attention(q, cache["k"][li][:, :, :start + t], cache["v"][li][:, :, :start + t], start)
             a = a.transpose(1, 2).reshape(b * t, HEADS * HEAD_DIM).contiguous()
             h = h + self._linear("o", a, blk["o"], reference).reshape(b, t, HIDDEN)
             x = self.rms_norm(h, blk["post_norm"]).reshape(b * t, HIDDEN)
@@ -178,26 +194,49 @@ class RandomQwen3:
             h = h + self._linear("down", act, blk["down"], reference).reshape(b, t, HIDDEN)
         cache["len"] = start + t
         h = self.rms_norm(h, self.final_norm)
-        last = h if reference else h[:, -1:, :]
-        logits = self._linear("lm_head", last.reshape(-1, HIDDEN), self.lm_head, reference)
-        return logits.reshape(b, last.shape[1], VOCAB)
+        logits = self._linear("lm_head", h.reshape(-1, HIDDEN), self.lm_head, reference)
+        return logits.reshape(b, t, VOCAB)
+
+    def decode_step(self, tok, cache, attention, pos):
+        """One decode step of [B] tokens with every op in the library: RMSNorm, the quantized
+        projections, head norm + RoPE + cache write, decode attention, residual + RMSNorm.
+        ``pos`` (int32 [1], device) is the step's position; returns fp32 logits [B, VOCAB]."""
+        from kernels import add_rms_norm, qkv_norm_rope_to_cache, rms_norm
+        h = self.embed[tok]
+        x = rms_norm(h, self.blocks[0]["in_norm"], EPS)
+        for li, blk in enumerate(self.blocks):
+            qkv = self.linear_fn(x, blk["qkv"][1], swiglu=False)
+            q = qkv_norm_rope_to_cache(qkv, HEADS, KV_HEADS, blk["q_norm"], blk["k_norm"], self.cos, self.sin, pos, 1,
+                                       cache["k"][li], cache["v"][li], EPS)
+            a = attention(q, cache["k"][li], cache["v"][li], pos)
+            h, x = add_rms_norm(h, self.linear_fn(a, blk["o"][1], swiglu=False), blk["post_norm"], EPS)
+            act = self.linear_fn(x, blk["gate_up"][1], swiglu=True)
+            following = self.blocks[li + 1]["in_norm"] if li + 1 < self.layers else self.final_norm
+            h, x = add_rms_norm(h, self.linear_fn(act, blk["down"][1], swiglu=False), following, EPS)
+        cache["len"] += 1
+        return self.linear_fn(x, self.lm_head[1], swiglu=False).float()
 
     # -- decode and replay ------------------------------------------------------------------
 
     def generate(self, prompt, steps):
-        """Greedy decode: prefill with the reference linears (out of scope), then `steps`
-        decode steps through the library. Returns ([B, steps] token ids, [B, steps, VOCAB]
+        """Greedy decode: prefill through the reference (out of scope), then `steps` decode steps
+        through the library (``decode_step``). Returns ([B, steps] token ids, [B, steps, VOCAB]
         fp32 logits each emitted token was chosen from): token t is the argmax of logits t,
         which the prefill (t = 0) or decode step t - 1 produced."""
-        cache = {"len": 0, "k": {}, "v": {}}
+        from kernels import DecodeAttention
+        b = prompt.shape[0]
+        cache = self.new_cache(b, prompt.device)
         logits = self.forward(prompt, cache, reference=True)[:, -1, :].float()
+        attention = DecodeAttention(b, KV_HEADS, HEADS // KV_HEADS, HEAD_DIM, CAPACITY, prompt.device)
+        pos = torch.zeros(1, dtype=torch.int32, device=prompt.device)
         out, seen = [], []
         for t in range(steps):
             tok = logits.argmax(dim=-1)
             out.append(tok)
             seen.append(logits)
             if t + 1 < steps:
-                logits = self.forward(tok[:, None], cache, reference=False)[:, -1, :].float()
+                pos.fill_(cache["len"])
+                logits = self.decode_step(tok, cache, attention, pos)
         return torch.stack(out, dim=1), torch.stack(seen, dim=1)
 
     def replay_logits(self, prompt, tokens, dtype=torch.float32):
@@ -205,7 +244,7 @@ class RandomQwen3:
         [B, steps, VOCAB] fp32, entry t conditioned on the prompt and tokens[:, :t]. `dtype` is
         the reference matmuls' precision."""
         full = torch.cat([prompt, tokens], dim=1)
-        cache = {"len": 0, "k": {}, "v": {}}
+        cache = self.new_cache(prompt.shape[0], prompt.device)
         self.ref_dtype = dtype
         try:
             return self.forward(full, cache, reference=True)[:, prompt.shape[1] - 1:-1, :].float()

@@ -2,17 +2,20 @@
 W8A16 / FP8 W8A8 / W4A16 at batch 1 and 32, checked against the torch reference by the
 reference harness's teacher-forced replay (bench/harness.py:136-152, TIE_MARGIN at :21).
 
-Every decode-step projection (qkv, o, gate_up with the fused SwiGLU, down, lm_head) runs
-through the gfx950 library; attention, norms and RoPE are shared torch code (qwen3_random).
+Every op of every decode step runs through the gfx950 library (qwen3_random.decode_step):
+RMSNorm and residual + RMSNorm, the projections (qkv, o, gate_up with the fused SwiGLU, down,
+lm_head), the q/k head norm + RoPE + KV-cache write and decode attention. The reference replays
+in torch (its linears, its head norm + RoPE statement, fp32 attention).
 
 The check, per emitted step t of every sequence:
 
 * the library's logits (those token t was chosen from) against the reference's logits on
   the same context (teacher-forced replay): max |delta| and relative L2 are measured. The
-  library rounds to bf16 exactly where the reference does, so what separates them is fp32
-  summation order inside each projection, amplified through 36 layers -- the same kind of
-  difference as between the reference's own fp32 and fp64 matmuls. The relative L2 must stay
-  within twice that self-spread (the largest over the run's steps);
+  library rounds to bf16 exactly where the reference does (attention: its probabilities enter
+  the value product in bf16, as the reference engine's decode kernel has them), so what
+  separates them is summation order and that rounding, amplified through 36 layers -- the same
+  kind of difference as between the reference's own fp32 and fp64 matmuls. The relative L2 must
+  stay within twice that self-spread (the largest over the run's steps);
 * **identity where the reference decides**: wherever the reference's top-1 / top-2 margin
   exceeds twice that step's max |delta|, the emitted token must be the reference's argmax
   (every step is counted; the ones below the bound are printed);
