@@ -251,7 +251,8 @@ def cpu_model_name():
 
 
 def cpu_baseline(stack, reps=5, warmup=2):
-    """The reference's torch CPU path, timed on the host cores.
+    """The reference's torch CPU path -- dequantize (engine/kernels/cuda_fp8.py:1154-1161), then
+    F.linear -- timed on the host cores of the GPU box in the same run.
 
     Every projection of the stack (36 distinct layers + the lm_head: the same synthetic
     weights and activations, copied to host memory in their row-major packed form) runs
@@ -518,7 +519,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md).", file=sys.stderr)
+              "(the projections would shard column- and row-parallel, one process per GPU).", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
