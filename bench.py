@@ -419,6 +419,60 @@ def measure_config4(reps, layers=LAYERS):
     return out
 
 
+#: The reference's published H100 times (us) for its own INT8 g64 W8A16 kernel at M=1 on these
+#: shapes (NOTES.md:354-360 of the reference): context for the same call on MI355X, not a target.
+REF_H100_INT8_US = {"qkv": 9.5, "o": 8.1, "gate_up": 21.0, "down": 12.4, "lm_head": 150.8}
+
+
+def measure_reference_formats(reps=10):
+    """The reference engine's own weight formats through its own calls (cuda_fp8.quantize /
+    prepare / matmul and gate_up_swiglu, engine/engine.py:522-532, 881-884, 950-951): INT8 and
+    INT4 with an fp16 scale per 64 values in the tiled Prepared layout, at M=1, per projection
+    over enough distinct weights to cover >= 1 GiB (up to 36), replayed as one HIP graph. Bytes:
+    weight + scales + x in + y out. With the derived M=1 stack, 36 x (qkv + o + gate_up + down) +
+    lm_head, and the reference's published H100 INT8 figures beside them."""
+    import math
+    from kernels import cuda_fp8
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    out = {}
+    for bits in (8, 4):
+        res = {}
+        for name, n, k in PROJ + [LM_HEAD]:
+            per = n * k * (bits / 8) + n * (k // 64) * 2
+            count = min(LAYERS, max(1, math.ceil((1 << 30) / per)))
+            ws = []
+            for _ in range(count):
+                w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+                ws.append(cuda_fp8.prepare(cuda_fp8.quantize(w, bits=bits)))
+                del w
+            x = torch.randn(1, k, generator=gen, device="cuda").to(torch.bfloat16)
+            fn = cuda_fp8.gate_up_swiglu if name == "gate_up" else cuda_fp8.matmul
+
+            def run():
+                for p in ws:
+                    fn(x, p)
+            g = graph_of(run)
+            us = median_graph_ms(g, reps, 2, trials=3) / count * 1e3
+            del g
+            n_out = n // 2 if name == "gate_up" else n
+            alg = ws[0].bytes_moved() + 2 * k + 2 * n_out
+            res[name] = {"us": round(us, 2), "alg_MB": round(alg / 1e6, 3), "GBps": round(alg / us / 1e3, 1)}
+            del ws
+            torch.cuda.empty_cache()
+        stack_us = LAYERS * sum(res[nm]["us"] for nm, _, _ in PROJ) + res["lm_head"]["us"]
+        stack_b = LAYERS * sum(res[nm]["alg_MB"] for nm, _, _ in PROJ) + res["lm_head"]["alg_MB"]
+        res["stack_M1_us"] = round(stack_us, 1)
+        res["stack_M1_GBps"] = round(stack_b / stack_us * 1e3, 1)
+        if bits == 8:
+            res["reference_h100_us"] = dict(REF_H100_INT8_US, stack_M1=round(
+                LAYERS * sum(REF_H100_INT8_US[nm] for nm, _, _ in PROJ) + REF_H100_INT8_US["lm_head"], 1))
+        out[f"int{bits}_g64"] = res
+        log(f"reference formats int{bits} g64 M=1 (cuda_fp8.matmul): " +
+            ", ".join(f"{nm} {res[nm]['us']:.1f} us" for nm in ("qkv", "o", "gate_up", "down", "lm_head")) +
+            f"; stack {stack_us:.0f} us")
+    return out
+
+
 #: Decode attention cases (Qwen3-4B: 8 KV heads x 4 query heads, head_dim 128): batch, cache
 #: capacity, live keys. Batch 32 at 576 keys is config 5's last step (prompt 512 + 64 tokens).
 ATTENTION_CASES = ((1, 4096, 4096), (1, 32768, 32768), (32, 640, 576))
@@ -516,6 +570,8 @@ def main():
     ap.add_argument("--only-attention", action="store_true",
                     help="only the QKV consumer and decode attention figures: one JSON line, for profiling "
                          "(not the driver's line)")
+    ap.add_argument("--only-reference-formats", action="store_true",
+                    help="only the reference formats' cuda_fp8.matmul figures: one JSON line (not the driver's line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
@@ -529,6 +585,10 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.only_config4:
         print(json.dumps({"config4_w4_gate_up_swiglu_down": measure_config4(max(3, args.steps // 4))}), flush=True)
+        return
+    if args.only_reference_formats:
+        print(json.dumps({"reference_formats_cuda_fp8_matmul": measure_reference_formats(max(3, args.steps // 2))}),
+              flush=True)
         return
     if args.only_attention:
         print(json.dumps({"qkv_consumer_and_decode_attention": measure_attention(max(3, args.steps // 2))}),
@@ -609,6 +669,7 @@ def main():
         extra["per_projection_single_calls"] = per_cfg
         extra["config4_w4_gate_up_swiglu_down"] = measure_config4(max(3, args.steps // 4))
         extra["qkv_consumer_and_decode_attention"] = measure_attention(max(3, args.steps // 2))
+        extra["reference_formats_cuda_fp8_matmul"] = measure_reference_formats(max(3, args.steps // 2))
 
     line = {
         "metric": METRIC,

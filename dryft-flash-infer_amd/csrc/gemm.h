@@ -200,6 +200,7 @@ __device__ __forceinline__ uint32_t bf16_at(const uint16_t* p, int i) { return p
 //      loads complete 16 full 128-byte lines.
 struct FmtW4 {
   static constexpr int KSTEP = 256, LOADS = 2, NSC = 2, XBYTES = 2;
+  static constexpr bool SCALE_PAIR = true;  // scale_pair(): a step's two group scales
   static constexpr float BIAS = 136.f;  // bf16(128 + code) = q + 136
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     if (a.tiled)
@@ -211,6 +212,11 @@ struct FmtW4 {
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
     return bf2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 7) + 2 * step + j]);
   }
+  // Both group scales of a step, one 4-byte load (a row's k/128 groups are an even count).
+  __device__ static uint32_t scale_pair(const GemmArgs& a, int wrow, int step) {
+    return gmem(reinterpret_cast<const uint32_t*>(a.ws))[(size_t)wrow * (a.k >> 8) + step];
+  }
+  __device__ static float scale_of(uint32_t bits16) { return bf2f(bits16); }
   // A element order per word: k offsets [0,4,1,5,2,6,3,7] (nibble j and j+4 per dword);
   // the staged activation chunk (8 values in k order) is permuted to match.
   static constexpr bool GATHER = false;
@@ -393,6 +399,7 @@ __device__ __forceinline__ int ref_pos_natural(int p) {
 template <int BITS>
 struct FmtRef {
   static constexpr int KSTEP = 128, LOADS = BITS == 8 ? 2 : 1, NSC = 2, XBYTES = 2;
+  static constexpr bool SCALE_PAIR = true;
   static constexpr float BIAS = BITS == 8 ? 128.f : 136.f;
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     const int r = wrow & 15, tile = wrow >> 4, c = lane >> 4;
@@ -410,6 +417,11 @@ struct FmtRef {
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
     return h2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
   }
+  // Both block scales of a step, one 4-byte load (k is a multiple of 128).
+  __device__ static uint32_t scale_pair(const GemmArgs& a, int wrow, int step) {
+    return gmem(reinterpret_cast<const uint32_t*>(a.ws))[(size_t)wrow * (a.k >> 7) + step];
+  }
+  __device__ static float scale_of(uint32_t bits16) { return h2f((uint16_t)bits16); }
   // B position e (0..7) of chunk (c, u) of a 64-block holds permuted position 16c + 8u + sw(e):
   // 8-bit codes unpack in byte order, 4-bit codes as bytes (0,2),(1,3) per dword.
   __device__ static f32x4 bias_chain(const char* lds, int srel, int j, int lane, int xoff) {
@@ -425,16 +437,19 @@ struct FmtRef {
     return t4;
   }
   static constexpr bool GATHER = true;  // staged from permuted positions (stage_chunk)
+  // Chunk (c, u) of a 64-block -- permuted positions 16c + 8u + 0..7 -- holds the natural
+  // values 32u + 2c + {0, 1, 8, 9, 16, 17, 24, 25} (ref_pos_natural): four aligned pairs of
+  // consecutive values, read as four 4-byte loads. 8-bit codes take them in that order; 4-bit
+  // codes pair the values 8 apart (bytes (0, 2), (1, 3) of a dword).
   __device__ static uint4 stage_chunk(const GemmArgs& a, int mm, int kabs) {
-    const uint16_t* row = reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k;
-    const int blk = kabs & ~63, p0 = kabs & 63;
-    uint32_t v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int es = BITS == 8 ? e : ((e & 4) | ((e & 1) << 1) | ((e >> 1) & 1));
-      v[e] = bf16_at(row, blk + ref_pos_natural(p0 + es));
-    }
-    return uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)mm * a.k);
+    const int blk = kabs & ~63, p0 = kabs & 63;  // p0 = 16c + 8u
+    const int base = (blk + 32 * ((p0 >> 3) & 1) + 2 * (p0 >> 4)) >> 1;  // dword index of the first pair
+    const uint32_t d0 = gmem(row)[base], d1 = gmem(row)[base + 4], d2 = gmem(row)[base + 8],
+                   d3 = gmem(row)[base + 12];
+    if constexpr (BITS == 8) return uint4{d0, d1, d2, d3};
+    return uint4{__builtin_amdgcn_perm(d1, d0, 0x05040100u), __builtin_amdgcn_perm(d1, d0, 0x07060302u),
+                 __builtin_amdgcn_perm(d3, d2, 0x05040100u), __builtin_amdgcn_perm(d3, d2, 0x07060302u)};
   }
   template <int MT>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
@@ -486,6 +501,7 @@ struct FmtRef {
 //      v_cvt_pk_f32_fp8 (exact), -> bf16 by truncation (exact: e4m3 has 4 significant bits).
 struct FmtFP8WO {
   static constexpr int KSTEP = 128, LOADS = 2, NSC = 2, XBYTES = 2;
+  static constexpr bool SCALE_PAIR = false;
   static constexpr float BIAS = 0.f;
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + (size_t)wrow * a.k +
@@ -542,6 +558,7 @@ struct FmtFP8WO {
 //      byte 64j + 16c.
 struct FmtInt8 {
   static constexpr int KSTEP = 128, LOADS = 2, NSC = 2, XBYTES = 1;
+  static constexpr bool SCALE_PAIR = false;
   static constexpr float BIAS = 0.f;
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     return reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(a.w) + (size_t)wrow * a.k +
@@ -550,6 +567,11 @@ struct FmtInt8 {
   __device__ static float scale(const GemmArgs& a, int wrow, int step, int j) {
     return h2f(gmem(reinterpret_cast<const uint16_t*>(a.ws))[(size_t)wrow * (a.k >> 6) + 2 * step + j]);
   }
+  // Both block scales of a step, one 4-byte load (k is a multiple of 128).
+  __device__ static uint32_t scale_pair(const GemmArgs& a, int wrow, int step) {
+    return gmem(reinterpret_cast<const uint32_t*>(a.ws))[(size_t)wrow * (a.k >> 7) + step];
+  }
+  __device__ static float scale_of(uint32_t bits16) { return h2f((uint16_t)bits16); }
   template <int MT>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
@@ -805,6 +827,32 @@ __device__ void stage_scales(const GemmArgs& a, char* lds, int tg, int step0, in
       sc[rl] = tile < a.ntiles ? F::scale(a, weight_row(a, tile, rl & 15), 0, 0) : 0.f;
     }
   } else {
+    if constexpr (F::SCALE_PAIR) {
+      if ((rows & (rows - 1)) == 0) {
+        // A step's two scales of a row with one 4-byte load; with rows (16 rt) a power of two the
+        // (step, row) of an index is a shift and a mask. Four loads in flight per thread.
+        const int lg = __builtin_ctz(rows);
+        const int total = nst * rows;
+        for (int q0 = tid; q0 < total; q0 += 4 * nthr) {
+          uint32_t v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * nthr, st = q >> lg, rl = q & (rows - 1);
+            const int tile = tg * a.rt + (rl >> 4);
+            v[u] = q < total && tile < a.ntiles ? F::scale_pair(a, weight_row(a, tile, rl & 15), step0 + st) : 0u;
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * nthr, st = q >> lg, rl = q & (rows - 1);
+            if (q < total) {
+              sc[(2 * st) * a.sc_stride + rl] = F::scale_of(v[u] & 0xffffu);
+              sc[(2 * st + 1) * a.sc_stride + rl] = F::scale_of(v[u] >> 16);
+            }
+          }
+        }
+        return;
+      }
+    }
     // Four loads in flight per thread, then their stores: one memory round trip per batch.
     const int total = nst * F::NSC * rows;
     for (int q0 = tid; q0 < total; q0 += 4 * nthr) {
