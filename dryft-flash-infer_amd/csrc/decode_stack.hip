@@ -115,15 +115,15 @@ struct ExecDepth<FmtW4, PIECES> {
 };
 
 // Group scales a workgroup's threads hold for one item (formats with per-group scales): up
-// to kScaleRegs bf16 values per thread, loaded with the weights instead of after staging
-// (5 x 512 threads: every Qwen3-4B item at M = 1, gate_up's 2560 included).
+// to kScaleRegs pairs of bf16 values (a step's two groups) per thread, loaded with the weights
+// instead of after staging (5 x 512 pairs: every Qwen3-4B item at M = 1).
 constexpr int kScaleRegs = 5;
 
 struct ExecItem {
   int tg, s, np, step0, nst, wt, kwi, my, last, wrow;
   uint32_t scb;  // the per-row scale's bf16 bits, converted only when staged
   bool scpre;    // the item's group scales are in scw (else staged from memory)
-  uint32_t scw[kScaleRegs];  // group scales' bf16 bits, slot q = tid + u * threads
+  uint32_t scw[kScaleRegs];  // group scale pairs (bf16 bits), slot q = tid + u * threads
 };
 
 // Issue the wave's first ExecDepth<F, PIECES>::PF weight steps (and the per-row scale) of a work
@@ -154,19 +154,17 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
     if (rl < 16 * a.rt && tile < a.ntiles)
       it.scb = gmem(reinterpret_cast<const uint16_t*>(a.ws))[weight_row(a, tile, rl & 15)];
   } else {
-    // Group scales of the item: slot q is row q / nsj, group step0 * NSC + q % nsj (a row's
-    // groups are contiguous in memory, so consecutive threads read consecutive scales).
-    const int nsj = nst * F::NSC, total = nsj * 16 * a.rt;
+    // Group scales of the item, a step's two per 4-byte load: slot q is step q >> lg, row
+    // q & (rows - 1) (rows = 16 rt, a power of two: a shift and a mask, no division).
+    const int rows = 16 * a.rt, lg = __builtin_ctz(rows), total = nst * rows;
     it.scpre = total <= kScaleRegs * WAVES * 64;
     if (it.scpre) {
-      const auto ws = gmem(reinterpret_cast<const uint16_t*>(a.ws));
 #pragma unroll
       for (int u = 0; u < kScaleRegs; ++u) {
         const int q = threadIdx.x + u * WAVES * 64;
-        const int rl = q / nsj, sj = q - rl * nsj, tile = tg * a.rt + (rl >> 4);
+        const int rl = q & (rows - 1), tile = tg * a.rt + (rl >> 4);
         it.scw[u] = 0u;
-        if (q < total && tile < a.ntiles)
-          it.scw[u] = ws[(size_t)weight_row(a, tile, rl & 15) * (a.k >> 7) + step0 * F::NSC + sj];
+        if (q < total && tile < a.ntiles) it.scw[u] = F::scale_pair(a, weight_row(a, tile, rl & 15), step0 + (q >> lg));
       }
     }
   }
@@ -301,13 +299,16 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
       const float scv = bf2f(it.scb);
       if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
     } else if (it.scpre) {
-      const int nsj = nst * F::NSC, total = nsj * 16 * a.rt;
+      const int rows = 16 * a.rt, lg = __builtin_ctz(rows), total = nst * rows;
       float* sc = reinterpret_cast<float*>(lds + a.off_sc);
 #pragma unroll
       for (int u = 0; u < kScaleRegs; ++u) {
         const int q = threadIdx.x + u * WAVES * 64;
-        const int rl = q / nsj, sj = q - rl * nsj;
-        if (q < total) sc[sj * a.sc_stride + rl] = bf2f(it.scw[u]);
+        const int rl = q & (rows - 1), st = q >> lg;
+        if (q < total) {
+          sc[(2 * st) * a.sc_stride + rl] = F::scale_of(it.scw[u] & 0xffffu);
+          sc[(2 * st + 1) * a.sc_stride + rl] = F::scale_of(it.scw[u] >> 16);
+        }
       }
     } else {
       stage_scales<F>(a, lds, it.tg, step0, nst, ComputeTeam<WAVES>{});
