@@ -52,7 +52,27 @@ struct alignas(16) StackDesc {
   int off_red;      // LDS byte offset of the waves' partial sums (apart from the staged x)
   int rot;          // workgroup p holds share (p - rot) mod nwg of this projection
   int nwg;          // workgroups per lane
+  // FP8 chains: a published output also carries, per token and 16-row weight tile, the
+  // largest magnitude of the tile's bf16 outputs (words {16-bit run tag, bf16}); a projection
+  // reading it combines the xmax_n tiles of its k columns instead of reading whole rows for its
+  // token scales. Token row mm, row block g, tile tl of the block: word
+  // mm * pitch + g * kMaxLine + tl (each row block's words on a cache line of their own: one
+  // workgroup writes them, and small stores of many workgroups into one line queue up).
+  uint32_t* ymax;        // publish this projection's maxima here, or null
+  const uint32_t* xmax;  // the producer's maxima, or null (read whole rows)
+  int ymax_pitch;        // words per token row of ymax: row blocks x kMaxLine
+  int xmax_pitch;        // the producer's ymax_pitch
+  int xmax_n;            // the producer's tiles that make up this projection's k columns
+  int xmax_rt;           // the producer's tiles per row block
 };
+
+constexpr int kMaxLine = 32;  // maxima words per row block: one 128-byte line
+// The published maxima pay from 5 tokens on. Every item of a Qwen3-4B chain covers the whole
+// K range, so below that one pass reads each row (token maxima and slice from the same
+// registers) and the maxima only add work; beyond it the whole-row prologue reads x twice.
+// Measured on the Qwen3-4B FP8 chain (us per step, without / with): M=1 1180 / 1319, M=2
+// 1486 / 1568, M=4 2029 / 2027, M=8 3287 / 2918, M=16 5148 / 3928.
+constexpr int kMaximaMinM = 4;
 
 // Workgroup p's share of a projection. Shares are rotated from projection to projection (each
 // starts where the previous one's workgroups ended), so that when a projection has fewer
@@ -265,6 +285,141 @@ __device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, 
   }
 }
 
+// The producer's published per-token maxima an FP8 item combines (StackDesc.xmax), or none.
+struct MaxIn {
+  const uint32_t* p;
+  int pitch, n, rt;
+};
+
+// FP8 prologue of a published activation whose producer also published per-token maxima of
+// each weight tile's outputs: the token maxima are combined from those n words per token, so
+// the item reads only its slice of x. They are maxima of the same bf16 values, so the token
+// scales and codes equal those of the whole-row prologue (stage_fp8_act). When the slice fits
+// one batch, its chunks are polled together with the first batch of maxima words (the last of
+// them lands with the producer's last output). `amax` is zeroed.
+template <class XS>
+__device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs, const MaxIn& mi, char* lds,
+                                                 int step0, int nst, uint32_t* amax) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  constexpr int U_ = stage_unroll<XS, true>();
+  constexpr int MW = 4;  // 16-byte loads of maxima words per thread in flight
+  const int cps = nst * 16, total = a.m * cps;  // the slice's 8-value chunks
+  const bool one_pass = total <= U_ * nthr;
+  typename XS::Raw r[U_];
+  auto first = [&](int u, int& mm, int& kabs) {
+    const int q = tid + u * nthr;
+    mm = q / cps;
+    kabs = step0 * 128 + (q - mm * cps) * 8;
+    return q < total;
+  };
+  unsigned sstale = 0;  // bit u: slice chunk u has not arrived
+  if (one_pass) {
+#pragma unroll
+    for (int u = 0; u < U_; ++u) {
+      int mm, kabs;
+      if (first(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U_; ++u) {
+      int mm, kabs;
+      if (first(u, mm, kabs) && !xs.ready(r[u])) sstale |= 1u << u;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t mrs = wire_rsrc(mi.p, (unsigned)a.m * (unsigned)mi.pitch * 4u);
+  const uint32_t tag = wire_tag(xs.w.epoch);
+  // 16-byte loads: per row block, per token row, in all
+  const int lpb = (mi.rt + 3) >> 2, per = (mi.n + mi.rt - 1) / mi.rt * lpb, nl = a.m * per;
+  auto word_ok = [&](const u32x4& v, int valid) {
+    bool ok = true;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ok &= e >= valid || (v[e] >> 16) == tag;
+    return ok;
+  };
+  // Every thread takes the first round (its slice chunks are polled there), with or without
+  // maxima words of its own.
+  for (int l0 = tid; l0 == tid || l0 < nl; l0 += MW * nthr) {
+    u32x4 mv[MW];
+    unsigned off[MW];
+    int valid[MW], tok[MW];
+    unsigned stale = 0;
+#pragma unroll
+    for (int j = 0; j < MW; ++j) {
+      const int q = l0 + j * nthr;
+      tok[j] = q / per;
+      const int c = q - tok[j] * per, blk = c / lpb, i4 = 4 * (c - blk * lpb);
+      valid[j] = q < nl ? max(0, min(4, min(mi.rt - i4, mi.n - blk * mi.rt - i4))) : 0;
+      off[j] = ((unsigned)tok[j] * mi.pitch + blk * kMaxLine + i4) * 4u;
+      if (q < nl) mv[j] = wire_load16(mrs, off[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < MW; ++j)
+      if (valid[j] && !word_ok(mv[j], valid[j])) stale |= 1u << j;
+    while ((stale | sstale) && !xs.expired()) {
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int j = 0; j < MW; ++j)
+        if (stale >> j & 1u) mv[j] = wire_load16(mrs, off[j]);
+#pragma unroll
+      for (int u = 0; u < U_; ++u) {
+        int mm, kabs;
+        if (sstale >> u & 1u) {
+          first(u, mm, kabs);
+          xs.refetch(a, mm, kabs, r[u]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < MW; ++j)
+        if ((stale >> j & 1u) && word_ok(mv[j], valid[j])) stale &= ~(1u << j);
+#pragma unroll
+      for (int u = 0; u < U_; ++u)
+        if ((sstale >> u & 1u) && xs.ready(r[u])) sstale &= ~(1u << u);
+    }
+#pragma unroll
+    for (int j = 0; j < MW; ++j) {
+      if (!valid[j]) continue;
+      uint32_t b = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < valid[j]) b = max(b, mv[j][e] & 0xffffu);
+      atomicMax(&amax[tok[j]], b << 16);
+    }
+  }
+  __syncthreads();
+  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+  auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
+  for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
+  if (one_pass) {
+    settle_batch<XS, U_>(a, xs, r, first);  // arrived with the maxima (nothing left, but a run past its deadline)
+#pragma unroll
+    for (int u = 0; u < U_; ++u) {
+      int mm, kabs;
+      if (first(u, mm, kabs))
+        store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), token_scale(mm));
+    }
+    return;
+  }
+  for (int q0 = tid; q0 < total; q0 += U_ * nthr) {
+    auto chunk = [&](int u, int& mm, int& kabs) {
+      const int q = q0 + u * nthr;
+      mm = q / cps;
+      kabs = step0 * 128 + (q - mm * cps) * 8;
+      return q < total;
+    };
+#pragma unroll
+    for (int u = 0; u < U_; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
+    }
+    settle_batch<XS, U_>(a, xs, r, chunk);
+#pragma unroll
+    for (int u = 0; u < U_; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs))
+        store_e4m3_chunk(lds + mm * a.xstride + (kabs - step0 * 128), xs.value(r[u]), token_scale(mm));
+    }
+  }
+}
+
 // Stage what the item needs in LDS and stream its weight steps through the MFMAs. With
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
 // projection, same steps -- is still in place. With poller waves (NP > 0) they stage the
@@ -272,7 +427,7 @@ __device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, 
 template <class F, int WAVES, int NP, bool PIECES, class XS>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
                                           uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS], f32x4 (&acc)[1][1],
-                                          uint32_t* amax) {
+                                          uint32_t* amax, const MaxIn& mi = {}) {
   constexpr int PF = ExecDepth<F, PIECES>::PF;
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
@@ -280,9 +435,16 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
   if (!reuse) {
     if constexpr (NP == 0) {
-      if constexpr (FP8)
-        stage_fp8_act(a, xs, lds, step0, nst, BlockTeam{}, amax);  // amax: zeroed, as the pollers' is
-      else
+      if constexpr (FP8) {
+        bool done = false;
+        if constexpr (XS::POLLS) {
+          if (mi.p) {
+            stage_fp8_maxima(a, xs, mi, lds, step0, nst, amax);
+            done = true;
+          }
+        }
+        if (!done) stage_fp8_act(a, xs, lds, step0, nst, BlockTeam{}, amax);  // amax: zeroed, as the pollers' is
+      } else
         stage_bf16<F>(a, xs, lds, step0, nst);
     } else if (poller) {
       if constexpr (FP8)
@@ -361,8 +523,10 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
 
 // Combine the item's waves; then, per output pair: write it (np == 1), publish this piece's
 // partial sums (piece > 0), or add the other pieces' partials in piece order and write
-// (piece 0). Outputs go to y and, when a later projection reads them, to ywire.
-template <class F, bool SW, bool PIECES, class Team = BlockTeam>
+// (piece 0). Outputs go to y and, when a later projection reads them, to ywire. With MAXIMA
+// (FP8 chains without poller waves) and d.ymax, the writer of each tile's outputs also
+// publishes each token's largest magnitude among them.
+template <class F, bool SW, bool PIECES, bool MAXIMA = false, class Team = BlockTeam>
 __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const ExecItem& it,
                                             const f32x4 (&acc)[1][1], const Waits& w, const Team& team = {},
                                             bool guard = true) {
@@ -447,6 +611,20 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
     const uint32_t pair = bf16_pair(o0, o1);
     *gmem(reinterpret_cast<uint32_t*>(y + (size_t)mm * nout + oi)) = pair;
     if (d.ywire) wire_store_pair(d.ywire + (size_t)mm * (nout >> 1) + (oi >> 1), pair, w.epoch);
+    if constexpr (MAXIMA) {
+      if (d.ymax) {
+        // The tile's pairs of this token are rows_out / 2 consecutive lanes (idx steps by whole
+        // waves, and tiles and tokens by rows_out / 2), all active together: their largest
+        // magnitude (fmaxf drops a NaN, as the staging's maxima do) goes out from the first.
+        float mx = fmaxf(0.f, fmaxf(fabsf(bf2f(pair & 0xffffu)), fabsf(bf2f(pair >> 16))));
+#pragma unroll
+        for (int sh = 1; sh < rows_out / 2; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh));
+        if (nl == 0)
+          __hip_atomic_store(gmem(d.ymax + (size_t)mm * d.ymax_pitch + it.tg * kMaxLine + tl),
+                             (wire_tag(w.epoch) << 16) | (__float_as_uint(mx) >> 16), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 
@@ -527,6 +705,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
+  constexpr bool MAXIMA = std::is_same<F, FmtFP8>::value && NP == 0;  // published row-block maxima
   uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 staging: per-token maxima
   if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   const StackDesc* calls = gcalls;
@@ -554,7 +733,8 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     cur = nxt;
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire)
-      exec_main<F, WAVES, NP, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax);
+      exec_main<F, WAVES, NP, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax,
+                                      MaxIn{NP == 0 ? d.xmax : nullptr, d.xmax_pitch, d.xmax_n, d.xmax_rt});
     else
       exec_main<F, WAVES, NP, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax);
     staged_c = c;
@@ -567,9 +747,9 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
       __syncthreads();  // the barrier of acc_to_lds in exec_finish
       if (threadIdx.x - WAVES * 64 < 16) amax[threadIdx.x - WAVES * 64] = 0u;  // for the next staging
     } else if (d.sw) {
-      exec_finish<F, true, PIECES>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
+      exec_finish<F, true, PIECES, MAXIMA>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     } else {
-      exec_finish<F, false, PIECES>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
+      exec_finish<F, false, PIECES, MAXIMA>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     }
     const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
     have = after.have;
@@ -828,13 +1008,33 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     if (occ >= lanes) break;
     lanes = occ;
   }
-  // Arena: published outputs and partial sums, 256-byte aligned regions.
+  // FP8 chains of more than kMaximaMinM tokens without poller waves: a published output also
+  // carries its per-token maxima per weight tile, and a projection reading it combines those of
+  // its k columns instead of reading whole rows for its token scales.
+  const bool maxima = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM;
+  auto tile_cols = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? 8 : 16; };  // outputs per tile
+  auto max_pitch = [&](int c) {
+    GemmArgs a = {};
+    layout(fi, sp[c].plan, m, calls[c].n, calls[c].k, a);
+    return a.tile_groups * kMaxLine;
+  };
+  auto max_rt = [&](int c) {
+    GemmArgs a = {};
+    layout(fi, sp[c].plan, m, calls[c].n, calls[c].k, a);
+    return a.rt;
+  };
+  // Arena: published outputs (and their maxima) and partial sums, 256-byte aligned regions.
   long long off = 0;
-  std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1);
+  std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1), max_off(ncalls, -1);
   for (int c = 0; c < ncalls; ++c) {
     if (published[c]) {
       wire_off[c] = off;
       off += ((8LL * m * (nout(c) / 2)) + 255) & ~255LL;
+      if (maxima) {
+        QLX_REQUIRE(max_rt(c) <= kMaxLine, "projection %d: %d tiles per row block", c, max_rt(c));
+        max_off[c] = off;
+        off += (4LL * m * max_pitch(c) + 255) & ~255LL;
+      }
     }
     if (sp[c].max_np > 1) {
       part_off[c] = off;
@@ -860,6 +1060,17 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       d.part = part_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + part_off[c]) : nullptr;
       d.xwire = src[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[src[c]]) : nullptr;
       d.xpitch = src[c] >= 0 ? nout(src[c]) : 0;
+      if (max_off[c] >= 0) {
+        d.ymax = reinterpret_cast<uint32_t*>(base + max_off[c]);
+        d.ymax_pitch = max_pitch(c);
+      }
+      const int j = src[c];
+      if (j >= 0 && max_off[j] >= 0 && q.k % tile_cols(j) == 0) {
+        d.xmax = reinterpret_cast<const uint32_t*>(base + max_off[j]);
+        d.xmax_pitch = max_pitch(j);
+        d.xmax_n = q.k / tile_cols(j);
+        d.xmax_rt = max_rt(j);
+      }
     }
     d.units = sp[c].units;
     d.nwg = P;
