@@ -191,28 +191,31 @@ def test_every_tile_split_is_exact(kw, pollers):
     check_against_single_calls(fmt, bufs, weights, ("kw", kw, pollers))
 
 
-@pytest.mark.parametrize("fmt,waves,lanes", [("fp8", 4, 3), ("w4a16", 4, 2), ("w8a16", 8, 2)])
-def test_lanes_and_small_workgroups(fmt, waves, lanes):
+@pytest.mark.parametrize("fmt,waves,lanes,m", [("fp8", 4, 3, 4), ("w4a16", 4, 2, 4), ("w8a16", 8, 2, 4),
+                                               ("fp8", 8, 2, 8)])
+def test_lanes_and_small_workgroups(fmt, waves, lanes, m):
     """Projections spread over several lanes (chained inputs cross lanes) give the same
-    results as the single-call linears."""
-    chain, bufs, weights, _ = build_chain(fmt, 4, 300 + lanes, waves=waves, lanes=lanes)
+    results as the single-call linears (FP8 at 8 tokens: token maxima published by a
+    projection of another lane)."""
+    print(f"decode stack lanes {fmt} waves={waves} lanes={lanes} m={m}", flush=True)
+    chain, bufs, weights, _ = build_chain(fmt, m, 300 + lanes, waves=waves, lanes=lanes)
     assert chain.launch.lanes >= 1 and chain.launch.waves == waves
     for run in range(2):
         if run:
-            bufs["x"].copy_(rand((4, 1024), 11).to(DEV))
-            bufs["g"].copy_(rand((4, 9728), 12).to(DEV))
+            bufs["x"].copy_(rand((m, 1024), 11).to(DEV))
+            bufs["g"].copy_(rand((m, 9728), 12).to(DEV))
         chain.run()
         torch.cuda.synchronize()
         assert not chain.failed()
         check_against_single_calls(fmt, bufs, weights, (fmt, waves, lanes, run))
 
 
-@pytest.mark.parametrize("waves,pollers", [(8, 0), (4, 4)])
-def test_bounded_wait_gives_up_and_recovers(waves, pollers):
+@pytest.mark.parametrize("waves,pollers,m", [(8, 0, 2), (4, 4, 2), (8, 0, 8)])
+def test_bounded_wait_gives_up_and_recovers(waves, pollers, m):
     """A zero wait budget makes the waits give up (forced from the host): the kernel still
-    ends, flags the run, and after reset() a normal run is right again."""
-    m = 2
-    print(f"decode stack bounded wait waves={waves} pollers={pollers}", flush=True)
+    ends, flags the run, and after reset() a normal run is right again (FP8 at 8 tokens: the
+    wait for the published token maxima too)."""
+    print(f"decode stack bounded wait waves={waves} pollers={pollers} m={m}", flush=True)
     chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves, pollers=pollers)
     chain.run(budget_us=0)
     torch.cuda.synchronize()
