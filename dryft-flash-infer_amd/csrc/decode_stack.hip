@@ -481,7 +481,7 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   // the next staging, which the end-of-item barrier orders after this.
   if constexpr (FP8 && NP == 0)
     if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
-  if constexpr (F::BIAS != 0.f) {
+  if constexpr (needs_bias_totals<F>()) {
     if (!reuse) {
       if (!poller) stage_bias<F, WAVES>(a, lds, nst);
       __syncthreads();

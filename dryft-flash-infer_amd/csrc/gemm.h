@@ -202,6 +202,7 @@ struct FmtW4 {
   static constexpr int KSTEP = 256, LOADS = 2, NSC = 2, XBYTES = 2;
   static constexpr bool SCALE_PAIR = true;  // scale_pair(): a step's two group scales
   static constexpr float BIAS = 136.f;  // bf16(128 + code) = q + 136
+  static constexpr bool FUSED_BIAS = true;  // compute() runs the bias chain itself (no xb)
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     if (a.tiled)
       return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) +
@@ -246,12 +247,15 @@ struct FmtW4 {
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int rowl) {
     const float* sc = reinterpret_cast<const float*>(lds + a.off_sc);
-    const float* xbp = reinterpret_cast<const float*>(lds + a.off_xb);
+    // The code bias: the same MFMA chain with every code at the bias, on the fragments the
+    // step reads anyway -- bias_chain's value bit for bit (same operands, same order), with no
+    // staging pass, barrier or LDS table before the first step.
+    const uint4 avb = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      f32x4 tmp[MT];
+      f32x4 tmp[MT], tb[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < MT; ++mt) tmp[mt] = tb[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
       const uint32_t wd[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
       const int kb = (srel * 256 + j * 128 + (lane >> 4) * 32) * 2;
 #pragma unroll
@@ -265,15 +269,14 @@ struct FmtW4 {
         for (int mt = 0; mt < MT; ++mt) {
           const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
           tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+          tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
         }
       }
       const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + (srel * 2 + j) * a.sc_stride + rowl);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float xb = xbp[mrow[mt] * a.xb_stride + srel * 2 + j];
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - xb, acc[mt][i]);
-      }
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - tb[mt][i], acc[mt][i]);
     }
   }
   __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
@@ -284,6 +287,7 @@ struct FmtW4 {
 struct FmtW8 {
   static constexpr int KSTEP = 128, LOADS = 2, NSC = 0, XBYTES = 2;
   static constexpr float BIAS = 128.f;  // (byte ^ 0x80) = q + 128
+  static constexpr bool FUSED_BIAS = true;  // compute() runs the bias chain itself (no xb)
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     if (a.tiled)
       return reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.w) + tile_offset(wrow, step, j, lane, a.k));
@@ -313,9 +317,11 @@ struct FmtW8 {
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int) {
-    f32x4 tmp[MT];
+    // The code bias as in FmtW4::compute: bias_chain's value bit for bit, from the same fragments.
+    const uint4 avb = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
+    f32x4 tmp[MT], tb[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) tmp[mt] = tb[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint32_t wd[4] = {c[j].x ^ 0x80808080u, c[j].y ^ 0x80808080u, c[j].z ^ 0x80808080u,
@@ -329,15 +335,14 @@ struct FmtW8 {
         for (int mt = 0; mt < MT; ++mt) {
           const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
           tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+          tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
         }
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float xb = reinterpret_cast<const float*>(lds + a.off_xb)[mrow[mt] * a.xb_stride + srel];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[mt][i] - xb;
-    }
+      for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[mt][i] - tb[mt][i];
   }
   // Per-channel scale once, after the K sum.
   __device__ static float finish(const GemmArgs& a, const char* lds, float v, int rl, int) {
@@ -401,6 +406,7 @@ struct FmtRef {
   static constexpr int KSTEP = 128, LOADS = BITS == 8 ? 2 : 1, NSC = 2, XBYTES = 2;
   static constexpr bool SCALE_PAIR = true;
   static constexpr float BIAS = BITS == 8 ? 128.f : 136.f;
+  static constexpr bool FUSED_BIAS = true;  // compute() runs the bias chain itself (no xb)
   __device__ static const uint4* chunk_ptr(const GemmArgs& a, int wrow, int step, int lane, int j) {
     const int r = wrow & 15, tile = wrow >> 4, c = lane >> 4;
     const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
@@ -456,7 +462,9 @@ struct FmtRef {
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int rowl) {
     const float* sc = reinterpret_cast<const float*>(lds + a.off_sc);
-    const float* xbp = reinterpret_cast<const float*>(lds + a.off_xb);
+    // The code bias as in FmtW4::compute: bias_chain's value bit for bit, from the same fragments.
+    const uint32_t bb = BITS == 8 ? 0x43004300u : 0x43084308u;  // bf16 128 / 136
+    const uint4 avb = {bb, bb, bb, bb};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       uint4 av[2];
@@ -472,9 +480,9 @@ struct FmtRef {
         av[0] = uint4{nib_pair(ch.x, sh), nib_pair(ch.x, sh + 8), nib_pair(ch.y, sh), nib_pair(ch.y, sh + 8)};
         av[1] = uint4{nib_pair(ch.z, sh), nib_pair(ch.z, sh + 8), nib_pair(ch.w, sh), nib_pair(ch.w, sh + 8)};
       }
-      f32x4 tmp[MT];
+      f32x4 tmp[MT], tb[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) tmp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < MT; ++mt) tmp[mt] = tb[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
       const int kb = (srel * 128 + j * 64 + (lane >> 4) * 16) * 2;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -482,15 +490,14 @@ struct FmtRef {
         for (int mt = 0; mt < MT; ++mt) {
           const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + u * 16);
           tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[u]), as_bf16x8(bv), tmp[mt], 0, 0, 0);
+          tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
         }
       }
       const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + (srel * 2 + j) * a.sc_stride + rowl);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float xb = xbp[mrow[mt] * a.xb_stride + srel * 2 + j];
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - xb, acc[mt][i]);
-      }
+        for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(s4[i], tmp[mt][i] - tb[mt][i], acc[mt][i]);
     }
   }
   __device__ static float finish(const GemmArgs&, const char*, float v, int, int) { return v; }
@@ -665,6 +672,14 @@ __device__ __forceinline__ void stage_bf16(const GemmArgs& a, const XS& xs, char
     }
   }
 }
+
+// Formats whose compute() removes the code bias itself (FUSED_BIAS) need no bias totals.
+template <class F, class = void>
+struct fused_bias : std::false_type {};
+template <class F>
+struct fused_bias<F, std::void_t<decltype(F::FUSED_BIAS)>> : std::bool_constant<F::FUSED_BIAS> {};
+template <class F>
+constexpr bool needs_bias_totals() { return F::BIAS != 0.f && !fused_bias<F>::value; }
 
 // Bias totals per (token, scale group) from the staged activation, one MFMA chain per
 // (group, 16-token fragment), spread over the workgroup's waves. Needs the staged x.
@@ -1124,7 +1139,7 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
   }
   stage_scales<F>(a, lds, tg, step0, nst);
   __syncthreads();
-  if constexpr (F::BIAS != 0.f) {
+  if constexpr (needs_bias_totals<F>()) {
     stage_bias<F, WAVES>(a, lds, nst);
     __syncthreads();
   }

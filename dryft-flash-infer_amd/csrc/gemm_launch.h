@@ -13,12 +13,14 @@ constexpr int kLdsTarget = 64 * 1024;
 constexpr int kLdsLimit = 159 * 1024;  // 160 KB less room for the kernel's static LDS
 
 struct FmtInfo {
-  int kstep, nsc, xbytes, bias;
+  int kstep, nsc, xbytes;
+  int bias;    // the codes carry a bias that the sums remove
+  int totals;  // ... by bias totals staged in LDS (not by compute() itself)
 };
 
 template <class F>
 constexpr FmtInfo info() {
-  return FmtInfo{F::KSTEP, F::NSC, F::XBYTES, F::BIAS != 0.f};
+  return FmtInfo{F::KSTEP, F::NSC, F::XBYTES, F::BIAS != 0.f, needs_bias_totals<F>()};
 }
 
 inline int round16(int v) { return (v + 15) & ~15; }
@@ -48,7 +50,7 @@ inline int layout(const FmtInfo& fi, const qlx_plan& p, int m, int n, int k, Gem
   const int sc_floats = fi.nsc == 0 ? a.sc_stride : a.sps * fi.nsc * a.sc_stride;
   a.off_xb = round16(a.off_sc + sc_floats * 4);
   a.xb_stride = a.sps * (fi.nsc > 1 ? fi.nsc : 1);
-  const int xb_floats = fi.bias ? m * a.xb_stride : 0;
+  const int xb_floats = fi.totals ? m * a.xb_stride : 0;
   a.off_sx = round16(a.off_xb + xb_floats * 4);
   return a.off_sx + copies * m * (a.xb_stride > 2 ? a.xb_stride : 2) * 4;
 }

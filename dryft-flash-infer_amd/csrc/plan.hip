@@ -19,7 +19,7 @@ qlx::FmtInfo fmt_info(int fmt) {
     case QLX_FMT_REF4: return qlx::info<qlx::FmtRef<4>>();
     case QLX_FMT_FP8WO: return qlx::info<qlx::FmtFP8WO>();
     case QLX_FMT_INT8: return qlx::info<qlx::FmtInt8>();
-    default: return qlx::FmtInfo{0, 0, 0, 0};
+    default: return qlx::FmtInfo{0, 0, 0, 0, 0};
   }
 }
 
