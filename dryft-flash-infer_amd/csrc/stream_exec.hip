@@ -325,15 +325,16 @@ struct SxRing {
 };
 
 // One K step of W4A16 from ring lines c[0..1] and the group scales of this wave's rows (bf16
-// pairs (group 2s, 2s + 1) for rows rowl..rowl+3): the arithmetic of FmtW4::compute with the
-// scales taken from the ring's gather instead of the staged scale table.
+// pairs (group 2s, 2s + 1) for rows rowl..rowl+3): the arithmetic of FmtW4::compute (the code
+// bias from the same fragments, in the same MFMA order) with the scales taken from the ring's
+// gather instead of the staged scale table.
 __device__ __forceinline__ void sx_w4_step(f32x4& acc, const uint4 (&c)[2], const uint4& scw, const char* stage,
-                                           const GemmArgs& a, int s, int lane, int xoff, int mrow) {
-  const float* xbp = reinterpret_cast<const float*>(stage + a.off_xb);
+                                           const GemmArgs& a, int s, int lane, int xoff, int) {
   const uint32_t sw4[4] = {scw.x, scw.y, scw.z, scw.w};
+  const uint4 avb = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    f32x4 tmp = {0.f, 0.f, 0.f, 0.f};
+    f32x4 tmp = {0.f, 0.f, 0.f, 0.f}, tb = {0.f, 0.f, 0.f, 0.f};
     const uint32_t wd[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
     const int kb = (s * 256 + j * 128 + (lane >> 4) * 32) * 2;
 #pragma unroll
@@ -345,12 +346,12 @@ __device__ __forceinline__ void sx_w4_step(f32x4& acc, const uint4 (&c)[2], cons
       av.w = nib_pair(wd[t], 12);
       const uint4 bv = *reinterpret_cast<const uint4*>(stage + xoff + kb + t * 16);
       tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp, 0, 0, 0);
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb, 0, 0, 0);
     }
-    const float xb = xbp[mrow * a.xb_stride + s * 2 + j];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float sc = bf2f(j ? sw4[i] >> 16 : sw4[i] & 0xffffu);
-      acc[i] = fmaf(sc, tmp[i] - xb, acc[i]);
+      acc[i] = fmaf(sc, tmp[i] - tb[i], acc[i]);
     }
   }
 }
@@ -371,7 +372,7 @@ __device__ __host__ inline void sx_stage_args(const FmtInfo& fi, int m, int k, G
 __host__ __device__ inline int sx_stage_bytes(const FmtInfo& fi, int m, int k) {
   GemmArgs a = {};
   sx_stage_args(fi, m, k, a);
-  return a.off_xb + (fi.bias ? m * a.xb_stride * 4 : 0);
+  return a.off_xb + (fi.totals ? m * a.xb_stride * 4 : 0);
 }
 // A residual + RMSNorm stage keeps its sums of squares (one double per 8-value chunk, then the
 // token totals) in its staging buffer after what the compute waves read: kSxCssBytes from here.
@@ -413,7 +414,7 @@ __device__ __forceinline__ void sx_own_steps_prologue(const GemmArgs& a, char* s
         *reinterpret_cast<uint2*>(p + c * 8) = e4m3_chunk(v, sc, y);
       }
     }
-  } else if constexpr (F::BIAS != 0.f) {
+  } else if constexpr (needs_bias_totals<F>()) {
     constexpr int NJ = F::NSC > 1 ? F::NSC : 1;
     const int mm = lane & 15, mrow = min(mm, m - 1);
     float* xb = reinterpret_cast<float*>(stage + a.off_xb);
