@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle as O
+from oracle import bf16_to_f32, f32_to_bf16
 from kernels import qlinear
 from kernels.decode_stack import DecodeStack
 
@@ -99,7 +100,9 @@ def check_against_single_calls(fmt, bufs, weights, tag, chain_def=None):
         assert same > 0.5, (tag, name, "most outputs are bitwise equal", same)
 
 
-def oracle_check(fmt, x_bits, packed, y):
+def oracle_check(fmt, x_bits, packed, y, swiglu=False):
+    """rel-L2 of y against the oracle's product (with swiglu: the oracle's SwiGLU of the
+    bf16-rounded gate/up product, reference.py:74-79)."""
     q, s = packed
     if fmt == "fp8":
         ref = O.linear_fp8_w8a8(x_bits, q.view(torch.uint8).cpu().numpy(), bits16(s))
@@ -109,6 +112,8 @@ def oracle_check(fmt, x_bits, packed, y):
     else:
         ref = O.linear_dequant(x_bits, O.dequantize(O.unpack_int4_k32(q.cpu().numpy()), bits16(s), bits=4,
                                                     scale_dtype="bf16"))
+    if swiglu:
+        ref = bf16_to_f32(O.swiglu(f32_to_bf16(np.asarray(ref, np.float32))))
     return O.rel_l2(y.float().cpu().numpy(), ref)
 
 
@@ -128,9 +133,9 @@ def run_chain_checks(fmt, m, waves=8, pollers=0):
         for name, *_ in CHAIN:
             assert torch.equal(bufs[name], first[name]), (fmt, m, run, name, "deterministic")
         check_against_single_calls(fmt, bufs, weights, (fmt, m, run))
-    for name in ("c2", "d", "i"):
-        src = [c for c in CHAIN if c[0] == name][0][3]
-        assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name]) < 1e-2, name
+    for name in ("b", "c2", "d", "h", "i"):
+        _, _, _, src, sw = [c for c in CHAIN if c[0] == name][0]
+        assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name], swiglu=sw) < 1e-2, name
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
@@ -169,9 +174,8 @@ def test_layer_chain_without_pieces(fmt):
         for name, *_ in QWEN_LAYER:
             assert torch.equal(bufs[name], first[name]), (fmt, run, name, "deterministic")
         check_against_single_calls(fmt, bufs, weights, (fmt, "layer", run), chain_def=QWEN_LAYER)
-    for name in ("o", "dn"):
-        src = [c for c in QWEN_LAYER if c[0] == name][0][3]
-        assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name]) < 1e-2, name
+    for name, _, _, src, sw in QWEN_LAYER:  # every projection, gate_up through its SwiGLU
+        assert oracle_check(fmt, bits16(source(bufs, src)), raw[name], bufs[name], swiglu=sw) < 1e-2, name
 
 
 @pytest.mark.parametrize("kw", [1, 2, 4, 8])
