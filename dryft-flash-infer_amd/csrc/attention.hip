@@ -413,12 +413,13 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   }
 }
 
-// Merge of the split partials of one head (one workgroup per sequence x KV head): the splits in
-// use (se, from the same position) combine as in attention.py:144-178 -- weights
-// exp(max_s - max), weighted accumulators over weighted totals -- in a fixed order. ng thread
-// groups share an item's splits (contiguous ranges); a thread issues the loads of up to 16
-// splits at once (one memory round trip), merges them, and the groups' results combine in group
-// order through LDS. With one split in use the attention kernel wrote the output itself.
+// Merge of the split partials of one query row of one head (a workgroup per sequence x KV head
+// x row: its loads spread over that many CUs, not one per head): the splits in use (se, from
+// the same position) combine as in attention.py:144-178 -- weights exp(max_s - max), weighted
+// accumulators over weighted totals -- in a fixed order. ng thread groups share an item's
+// splits (contiguous ranges); a thread issues the loads of up to 16 splits at once (one memory
+// round trip), merges them, and the groups' results combine in group order through LDS. With
+// one split in use the attention kernel wrote the output itself.
 __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
   extern __shared__ float gbuf[];  // the groups' results: 6 floats per slot
   const int head = blockIdx.x;
@@ -429,8 +430,8 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
   const int nblk = end > 0 ? (end + 31) >> 5 : 0;
   const int se = max(1, min(a.splits, (nblk + 3) >> 2));
   if (se == 1) return;
-  const int items = a.R * 32;
-  const int ng = items >= 256 ? 1 : 256 / items;
+  const int items = 32, row = blockIdx.y;  // items: the row's 4-value chunks
+  const int ng = 256 / items;
   const int per = (se + ng - 1) / ng;
   const int slots = items * ng;
   const size_t nslot = (size_t)a.heads * a.splits * a.R;
@@ -441,7 +442,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
   float* gl = gm + slots;
   for (int w0 = threadIdx.x; w0 < slots; w0 += 256) {
     const int item = w0 % items, sg = w0 / items;
-    const int r = item >> 5, d4 = (item & 31) * 4;
+    const int r = row, d4 = (item & 31) * 4;
     const int s_lo = sg * per, s_hi = min(se, s_lo + per);
     float Mt = kNegInf, Lt = 0.f;
     f32x4 At = {0.f, 0.f, 0.f, 0.f};
@@ -489,7 +490,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
       A += f * ga[g2 * items + item];
       L += f * gl[g2 * items + item];
     }
-    const int r = item >> 5, d4 = (item & 31) * 4;
+    const int r = row, d4 = (item & 31) * 4;
     const int t = r / a.G, gi = r - t * a.G;
     uint16_t* o = a.out + ((size_t)(seq * a.T + t) * NQ + kvh * a.G + gi) * 128 + d4;
     *gmem(reinterpret_cast<u32x2*>(o)) = u32x2{pack_bf(A[0] / L, A[1] / L), pack_bf(A[2] / L, A[3] / L)};
@@ -500,8 +501,7 @@ template <int RT, bool Q8>
 static int launch_attn(const AttnArgs& a, int heads, hipStream_t st) {
   attn_kernel<RT, Q8><<<dim3(heads, a.splits), 256, (size_t)4 * a.R * 128 * sizeof(float), st>>>(a);
   if (a.splits > 1) {
-    const size_t items = (size_t)a.R * 32, slots = items >= 256 ? items : 256;
-    attn_merge_kernel<<<heads, 256, 6 * slots * sizeof(float), st>>>(a);
+    attn_merge_kernel<<<dim3(heads, a.R), 256, 6 * 256 * sizeof(float), st>>>(a);
   }
   QLX_LAUNCH_CHECK("decode attention");
 }
