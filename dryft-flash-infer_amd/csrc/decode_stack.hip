@@ -847,7 +847,7 @@ int check_shares(int groups, int ns, int U, int pe, int gran, int sps) {
 // 2 KB in every executor format), a fixed charge per item, and one extra dependency trip
 // when row blocks are cut into pieces.
 bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, int waves, int force_kw,
-                     int lds_limit, StackPlan& out) {
+                     int lds_limit, StackPlan& out, double stage_bytes = 0.0) {
   // An item costs about one memory round trip more than its bytes (staging, epilogue) and a
   // cut row block one more dependency trip: ~4 us, ~128 KB of one workgroup's stream.
   const double kStepBytes = 2048.0, kItemBytes = 131072.0, kPieceBytes = 98304.0;
@@ -888,7 +888,8 @@ bool plan_projection(const FmtInfo& fi, int mode, int m, int n, int k, int P, in
         const int max_np = check_shares(groups, ns, (int)U, pe, gran, sps);
         if (max_np < 1 || max_np > kMaxPieces) continue;
         const long long items = whole ? per / ns : (per + ns - 1) / ns + 1;
-        const double cost = (double)per * rt * kStepBytes + items * kItemBytes + (max_np > 1 ? kPieceBytes : 0.0);
+        const double cost = (double)per * rt * kStepBytes + items * kItemBytes + (max_np > 1 ? kPieceBytes : 0.0) +
+                            (double)per * stage_bytes;
         if (cost < best) {
           best = cost;
           found = true;
@@ -984,7 +985,14 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     int items_lds = 0;
     for (int c = 0; c < ncalls; ++c) {
       const qlx_stack_call& q = calls[c];
-      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c]),
+      // With published token maxima an FP8 item reads only its slice of a published input, 4
+      // bytes per value and token, after the input arrives (the weights were prefetched while
+      // it was awaited): the planner charges those bytes 4x a weight byte (measured on the
+      // Qwen3-4B FP8 chain, us per step at M = 8 / 16 by the factor: none 2914 / 3932, 1x 2641 /
+      // 3930, 2x 2642 / 3475, 3x 2462 / 3490, 4x 2412 / 3488, 6x 2422 / 3483).
+      const bool slice_staged = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM && src[c] >= 0;
+      const double stage_bytes = slice_staged ? 4.0 * 4.0 * fi.kstep * m : 0.0;
+      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c], stage_bytes),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
       GemmArgs a = {};
       const int l = exec_lds(fi, sp[c].plan, m, q.n, q.k, a);
