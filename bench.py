@@ -122,12 +122,13 @@ class Stack:
                 h = y
         return chain.build()
 
-    def norm_executor(self, eps=1e-6):
+    def norm_executor(self, eps=1e-6, stream=True):
         """The decode step with its residual adds and RMSNorms as input stages of the stream
-        executor: qkv <- rmsnorm(h), gate_up <- rmsnorm(h + o), the next qkv and the lm_head <-
-        rmsnorm(h + o + down) (FP8: the normed input quantized per token in the same stage)."""
-        from kernels.decode_stack import StreamStack
-        chain = StreamStack(self.fmt, self.m)
+        executor (or, with ``stream`` False, of the first executor): qkv <- rmsnorm(h), gate_up
+        <- rmsnorm(h + o), the next qkv and the lm_head <- rmsnorm(h + o + down) (FP8: the normed
+        input quantized per token in the same stage)."""
+        from kernels.decode_stack import DecodeStack, StreamStack
+        chain = StreamStack(self.fmt, self.m) if stream else DecodeStack(self.fmt, self.m)
         gen = torch.Generator(device="cuda").manual_seed(77)
         new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
         norm_w = lambda: (1.0 + 0.1 * torch.randn(2560, generator=gen, device="cuda")).to(torch.bfloat16)
@@ -350,20 +351,21 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
                                               "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
                                               "pieces": chain.launch.pieces != 0}
             del chain
-    if m <= 2:
-        # the full decode step's linear path with its residual adds and RMSNorms fused into the
-        # projections' input stages (stream executor); not the headline, which is the linears alone
+    # the full decode step's linear path with its residual adds and RMSNorms fused into the
+    # projections' input stages (either executor); not the headline, which is the linears alone
+    for stream, key, top in ((True, "norm_chain_us", 2), (False, "stack_norm_chain_us", 4)):
+        if m > top:
+            continue
         try:
-            chain = stack.norm_executor()
+            chain = stack.norm_executor(stream=stream)
         except ValueError as e:  # the builder's own limits
-            chain = None
-            out["norm_chain_unsupported"] = str(e)
-        if chain is not None:
-            ms_norm = time_fn(chain.run, steps, warmup)
-            if chain.failed():
-                raise RuntimeError("stream executor with norm stages: a wait gave up")
-            out["norm_chain_us"] = round(ms_norm * 1e3, 2)
-            del chain
+            out[key.replace("_us", "_unsupported")] = str(e)
+            continue
+        ms_norm = time_fn(chain.run, steps, warmup)
+        if chain.failed():
+            raise RuntimeError("executor with norm stages: a wait gave up")
+        out[key] = round(ms_norm * 1e3, 2)
+        del chain
     cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
     ms = cands[out["path"]] / 1e3
@@ -704,6 +706,7 @@ def main():
                      "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
                      "executor_shapes": head.get("shapes_us"),
                      # the step with its residual adds and RMSNorms fused into the input stages
+                     "executor_with_norm_stages": head.get("stack_norm_chain_us"),
                      "stream_executor_with_norm_stages": head.get("norm_chain_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),

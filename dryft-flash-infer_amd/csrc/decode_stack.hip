@@ -64,6 +64,18 @@ struct alignas(16) StackDesc {
   int xmax_pitch;        // the producer's ymax_pitch
   int xmax_n;            // the producer's tiles that make up this projection's k columns
   int xmax_rt;           // the producer's tiles per row block
+  // Residual add + RMSNorm input stage (nw non-null): the input is
+  // bf16(bf16(r * rsqrt(mean(r^2) + eps)) * nw) with r = bf16(resid + delta), delta the
+  // published output xwire points at (if any), resid in memory (rmem) or published by an
+  // earlier stage (rwire, [m][k] words). The workgroup holding row block 0 (piece 0) writes r
+  // to rout and the input to nout (either may be null) and publishes r to rpub.
+  const void* nw;
+  const void* rmem;
+  const uint64_t* rwire;
+  void* rout;
+  void* nout;
+  uint64_t* rpub;
+  float eps;
 };
 
 constexpr int kMaxLine = 32;  // maxima words per row block: one 128-byte line
@@ -420,6 +432,152 @@ __device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs
   }
 }
 
+// Chunks of 8 values each thread holds through a norm stage: the stage is one pass over its
+// rows (m * k / 8 <= kNormU * threads, checked on the host).
+constexpr int kNormU = 3;
+
+// Residual add + RMSNorm input stage of an item (see StackDesc.nw): every workgroup with work in
+// the projection computes r and the normed input from the same words in the same order -- the
+// sum of r^2 per token in fp64, per 8-value chunk, then the token's chunks lane-strided and the
+// lanes in a fixed tree; mean rounded to fp32, scale = 1 / sqrt(mean + eps) in fp32; input
+// bf16(bf16(r * scale) * w) (norm.py:53-80, reference.py:13-28) -- and stages its slice of that
+// input like any activation (FP8: quantized per token over the whole normed row). The owner
+// (row block 0) also writes r and the input and publishes r. `css` holds m * k / 8 + 16 doubles.
+template <class F, int U>
+__device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
+                                           double* css, bool owner, const Waits& w) {
+  constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
+  const GemmArgs& a = d.a;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
+  const int cpr = a.k >> 3, total = a.m * cpr;
+  const bool has_delta = d.xwire != nullptr, rwire = d.rwire != nullptr;
+  const XWire dx(has_delta ? d.xwire : nullptr, has_delta ? d.xpitch : 0, a.m, w);
+  const XWire rx(rwire ? d.rwire : nullptr, rwire ? a.k : 0, a.m, w);
+  auto chunk = [&](int u, int& mm, int& kabs) {
+    const int q = tid + u * nthr;
+    mm = q / cpr;
+    kabs = (q - mm * cpr) * 8;
+    return q < total;
+  };
+  XWire::Raw rd[U], rr[U];
+  uint4 rp[U], wv[U], rv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      if (has_delta) dx.fetch(a, mm, kabs, rd[u]);
+      if (rwire) {
+        rx.fetch(a, mm, kabs, rr[u]);
+      } else {
+        const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(d.rmem) +
+                                                              (size_t)mm * a.k + kabs));
+        rp[u] = uint4{t[0], t[1], t[2], t[3]};
+      }
+      const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(d.nw) + kabs));
+      wv[u] = uint4{t[0], t[1], t[2], t[3]};
+    }
+  }
+  if (has_delta) settle_batch<XWire, U>(a, dx, rd, chunk);
+  if (rwire) settle_batch<XWire, U>(a, rx, rr, chunk);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      const uint4 x = rwire ? rx.value(rr[u]) : rp[u];
+      uint4 r = x;
+      if (has_delta) {
+        const uint4 dv = dx.value(rd[u]);
+        const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ds[4] = {dv.x, dv.y, dv.z, dv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = bf16_pair(bf2f(xs[i] & 0xffffu) + bf2f(ds[i] & 0xffffu), bf2f(xs[i] >> 16) + bf2f(ds[i] >> 16));
+        r = uint4{o[0], o[1], o[2], o[3]};
+      }
+      rv[u] = r;
+      const uint32_t rs[4] = {r.x, r.y, r.z, r.w};
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double lo = bf2f(rs[i] & 0xffffu), hi = bf2f(rs[i] >> 16);
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+      css[tid + u * nthr] = ss;
+    }
+  }
+  __syncthreads();
+  double* tot = css + total;
+  for (int t = tid >> 6; t < a.m; t += nthr >> 6) {  // token t's total, by one wave
+    double sum = 0.0;
+    for (int c = lane; c < cpr; c += 64) sum += css[t * cpr + c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) tot[t] = sum;
+  }
+  __syncthreads();
+  // The normed input of chunk u (and its largest magnitude): mean rounded to fp32, + eps and
+  // 1/sqrt in fp32, as torch's rsqrt(mean + eps).
+  auto normed_chunk = [&](int u, int mm, float& mx) {
+    const float scale = 1.0f / sqrtf((float)(tot[mm] / (double)a.k) + d.eps);
+    const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+    uint32_t o[4];
+    mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale) * bf2f(ws[i] & 0xffffu));
+      const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale) * bf2f(ws[i] >> 16));
+      o[i] = bf16_pair(y0, y1);
+      mx = fmaxf(mx, fmaxf(fabsf(y0), fabsf(y1)));
+    }
+    return uint4{o[0], o[1], o[2], o[3]};
+  };
+  const int c0 = step0 * (F::KSTEP / 8), c1 = c0 + nst * (F::KSTEP / 8);  // the slice's chunks of a row
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int mm, kabs;
+    if (chunk(u, mm, kabs)) {
+      float mx;
+      const uint4 y = normed_chunk(u, mm, mx);
+      const uint32_t o[4] = {y.x, y.y, y.z, y.w};
+      if constexpr (!FP8) {
+        const int kc = kabs >> 3;
+        if (kc >= c0 && kc < c1)
+          *reinterpret_cast<uint4*>(lds + mm * a.xstride + (kabs - step0 * F::KSTEP) * 2) = F::order(y);
+      }
+      if (owner) {
+        const size_t e = (size_t)mm * a.k + kabs;
+        if (d.rout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.rout) + e)) =
+                        u32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+        if (d.nout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.nout) + e)) =
+                        u32x4{o[0], o[1], o[2], o[3]};
+        if (d.rpub) {
+          const uint32_t rs2[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wire_store_pair(d.rpub + (e >> 1) + i, rs2[i], w.epoch);
+        }
+      }
+      if constexpr (FP8) atomicMax(&amax[mm], __float_as_uint(mx));
+    }
+  }
+  if constexpr (FP8) {  // the codes of the slice, at the token scales of the whole normed rows
+    __syncthreads();
+    float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+    auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
+    for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int mm, kabs;
+      if (chunk(u, mm, kabs)) {
+        const int kc = kabs >> 3;
+        float mx;
+        if (kc >= c0 && kc < c1)
+          store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, normed_chunk(u, mm, mx), token_scale(mm));
+      }
+    }
+  }
+}
+
 // Stage what the item needs in LDS and stream its weight steps through the MFMAs. With
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
 // projection, same steps -- is still in place. With poller waves (NP > 0) they stage the
@@ -427,7 +585,8 @@ __device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs
 template <class F, int WAVES, int NP, bool PIECES, class XS>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
                                           uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS], f32x4 (&acc)[1][1],
-                                          uint32_t* amax, const MaxIn& mi = {}) {
+                                          uint32_t* amax, const MaxIn& mi = {}, const StackDesc* nd = nullptr,
+                                          const Waits* nw = nullptr) {
   constexpr int PF = ExecDepth<F, PIECES>::PF;
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
@@ -435,7 +594,14 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
   if (!reuse) {
     if constexpr (NP == 0) {
-      if constexpr (FP8) {
+      if (nd) {  // a residual add + RMSNorm stage (no poller waves: checked on the host)
+        double* css = reinterpret_cast<double*>(reinterpret_cast<char*>(amax) + 64);
+        const bool owner = it.tg == 0 && it.s == 0;
+        if (a.m * (a.k >> 3) <= (int)blockDim.x)  // one chunk per thread (every M = 1 stage)
+          stage_norm<F, 1>(*nd, lds, step0, nst, amax, css, owner, *nw);
+        else
+          stage_norm<F, kNormU>(*nd, lds, step0, nst, amax, css, owner, *nw);
+      } else if constexpr (FP8) {
         bool done = false;
         if constexpr (XS::POLLS) {
           if (mi.p) {
@@ -732,11 +898,12 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     const StackDesc& d = calls[c];
     cur = nxt;
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
-    if (d.xwire)
+    if (d.xwire && !d.nw)
       exec_main<F, WAVES, NP, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax,
                                       MaxIn{NP == 0 ? d.xmax : nullptr, d.xmax_pitch, d.xmax_n, d.xmax_rt});
-    else
-      exec_main<F, WAVES, NP, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax);
+    else  // x in memory, or a norm stage (one call site: the kernel's code stays as small)
+      exec_main<F, WAVES, NP, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax, MaxIn{}, d.nw ? &d : nullptr,
+                                      &w);
     staged_c = c;
     staged_step0 = cur.step0;
     staged_nst = cur.nst;
@@ -923,6 +1090,13 @@ int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
                     int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
                     qlx_stack_launch* launch) {
+  return qlx_stack_build_normed(fmt, m, calls, ncalls, nullptr, waves, groups_per_cu, pollers, desc, plans, arena,
+                                arena_bytes, launch);
+}
+
+int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                           int waves, int groups_per_cu, int pollers, void* desc, qlx_plan* plans, void* arena,
+                           long long* arena_bytes, qlx_stack_launch* launch) {
   QLX_REQUIRE(stack_fn_for(fmt, 8, 0, false, false) != nullptr,
               "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
@@ -935,10 +1109,12 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
   QLX_REQUIRE(stack_shape_ok(waves, pollers), "poller waves run beside 4 compute waves (waves=%d, pollers=%d)", waves,
               pollers);
   const FmtInfo fi = stack_info(fmt);
+  auto normed = [&](int c) { return norms != nullptr && norms[c].norm_w != nullptr; };
   // Shapes, and which earlier projection (if any) produces each activation. Outputs may not
   // overlap each other or an activation read from memory: the chain has no ordering between
   // projections other than these data dependencies.
-  std::vector<int> src(ncalls, -1), published(ncalls, 0);
+  std::vector<int> src(ncalls, -1), published(ncalls, 0), rsrc(ncalls, -1), rpublished(ncalls, 0);
+  int css_doubles = 0;  // LDS of the widest norm stage's per-chunk sums
   for (int c = 0; c < ncalls; ++c) {
     const qlx_stack_call& q = calls[c];
     QLX_REQUIRE(q.kw == 0 || q.kw == 1 || q.kw == 2 || q.kw == 4 || q.kw == 8,
@@ -946,14 +1122,59 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     QLX_REQUIRE(q.n >= 16 && q.n % 16 == 0 && q.k > 0 && q.k % fi.kstep == 0,
                 "projection %d: n=%d k=%d do not fit the tiled format", c, q.n, q.k);
     QLX_REQUIRE(q.mode == QLX_MODE_BF16 || q.mode == QLX_MODE_SWIGLU, "projection %d: mode %d", c, q.mode);
-    QLX_REQUIRE(q.w && q.w_scale && q.x && q.y, "projection %d: NULL pointer", c);
+    QLX_REQUIRE(q.w && q.w_scale && q.y && (normed(c) ? q.x == nullptr : q.x != nullptr),
+                "projection %d: NULL pointer (x must be NULL exactly when the input is a norm stage)", c);
+    if (normed(c)) {
+      QLX_REQUIRE(norms[c].resid != nullptr, "projection %d: a norm stage needs its residual", c);
+      QLX_REQUIRE(pollers == 0, "projection %d: norm stages run on workgroups without poller waves", c);
+      QLX_REQUIRE(m * (q.k / 8) <= kNormU * waves * 64,
+                  "projection %d: a norm stage takes m * k <= %d (one pass; m=%d, k=%d)", c, kNormU * waves * 64 * 8,
+                  m, q.k);
+      css_doubles = std::max(css_doubles, m * (q.k / 8) + 16);
+    }
   }
   auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };
+  // memory a projection or a norm stage writes
+  auto written = [&](const void* p, long long bytes) {
+    for (int j = 0; j < ncalls; ++j) {
+      if (overlaps(p, bytes, calls[j].y, 2LL * m * nout(j))) return true;
+      if (normed(j) && norms[j].resid_out && overlaps(p, bytes, norms[j].resid_out, 2LL * m * calls[j].k)) return true;
+      if (normed(j) && norms[j].normed_out && overlaps(p, bytes, norms[j].normed_out, 2LL * m * calls[j].k))
+        return true;
+    }
+    return false;
+  };
   for (int c = 0; c < ncalls; ++c) {
     const long long ybytes = 2LL * m * nout(c);
     for (int j = 0; j < ncalls; ++j) {
       if (j != c) QLX_REQUIRE(!overlaps(calls[c].y, ybytes, calls[j].y, 2LL * m * nout(j)),
                               "outputs of projections %d and %d overlap", c, j);
+    }
+    if (normed(c)) {
+      const qlx_norm_input& nd = norms[c];
+      const long long rbytes = 2LL * m * calls[c].k;
+      if (nd.delta) {
+        for (int j = 0; j < c; ++j)
+          if (nd.delta == calls[j].y && calls[c].k == nout(j)) {
+            src[c] = j;
+            published[j] = 1;
+            break;
+          }
+        QLX_REQUIRE(src[c] >= 0, "projection %d: the delta of a norm stage is the whole output of an earlier "
+                    "projection", c);
+      }
+      for (int j = 0; j < c; ++j)
+        if (normed(j) && norms[j].resid_out && nd.resid == norms[j].resid_out && calls[j].k == calls[c].k) {
+          rsrc[c] = j;
+          rpublished[j] = 1;
+          break;
+        }
+      QLX_REQUIRE(rsrc[c] >= 0 || !written(nd.resid, rbytes),
+                  "projection %d: the residual is memory the chain writes (only an earlier stage's resid_out can "
+                  "be)", c);
+      QLX_REQUIRE(!nd.resid_out || !overlaps(nd.resid_out, rbytes, nd.resid, rbytes),
+                  "projection %d: resid_out overlaps the residual", c);
+      continue;
     }
     const long long xbytes = 2LL * m * calls[c].k;
     for (int j = 0; j < ncalls; ++j) {
@@ -964,10 +1185,9 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       }
     }
     if (src[c] < 0)
-      for (int j = 0; j < ncalls; ++j)
-        QLX_REQUIRE(!overlaps(calls[c].x, xbytes, calls[j].y, 2LL * m * nout(j)),
-                    "projection %d reads memory that projection %d writes (only the whole output of an "
-                    "earlier projection can be an input)", c, j);
+      QLX_REQUIRE(!written(calls[c].x, xbytes),
+                  "projection %d reads memory the chain writes (only the whole output of an earlier projection "
+                  "can be an input)", c);
   }
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -990,7 +1210,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       // it was awaited): the planner charges those bytes 4x a weight byte (measured on the
       // Qwen3-4B FP8 chain, us per step at M = 8 / 16 by the factor: none 2914 / 3932, 1x 2641 /
       // 3930, 2x 2642 / 3475, 3x 2462 / 3490, 4x 2412 / 3488, 6x 2422 / 3483).
-      const bool slice_staged = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM && src[c] >= 0;
+      const bool slice_staged = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM && src[c] >= 0 && !normed(c);
       const double stage_bytes = slice_staged ? 4.0 * 4.0 * fi.kstep * m : 0.0;
       QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c], stage_bytes),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
@@ -999,7 +1219,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       if (l > items_lds) items_lds = l;
     }
     amax_off = (items_lds + 15) & ~15;
-    const int items_end = amax_off + 64;
+    const int items_end = amax_off + 64 + 8 * css_doubles;  // FP8 row maxima, norm stages' sums
     desc_lds = items_end + desc_bytes <= kLdsLimit ? items_end : -1;
     lds = desc_lds >= 0 ? (int)(items_end + desc_bytes) : items_end;
     pieces = false;
@@ -1033,7 +1253,7 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
   };
   // Arena: published outputs (and their maxima) and partial sums, 256-byte aligned regions.
   long long off = 0;
-  std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1), max_off(ncalls, -1);
+  std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1), max_off(ncalls, -1), rpub_off(ncalls, -1);
   for (int c = 0; c < ncalls; ++c) {
     if (published[c]) {
       wire_off[c] = off;
@@ -1047,6 +1267,10 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
     if (sp[c].max_np > 1) {
       part_off[c] = off;
       off += ((8LL * (sp[c].max_np - 1) * m * calls[c].n) + 255) & ~255LL;
+    }
+    if (rpublished[c]) {  // a norm stage's r, read by later stages
+      rpub_off[c] = off;
+      off += ((4LL * m * calls[c].k) + 255) & ~255LL;
     }
   }
   StackDesc* out = reinterpret_cast<StackDesc*>(desc);
@@ -1081,6 +1305,20 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
       }
     }
     d.units = sp[c].units;
+    if (normed(c)) {
+      const qlx_norm_input& nd = norms[c];
+      d.nw = nd.norm_w;
+      d.eps = nd.eps;
+      d.rout = nd.resid_out;
+      d.nout = nd.normed_out;
+      if (base) {
+        if (rsrc[c] >= 0)
+          d.rwire = reinterpret_cast<const uint64_t*>(base + rpub_off[rsrc[c]]);
+        else
+          d.rmem = nd.resid;
+        d.rpub = rpub_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + rpub_off[c]) : nullptr;
+      }
+    }
     d.nwg = P;
     d.rot = rot;
     rot = (rot + sp[c].pe) % P;

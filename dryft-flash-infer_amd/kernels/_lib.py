@@ -118,6 +118,8 @@ SIGNATURES = {
     "qlx_stack_desc_size": ([], _I),
     "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
                          ctypes.POINTER(StackLaunch)], _I),
+    "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _I, _P,
+                                _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_build": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _P, _PLL, _P, _PLL,
                           ctypes.POINTER(StreamLaunch)],

@@ -16,7 +16,8 @@ weights while its input is still being produced, and wait only for the words the
 Inputs and outputs are caller-owned bf16 tensors that stay in place between runs (the
 descriptors hold their addresses), like the static buffers of a captured decode graph. An
 input is either memory no projection of the chain writes, or an earlier projection's output
-tensor -- whole, or its first columns (``y_qkv[:, :4096]``, the attention's query part).
+tensor -- whole, or its first columns (``y_qkv[:, :4096]``, the attention's query part) -- or,
+with ``add_normed``, a residual add + RMSNorm of them computed inside the same launch.
 """
 
 import ctypes
@@ -50,6 +51,7 @@ class DecodeStack:
         self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
         self.pollers = pollers
         self.calls, self._keep = [], []
+        self.norms = []
         self.desc = None
         self.epoch = 0
 
@@ -74,7 +76,46 @@ class DecodeStack:
         self.calls.append(_lib.StackCall(weight.weight.data_ptr(), weight.scale.data_ptr(), x.data_ptr(),
                                          y.data_ptr(), weight.rows, weight.k,
                                          _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, int(kw)))
+        self.norms.append(_lib.NormInput())
         self._keep += [weight, x, y]
+        self.desc = None
+        return self
+
+    def add_normed(self, weight, resid, y, norm_w, eps, delta=None, resid_out=None, normed_out=None,
+                   swiglu=False):
+        """Append a projection of bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
+        r = bf16(resid + delta) (r = resid without delta), the residual add + RMSNorm run inside
+        the launch (norm.py:53-80, 125-154). ``resid`` is memory the chain does not write or an
+        earlier stage's ``resid_out``; ``delta`` the output tensor of an earlier projection;
+        ``resid_out`` / ``normed_out`` (optional) receive r and the normed input. FP8 W8A8
+        quantizes the normed input per token inside the same stage. A whole decode layer:
+
+            chain.add_normed(qkv, h_in, y_qkv, w_in, eps, resid_out=h0)          # rmsnorm(h_in)
+            chain.add(o, y_qkv[:, :4096], y_o)
+            chain.add_normed(gate_up, h0, y_act, w_post, eps, delta=y_o, resid_out=h1, swiglu=True)
+            chain.add(down, y_act, y_down)
+            chain.add_normed(next_qkv, h1, ..., delta=y_down, resid_out=h2)      # the next layer
+        """
+        if not isinstance(weight, Tiled) or weight.fmt != self.fmt:
+            raise ValueError(f"the chain takes {self.fmt} weights in tile layout (qlinear.prepare)")
+        shape = (self.m, weight.k)
+        tensors = [resid, norm_w] + [t for t in (delta, resid_out, normed_out) if t is not None]
+        _lib.require_device(weight.weight, weight.scale, y, *tensors)
+        for name, t in (("resid", resid), ("delta", delta), ("resid_out", resid_out), ("normed_out", normed_out)):
+            if t is not None and (t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous bf16 [{self.m}, {weight.k}] tensor")
+        if norm_w.dtype != torch.bfloat16 or tuple(norm_w.shape) != (weight.k,):
+            raise ValueError(f"norm_w must be bf16 [{weight.k}]")
+        out_n = weight.rows // 2 if swiglu else weight.rows
+        if y.dtype != torch.bfloat16 or tuple(y.shape) != (self.m, out_n):
+            raise ValueError(f"y must be bf16 [{self.m}, {out_n}]")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self.calls.append(_lib.StackCall(weight.weight.data_ptr(), weight.scale.data_ptr(), None, y.data_ptr(),
+                                         weight.rows, weight.k, _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, 0))
+        self.norms.append(_lib.NormInput(ptr(resid), ptr(delta), ptr(norm_w), ptr(resid_out), ptr(normed_out),
+                                         float(eps), 0))
+        self._keep += [weight, resid, y]
+        self._extra = getattr(self, "_extra", []) + tensors
         self.desc = None
         return self
 
@@ -85,18 +126,20 @@ class DecodeStack:
         device = self._keep[0].weight.device
         lib = _lib.lib()
         arr = (_lib.StackCall * len(self.calls))(*self.calls)
+        norms = (_lib.NormInput * len(self.norms))(*self.norms)
         fmt = _FMTS[self.fmt]
         arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
             opts = (self.waves, self.groups_per_cu, self.pollers)
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), *opts, None, None, None, arena_bytes,
-                                           launch), "qlx_stack_build")
+            _lib.check(lib.qlx_stack_build_normed(fmt, self.m, arr, len(self.calls), norms, *opts, None, None, None,
+                                                  arena_bytes, launch), "qlx_stack_build_normed")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
             self.error = torch.zeros(1, dtype=torch.int32, device=device)
             host = torch.empty(lib.qlx_stack_desc_size() * len(self.calls), dtype=torch.uint8)
             plans = (_lib.Plan * len(self.calls))()
-            _lib.check(lib.qlx_stack_build(fmt, self.m, arr, len(self.calls), *opts, ctypes.c_void_p(host.data_ptr()),
-                                           plans, _lib.ptr(self.arena), arena_bytes, launch), "qlx_stack_build")
+            _lib.check(lib.qlx_stack_build_normed(fmt, self.m, arr, len(self.calls), norms, *opts,
+                                                  ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.arena),
+                                                  arena_bytes, launch), "qlx_stack_build_normed")
             self.desc = host.to(device)
         #: (waves, kw, rw, most K pieces of one row block) per projection
         self.configs = [(p.waves, p.kw, p.rw, p.splits) for p in plans]
@@ -148,56 +191,12 @@ class StreamStack(DecodeStack):
     direct-to-LDS loads, running ahead across projections, while four IO waves poll, stage,
     reduce and publish, so no poll ever waits behind a weight load. Each projection's tiles go
     whole to workgroups; a tile's output is the fixed-order sum of eight K-interleaved partial
-    sums (deterministic). ``add`` takes the same arguments (``kw`` is ignored).
-
-    ``add_normed`` appends a projection whose input is a residual add + RMSNorm stage, so a
-    chain can be a whole decode layer's linear path:
-
-        chain.add_normed(qkv, h_in, y_qkv, w_in, eps, resid_out=h0)          # rmsnorm(h_in)
-        chain.add(o, y_qkv[:, :4096], y_o)
-        chain.add_normed(gate_up, h0, y_act, w_post, eps, delta=y_o, resid_out=h1, swiglu=True)
-        chain.add(down, y_act, y_down)
-        chain.add_normed(next_qkv, h1, ..., delta=y_down, resid_out=h2)      # the next layer
+    sums (deterministic). ``add`` and ``add_normed`` take the same arguments (``kw`` is
+    ignored).
     """
 
     def __init__(self, fmt, m):
         super().__init__(fmt, m)
-        self.norms = []
-
-    def add(self, weight, x, y, swiglu=False, kw=0):
-        super().add(weight, x, y, swiglu, kw)
-        self.norms.append(_lib.NormInput())
-        return self
-
-    def add_normed(self, weight, resid, y, norm_w, eps, delta=None, resid_out=None, normed_out=None,
-                   swiglu=False):
-        """Append a projection of bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
-        r = bf16(resid + delta) (r = resid without delta). ``resid`` is memory the chain does not
-        write or an earlier stage's ``resid_out``; ``delta`` the output tensor of an earlier
-        projection; ``resid_out`` / ``normed_out`` (optional) receive r and the normed input.
-        FP8 W8A8 quantizes the normed input per token inside the same stage."""
-        if not isinstance(weight, Tiled) or weight.fmt != self.fmt:
-            raise ValueError(f"the chain takes {self.fmt} weights in tile layout (qlinear.prepare)")
-        shape = (self.m, weight.k)
-        tensors = [resid, norm_w] + [t for t in (delta, resid_out, normed_out) if t is not None]
-        _lib.require_device(weight.weight, weight.scale, y, *tensors)
-        for name, t in (("resid", resid), ("delta", delta), ("resid_out", resid_out), ("normed_out", normed_out)):
-            if t is not None and (t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous()):
-                raise ValueError(f"{name} must be a contiguous bf16 [{self.m}, {weight.k}] tensor")
-        if norm_w.dtype != torch.bfloat16 or tuple(norm_w.shape) != (weight.k,):
-            raise ValueError(f"norm_w must be bf16 [{weight.k}]")
-        out_n = weight.rows // 2 if swiglu else weight.rows
-        if y.dtype != torch.bfloat16 or tuple(y.shape) != (self.m, out_n):
-            raise ValueError(f"y must be bf16 [{self.m}, {out_n}]")
-        ptr = lambda t: None if t is None else t.data_ptr()
-        self.calls.append(_lib.StackCall(weight.weight.data_ptr(), weight.scale.data_ptr(), None, y.data_ptr(),
-                                         weight.rows, weight.k, _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, 0))
-        self.norms.append(_lib.NormInput(ptr(resid), ptr(delta), ptr(norm_w), ptr(resid_out), ptr(normed_out),
-                                         float(eps), 0))
-        self._keep += [weight, resid, y]
-        self._extra = getattr(self, "_extra", []) + tensors
-        self.desc = None
-        return self
 
     def build(self):
         if not self.calls:

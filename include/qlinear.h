@@ -355,6 +355,20 @@ typedef struct qlx_norm_input {
   int pad;
 } qlx_norm_input;
 
+/* qlx_stack_build with residual add + RMSNorm input stages (f1): where norms[c].norm_w is not
+ * NULL, projection c's input is bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
+ * r = bf16(resid + delta) (r = resid without delta), computed inside the launch by every
+ * workgroup with work in the projection; calls[c].x is NULL exactly then. `resid` is memory the
+ * chain does not write or an earlier stage's resid_out; `delta` is the whole output of an
+ * earlier projection; resid_out / normed_out (optional) receive r and the input (FP8 W8A8:
+ * quantized per token over the normed row). A norm stage needs no poller waves and one pass
+ * over its rows: m * k <= 3 * 64 * waves * 8. norms may be NULL (= qlx_stack_build). Replaces
+ * the reference's plane consumers and residual + RMSNorm kernels between projections
+ * (engine/kernels/norm.py:53-80, 125-154; engine/kernels/cuda_small.py:43-87). */
+int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                           int waves, int groups_per_cu, int pollers, void* desc, qlx_plan* plans, void* arena,
+                           long long* arena_bytes, qlx_stack_launch* launch);
+
 /* Launch configuration of a stream-executor chain, filled by qlx_stream_build. */
 typedef struct qlx_stream_launch {
   int grid;          /* workgroups, one per CU (cooperative launch) */

@@ -14,7 +14,7 @@ import torch
 
 import oracle as O
 from kernels import qlinear
-from kernels.decode_stack import StreamStack
+from kernels.decode_stack import DecodeStack, StreamStack
 from test_gpu_decode_stack import CHAIN, DEV, QWEN_LAYER, bits16, check_against_single_calls, oracle_check, rand, \
     source
 
@@ -94,12 +94,12 @@ def test_stream_bounded_wait_gives_up_and_recovers():
     check_against_single_calls("fp8", bufs, weights, "stream after reset")
 
 
-def build_norm_chain(fmt, m, seed, layers=2):
+def build_norm_chain(fmt, m, seed, layers=2, cls=StreamStack):
     """`layers` Qwen3-4B layers with their residual adds and RMSNorms inside the chain, then a
     final norm into a small head: qkv <- rmsnorm(h); o; gate_up <- rmsnorm(h + o); down; the next
-    qkv <- rmsnorm(h + o + down); ..."""
+    qkv <- rmsnorm(h + o + down); ... (on the stream executor, or on the first executor)."""
     quant = qlinear.FORMATS[fmt][0]
-    chain = StreamStack(fmt, m)
+    chain = cls(fmt, m)
     bufs = {"h_in": rand((m, 2560), seed).to(DEV)}
     weights, raw, stages = {}, {}, []
     eps = 1e-6
@@ -141,14 +141,18 @@ def build_norm_chain(fmt, m, seed, layers=2):
     return chain, bufs, weights, raw, stages
 
 
-@pytest.mark.parametrize("fmt,m", [("fp8", 1), ("w4a16", 1), ("w8a16", 1), ("fp8", 2)])
-def test_stream_decode_layers_with_residual_and_norm(fmt, m):
-    """Residual add + RMSNorm (+ FP8 per-token quantize) as input stages of the stream executor:
+@pytest.mark.parametrize("executor", ["stream", "stack"])
+@pytest.mark.parametrize("fmt,m", [("fp8", 1), ("w4a16", 1), ("w8a16", 1), ("fp8", 2), ("w4a16", 3)])
+def test_decode_layers_with_residual_and_norm(fmt, m, executor):
+    """Residual add + RMSNorm (+ FP8 per-token quantize) as input stages of either executor:
     every stage's residual and normed input are bit-exact against the oracle on the chain's own
     inputs, every projection agrees with the single-call linear on its stage's normed input (and
     o / down with the oracle), and two runs are bitwise equal."""
-    print(f"stream exec norm chain {fmt} m={m}", flush=True)
-    chain, bufs, weights, raw, stages = build_norm_chain(fmt, m, 700 + m)
+    if executor == "stream" and m > 2:
+        pytest.skip("the stream executor's norm stages take at most 2 tokens at k = 2560")
+    print(f"{executor} exec norm chain {fmt} m={m}", flush=True)
+    cls = StreamStack if executor == "stream" else DecodeStack
+    chain, bufs, weights, raw, stages = build_norm_chain(fmt, m, 700 + m, cls=cls)
     linear = qlinear.FORMATS[fmt][1]
     for run in range(2):
         if run:
