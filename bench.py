@@ -35,10 +35,8 @@ LAYERS = 36
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
-#: Executors timed per stack: the stream executor, and the first one with 8 compute waves.
-EXECUTOR_SHAPES = (("stream", 0), (8, 0))
-#: Largest batch the stream executor takes per format (its staged activation must fit LDS).
-STREAM_MAX_M = {"fp8": 2, "w8a16": 1, "w4a16": 1}
+#: Executor shapes timed per stack: 8 compute waves, no poller waves.
+EXECUTOR_SHAPES = ((8, 0),)
 
 
 def log(*a):
@@ -103,12 +101,10 @@ class Stack:
             else:  # down, lm_head
                 q = h = self.linear(h if name == "lm_head" else q, packed)
 
-    def executor(self, waves=8, lanes=1, pollers=0, stream=False):
-        """The same chain as one decode-step executor launch (outputs preallocated): the first
-        executor, or with ``stream`` the stream executor."""
-        from kernels.decode_stack import DecodeStack, StreamStack
-        chain = StreamStack(self.fmt, self.m) if stream else DecodeStack(self.fmt, self.m, waves=waves,
-                                                                           groups_per_cu=lanes, pollers=pollers)
+    def executor(self, waves=8, lanes=1, pollers=0):
+        """The same chain as one decode-step executor launch (outputs preallocated)."""
+        from kernels.decode_stack import DecodeStack
+        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, pollers=pollers)
         self.outs = []
         h = self.x[2560]
         q = None
@@ -122,13 +118,12 @@ class Stack:
                 h = y
         return chain.build()
 
-    def norm_executor(self, eps=1e-6, stream=True):
-        """The decode step with its residual adds and RMSNorms as input stages of the stream
-        executor (or, with ``stream`` False, of the first executor): qkv <- rmsnorm(h), gate_up
-        <- rmsnorm(h + o), the next qkv and the lm_head <- rmsnorm(h + o + down) (FP8: the normed
-        input quantized per token in the same stage)."""
-        from kernels.decode_stack import DecodeStack, StreamStack
-        chain = StreamStack(self.fmt, self.m) if stream else DecodeStack(self.fmt, self.m)
+    def norm_executor(self, eps=1e-6):
+        """The decode step with its residual adds and RMSNorms as input stages of the executor:
+        qkv <- rmsnorm(h), gate_up <- rmsnorm(h + o), the next qkv and the lm_head <-
+        rmsnorm(h + o + down) (FP8: the normed input quantized per token in the same stage)."""
+        from kernels.decode_stack import DecodeStack
+        chain = DecodeStack(self.fmt, self.m)
         gen = torch.Generator(device="cuda").manual_seed(77)
         new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
         norm_w = lambda: (1.0 + 0.1 * torch.randn(2560, generator=gen, device="cuda")).to(torch.bfloat16)
@@ -325,15 +320,11 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
     del g
     out = {"graph_us": ms_graph * 1e3}
     if m <= 16:
-        # The executor in each workgroup shape: 8 compute waves, or 4 with 0, 2 or 4 poller waves
-        # (waves that only read and stage the published activations).
+        # The executor in each workgroup shape timed (compute waves, poller waves).
         for waves, pollers in EXECUTOR_SHAPES:
-            stream = waves == "stream"
-            if stream and m > STREAM_MAX_M.get(fmt, 0):
-                continue
-            key = "stream" if stream else f"{waves}c{pollers}p"
+            key = f"{waves}c{pollers}p"
             try:
-                chain = stack.executor(waves=waves, pollers=pollers, stream=stream)
+                chain = stack.executor(waves=waves, pollers=pollers)
             except ValueError as e:  # the builder's own limits (LDS, shapes): no such launch here
                 out.setdefault("shapes_unsupported", {})[key] = str(e)
                 continue
@@ -343,29 +334,24 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
             out.setdefault("shapes_us", {})[key] = round(ms_exec * 1e3, 2)
             if ms_exec * 1e3 < out.get("executor_us", 1e30):
                 out["executor_us"] = ms_exec * 1e3
-                if stream:
-                    out["executor_launch"] = {"kind": "stream", "grid": chain.grid, "lds": chain.lds,
-                                              "ring_lines": chain.launch.ring_lines}
-                else:
-                    out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": waves,
-                                              "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
-                                              "pieces": chain.launch.pieces != 0}
+                out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": waves,
+                                          "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
+                                          "pieces": chain.launch.pieces != 0}
             del chain
-    # the full decode step's linear path with its residual adds and RMSNorms fused into the
-    # projections' input stages (either executor); not the headline, which is the linears alone
-    for stream, key, top in ((True, "norm_chain_us", 2), (False, "stack_norm_chain_us", 4)):
-        if m > top:
-            continue
+    if m <= 4:
+        # the full decode step's linear path with its residual adds and RMSNorms fused into the
+        # projections' input stages; not the headline, which is the linears alone
         try:
-            chain = stack.norm_executor(stream=stream)
+            chain = stack.norm_executor()
         except ValueError as e:  # the builder's own limits
-            out[key.replace("_us", "_unsupported")] = str(e)
-            continue
-        ms_norm = time_fn(chain.run, steps, warmup)
-        if chain.failed():
-            raise RuntimeError("executor with norm stages: a wait gave up")
-        out[key] = round(ms_norm * 1e3, 2)
-        del chain
+            chain = None
+            out["norm_chain_unsupported"] = str(e)
+        if chain is not None:
+            ms_norm = time_fn(chain.run, steps, warmup)
+            if chain.failed():
+                raise RuntimeError("executor with norm stages: a wait gave up")
+            out["norm_chain_us"] = round(ms_norm * 1e3, 2)
+            del chain
     cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
     ms = cands[out["path"]] / 1e3
@@ -615,11 +601,8 @@ def main():
     if head["path"] == "executor":
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
         el = head["executor_launch"]
-        if el["kind"] == "stream":
-            kname = f"stream_kernel<{fmt_name}>"
-        else:
-            kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
-                     f"{str(el['pieces']).lower()}>")
+        kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
+                 f"{str(el['pieces']).lower()}>")
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
@@ -706,8 +689,7 @@ def main():
                      "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
                      "executor_shapes": head.get("shapes_us"),
                      # the step with its residual adds and RMSNorms fused into the input stages
-                     "executor_with_norm_stages": head.get("stack_norm_chain_us"),
-                     "stream_executor_with_norm_stages": head.get("norm_chain_us")},
+                     "executor_with_norm_stages": head.get("norm_chain_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),
         "roofline": roofline,

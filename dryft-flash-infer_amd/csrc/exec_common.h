@@ -1,4 +1,4 @@
-// Shared pieces of the decode-step executors (decode_stack.hip, stream_exec.hip): bounded
+// Shared pieces of the decode-step executor (decode_stack.hip): bounded
 // waits on the real-time counter, and the published-word ("wire") protocol by which a
 // projection's output reaches the workgroups of later projections without a grid barrier.
 #pragma once

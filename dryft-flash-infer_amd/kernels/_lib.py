@@ -54,14 +54,6 @@ class NormInput(ctypes.Structure):
                 ("pad", ctypes.c_int)]
 
 
-class StreamLaunch(ctypes.Structure):
-    """``qlx_stream_launch``: grid, LDS bytes, ring lines per compute wave, and the kernel's
-    LDS layout (opaque words)."""
-
-    _fields_ = [("grid", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("ring_lines", ctypes.c_int),
-                ("layout_words", ctypes.c_int), ("layout", ctypes.c_int * 32)]
-
-
 class RopeArgs(ctypes.Structure):
     """``qlx_rope_args``: the fused QKV head-norm + RoPE + cache write."""
 
@@ -121,10 +113,6 @@ SIGNATURES = {
     "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _I, _P,
                                 _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
-    "qlx_stream_build": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _P, _PLL, _P, _PLL,
-                          ctypes.POINTER(StreamLaunch)],
-                         _I),
-    "qlx_stream_run": ([_I, _P, ctypes.POINTER(StreamLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
     "qlx_qkv_norm_rope": ([ctypes.POINTER(RopeArgs), _P], _I),
     "qlx_attention_workspace": ([_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_size_t)], _I),

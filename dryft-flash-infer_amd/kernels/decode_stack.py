@@ -183,52 +183,3 @@ class DecodeStack:
 
     def bytes_moved(self):
         return sum(w.bytes_moved() for w in self._keep[0::3])
-
-
-class StreamStack(DecodeStack):
-    """The same chain on the stream executor (``qlx_stream_build`` / ``qlx_stream_run``): in
-    each workgroup eight compute waves stream every projection's weights into LDS rings with
-    direct-to-LDS loads, running ahead across projections, while four IO waves poll, stage,
-    reduce and publish, so no poll ever waits behind a weight load. Each projection's tiles go
-    whole to workgroups; a tile's output is the fixed-order sum of eight K-interleaved partial
-    sums (deterministic). ``add`` and ``add_normed`` take the same arguments (``kw`` is
-    ignored).
-    """
-
-    def __init__(self, fmt, m):
-        super().__init__(fmt, m)
-
-    def build(self):
-        if not self.calls:
-            raise ValueError("empty chain")
-        device = self._keep[0].weight.device
-        lib = _lib.lib()
-        arr = (_lib.StackCall * len(self.calls))(*self.calls)
-        norms = (_lib.NormInput * len(self.norms))(*self.norms)
-        fmt = _FMTS[self.fmt]
-        desc_bytes, arena_bytes, launch = ctypes.c_longlong(0), ctypes.c_longlong(0), _lib.StreamLaunch()
-        with torch.cuda.device(device):
-            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), norms, None, desc_bytes, None,
-                                            arena_bytes, launch), "qlx_stream_build")
-            self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
-            self.error = torch.zeros(1, dtype=torch.int32, device=device)
-            host = torch.zeros(desc_bytes.value, dtype=torch.uint8)
-            _lib.check(lib.qlx_stream_build(fmt, self.m, arr, len(self.calls), norms,
-                                            ctypes.c_void_p(host.data_ptr()), desc_bytes, _lib.ptr(self.arena),
-                                            arena_bytes, launch), "qlx_stream_build")
-            self.desc = host.to(device)
-        self.launch = launch
-        self.grid, self.lds = launch.grid, launch.lds_bytes
-        self.device = device
-        self.epoch = 0
-        return self
-
-    def run(self, budget_us=BUDGET_US):
-        """Run the whole chain once on the current stream (not capturable: see DecodeStack.run)."""
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("StreamStack.run cannot be captured into a graph: every run needs a new epoch")
-        if self.desc is None:
-            self.build()
-        self.epoch = self.epoch % 0xFFFF + 1
-        _lib.call("qlx_stream_run", _FMTS[self.fmt], _lib.ptr(self.desc), ctypes.byref(self.launch), self.epoch,
-                  _lib.ptr(self.error), int(budget_us), _lib.stream(self.device))

@@ -4,7 +4,7 @@
  * Plain pointers and sizes only. Every pointer argument is device memory (HBM) unless
  * it says otherwise; `stream` is a hipStream_t (NULL = the default stream). No entry
  * point allocates, synchronises or reads device memory on the host, so every call except
- * qlx_stack_run and qlx_stream_run is safe to capture into a hipGraph (a run's `epoch`
+ * qlx_stack_run is safe to capture into a hipGraph (a run's `epoch`
  * argument must differ from the previous run's, and every replay of a captured run would
  * repeat it). Each
  * returns QLX_OK (0) or a negative status; qlx_last_error() then holds a message
@@ -335,16 +335,16 @@ int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int
 int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
                   int* error, long long budget_us, void* stream);
 
-/* ---- decode-step stream executor ---------------------------------------------------- */
+/* ---- residual add + RMSNorm input stages of the decode-step executor ----------------- */
 
-/* Residual add + RMSNorm input stage of a stream-executor projection (the decode step's fused
+/* Residual add + RMSNorm input stage of an executor projection (the decode step's fused
  * residual consumer, engine/kernels/norm.py:125-139 with reference.py:13-28's casts). With norm_w
  * set, projection c's input is y = bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
  * r = bf16(resid + delta) (r = resid when delta is NULL), and calls[c].x must be NULL. resid is
  * bf16 [m][k] in memory the chain does not write, or the resid_out of an earlier stage; delta is
  * NULL or the whole output y of an earlier projection. resid_out (optional) receives r and
  * normed_out (optional) y. For FP8 W8A8 the staged y is quantized per token like any input: the
- * norm -> FP8 activation quantize is fused. A stage takes k a multiple of 512 and m * k <= 6144 (m <= 2). */
+ * norm -> FP8 activation quantize is fused. */
 typedef struct qlx_norm_input {
   const void* resid;
   const void* delta;
@@ -368,38 +368,6 @@ typedef struct qlx_norm_input {
 int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
                            int waves, int groups_per_cu, int pollers, void* desc, qlx_plan* plans, void* arena,
                            long long* arena_bytes, qlx_stack_launch* launch);
-
-/* Launch configuration of a stream-executor chain, filled by qlx_stream_build. */
-typedef struct qlx_stream_launch {
-  int grid;          /* workgroups, one per CU (cooperative launch) */
-  int lds_bytes;     /* LDS per workgroup */
-  int ring_lines;    /* 1 KB weight-ring lines per compute wave */
-  int layout_words;  /* words of `layout` in use */
-  int layout[32];    /* the kernel's LDS layout (opaque) */
-} qlx_stream_launch;
-
-/* The same chain as qlx_stack_build (projections of one format -- W8A16, W4A16 or FP8 W8A8 --
- * on tile-layout weights, m = 1..16, each input in memory or an earlier projection's output
- * or its first k columns; mode BF16 or SWIGLU; kw is ignored), run with the weight stream off
- * the dependency chain: in each workgroup (one per CU) four compute waves stream their share of
- * every projection's weights into private LDS rings with direct-to-LDS loads, running ahead
- * across projections, while four IO waves poll, stage, reduce and publish. Each projection's
- * 16-row tiles go whole to workgroups (balancing every workgroup's running weight bytes); a
- * tile's output is the fixed-order sum of four K-interleaved partials, so runs are
- * deterministic. Writes the descriptor image to host memory `desc` (NULL to size it:
- * *desc_bytes), to be copied to device memory as is; published outputs live in `arena`
- * (*arena_bytes, zeroed once before the first run). Same replacement as qlx_stack_build
- * (engine/kernels/cuda_fp8.py:47-50, 150-169; engine/kernels/cuda_jit.py:218-262). */
-int qlx_stream_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
-                     void* desc, long long* desc_bytes, void* arena, long long* arena_bytes,
-                     qlx_stream_launch* launch);
-
-/* Run a stream-executor chain (device copy of the descriptor image); epoch, error and budget
- * as for qlx_stack_run: a new nonzero low-16-bit epoch per run on one arena, runs sharing an
- * arena must not overlap, and it is not capturable into a graph (replays would repeat the
- * epoch). */
-int qlx_stream_run(int fmt, const void* desc, const qlx_stream_launch* launch, unsigned epoch, int* error,
-                   long long budget_us, void* stream);
 
 /* ---- QKV consumer and decode attention ----------------------------------------------- */
 

@@ -199,32 +199,32 @@ def test_selection_api_mirrors_the_reference():
             timing.time_calls(lambda w: None, ops, **bad)
 
 
-def test_executors_refuse_graph_capture(monkeypatch):
-    """Both executors tag what a run publishes with an epoch passed as a kernel argument, so a
+def test_executor_refuses_graph_capture(monkeypatch):
+    """The executor tags what a run publishes with an epoch passed as a kernel argument, so a
     captured run would replay with the same tag: run() raises under capture (forced from the host:
     no device work happens)."""
     import torch
-    from kernels.decode_stack import DecodeStack, StreamStack
+    from kernels.decode_stack import DecodeStack
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    for cls in (DecodeStack, StreamStack):
-        with pytest.raises(RuntimeError, match="captured"):
-            cls("fp8", 1).run()
+    with pytest.raises(RuntimeError, match="captured"):
+        DecodeStack("fp8", 1).run()
 
 
-def test_stream_norm_stage_contract_on_host():
-    """The stream executor's residual + RMSNorm stages are checked before any device work: x must
-    be NULL exactly for a norm stage, the delta must be the whole output of an earlier projection,
-    the residual may not be memory the chain writes, and m * k must fit one staging pass."""
+def test_norm_stage_contract_on_host():
+    """The executor's residual + RMSNorm stages are checked before any device work: x must be
+    NULL exactly for a norm stage, the delta must be the whole output of an earlier projection,
+    the residual may not be memory the chain writes, m * k must fit one staging pass, and the
+    workgroups may have no poller waves."""
     from kernels import _lib
     import ctypes
     lib = _lib.lib()
-    out = (ctypes.c_longlong(0), ctypes.c_longlong(0), _lib.StreamLaunch())
+    out = (ctypes.c_longlong(0), _lib.StackLaunch())
 
-    def build(m, calls, norms):
+    def build(m, calls, norms, waves=8, pollers=0):
         arr = (_lib.StackCall * len(calls))(*calls)
         nrm = (_lib.NormInput * len(norms))(*norms)
-        return lib.qlx_stream_build(_lib.FMT_FP8, m, arr, len(calls), nrm, None, ctypes.byref(out[0]), None,
-                                    ctypes.byref(out[1]), ctypes.byref(out[2]))
+        return lib.qlx_stack_build_normed(_lib.FMT_FP8, m, arr, len(calls), nrm, waves, 1, pollers, None, None, None,
+                                          ctypes.byref(out[0]), ctypes.byref(out[1]))
 
     W, S, R, NW = 1 << 30, 1 << 31, 1 << 32, 1 << 33
     first = _lib.StackCall(W, S, 1 << 34, 1 << 35, 2560, 2560, _lib.MODE_BF16, 0)  # y = 1 << 35, 2560 wide
@@ -240,10 +240,11 @@ def test_stream_norm_stage_contract_on_host():
     # a residual the chain writes
     bad_resid = _lib.NormInput(1 << 35, None, NW, None, None, 1e-6, 0)
     assert build(1, [first, normed], [plain, bad_resid]) == _lib.QLX_EINVAL and "residual" in _lib.last_error()
-    # m * k beyond one staging pass, and k not a multiple of 512
-    assert build(3, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
-    odd = _lib.StackCall(W, S, None, 1 << 36, 256, 2304, _lib.MODE_BF16, 0)
-    assert build(1, [odd], [_lib.NormInput(R, None, NW, None, None, 1e-6, 0)]) == _lib.QLX_EINVAL
+    # m * k beyond one staging pass (3 chunks of 8 per thread of 8 waves: m <= 4 at k = 2560)
+    assert build(5, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
+    # poller waves
+    assert build(1, [first, normed], [plain, good], waves=4, pollers=2) == _lib.QLX_EINVAL
+    assert "poller" in _lib.last_error()
 
 
 def test_qkv_consumer_and_attention_contract_on_host():
