@@ -35,8 +35,8 @@ LAYERS = 36
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
-#: Executor shapes timed per stack: 8 compute waves, no poller waves.
-EXECUTOR_SHAPES = ((8, 0),)
+#: Waves per executor workgroup.
+EXECUTOR_WAVES = 8
 
 
 def log(*a):
@@ -101,10 +101,10 @@ class Stack:
             else:  # down, lm_head
                 q = h = self.linear(h if name == "lm_head" else q, packed)
 
-    def executor(self, waves=8, lanes=1, pollers=0):
+    def executor(self, waves=EXECUTOR_WAVES, lanes=1):
         """The same chain as one decode-step executor launch (outputs preallocated)."""
         from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes, pollers=pollers)
+        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes)
         self.outs = []
         h = self.x[2560]
         q = None
@@ -320,23 +320,18 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True):
     del g
     out = {"graph_us": ms_graph * 1e3}
     if m <= 16:
-        # The executor in each workgroup shape timed (compute waves, poller waves).
-        for waves, pollers in EXECUTOR_SHAPES:
-            key = f"{waves}c{pollers}p"
-            try:
-                chain = stack.executor(waves=waves, pollers=pollers)
-            except ValueError as e:  # the builder's own limits (LDS, shapes): no such launch here
-                out.setdefault("shapes_unsupported", {})[key] = str(e)
-                continue
+        # the same chain as one executor launch
+        try:
+            chain = stack.executor()
+        except ValueError as e:  # the builder's own limits (LDS, shapes): no such launch here
+            out["executor_unsupported"] = str(e)
+        else:
             ms_exec = time_fn(chain.run, steps, warmup)
             if chain.failed():
-                raise RuntimeError(f"decode executor ({waves}, {pollers}): a wait gave up")
-            out.setdefault("shapes_us", {})[key] = round(ms_exec * 1e3, 2)
-            if ms_exec * 1e3 < out.get("executor_us", 1e30):
-                out["executor_us"] = ms_exec * 1e3
-                out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": waves,
-                                          "pollers": pollers, "desc_lds": chain.launch.desc_lds >= 0,
-                                          "pieces": chain.launch.pieces != 0}
+                raise RuntimeError("decode executor: a wait gave up")
+            out["executor_us"] = ms_exec * 1e3
+            out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": chain.waves,
+                                      "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
             del chain
     if m <= 4:
         # the full decode step's linear path with its residual adds and RMSNorms fused into the
@@ -594,15 +589,14 @@ def main():
 
     stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
     log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
-        f"executor {head.get('executor_us', float('nan')):.1f} {head.get('shapes_us')}), "
+        f"executor {head.get('executor_us', float('nan')):.1f}), "
         f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
 
     fmt_name = {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload]
     if head["path"] == "executor":
         # The whole step is one launch of the executor: its algorithmic bytes over its time.
         el = head["executor_launch"]
-        kname = (f"stack_kernel<{fmt_name}, {el['waves']}, {el['pollers']}, {str(el['desc_lds']).lower()}, "
-                 f"{str(el['pieces']).lower()}>")
+        kname = f"stack_kernel<{fmt_name}, {el['waves']}, {str(el['desc_lds']).lower()}, {str(el['pieces']).lower()}>"
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
@@ -687,7 +681,6 @@ def main():
         },
         "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
                      "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
-                     "executor_shapes": head.get("shapes_us"),
                      # the step with its residual adds and RMSNorms fused into the input stages
                      "executor_with_norm_stages": head.get("norm_chain_us")},
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),

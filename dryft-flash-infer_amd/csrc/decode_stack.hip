@@ -205,97 +205,14 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
     if (p < it.my) load_chunk<F>(buf[p], a, it.wrow, step0 + it.kwi + p * a.kw, lane);
 }
 
-// The two roles of an executor workgroup: WAVES compute waves (threads 0 .. 64 WAVES - 1)
-// stream weights and run the MFMAs and the epilogue; NP poller waves after them only read
-// published activations and stage them. A wave's memory operations complete in issue order,
-// so a compute wave's poll would wait for every weight load it has in flight (the next
-// item's prefetch: up to 12 KB per wave, 96 KB per CU); a poller has none. Both teams meet
-// at the workgroup's barriers, so they execute the same number of them per item.
+// The team of an executor workgroup's waves (threads 0 .. 64 WAVES - 1): they stream weights,
+// stage activations, run the MFMAs and the epilogue.
 template <int WAVES>
 struct ComputeTeam {
   __device__ int tid() const { return threadIdx.x; }
   __device__ int size() const { return WAVES * 64; }
   __device__ void sync() const { __syncthreads(); }
 };
-template <int WAVES, int NP>
-struct PollTeam {
-  __device__ int tid() const { return threadIdx.x - WAVES * 64; }
-  __device__ int size() const { return NP * 64; }
-  __device__ void sync() const { __syncthreads(); }
-};
-
-// Chunks of 8 values each poller thread keeps in registers between the two halves of the FP8
-// prologue (one pass over x when m * k <= 8 * 64 NP * kPollKeep: k <= 10240 at m = 1, NP = 4).
-constexpr int kPollKeep = 5;
-
-// FP8 prologue of the poller team: the per-token maxima over whole rows (atomicMax into the
-// zeroed `amax`), one workgroup barrier (the compute waves' matching one is in exec_main),
-// then the token scales and the e4m3 codes of the item's slice. Chunks kept from the first
-// pass are quantized from registers; the rest of the slice is read again (already published).
-template <int WAVES, int NP, class XS>
-__device__ __forceinline__ void poll_stage_fp8(const GemmArgs& a, const XS& xs, char* lds, int step0, int nst,
-                                               uint32_t* amax) {
-  constexpr int U = kPollKeep;
-  const PollTeam<WAVES, NP> team;
-  const int tid = team.tid(), nthr = team.size();
-  const int cpr = a.k >> 3, total = a.m * cpr;
-  uint4 kept[U];
-  for (int q0 = tid; q0 < total; q0 += U * nthr) {
-    typename XS::Raw r[U];
-    auto chunk = [&](int u, int& mm, int& kabs) {
-      const int q = q0 + u * nthr;
-      mm = q / cpr;
-      kabs = (q - mm * cpr) * 8;
-      return q < total;
-    };
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int mm, kabs;
-      if (chunk(u, mm, kabs)) xs.fetch(a, mm, kabs, r[u]);
-    }
-    settle_batch<XS, U>(a, xs, r, chunk);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int q = q0 + u * nthr;
-      if (q < total) {
-        const uint4 v = xs.value(r[u]);
-        if (q0 == tid) kept[u] = v;
-        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-        float mx = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf2f(d[j] & 0xffffu)), fabsf(bf2f(d[j] >> 16))));
-        atomicMax(&amax[q / cpr], __float_as_uint(mx));
-      }
-    }
-  }
-  __syncthreads();
-  float* sx = reinterpret_cast<float*>(lds + a.off_sx);
-  auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
-  for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
-  const int c0 = step0 * 16, c1 = c0 + nst * 16;  // the slice's 8-value chunks within a row
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int q = tid + u * nthr;
-    if (q < total) {
-      const int mm = q / cpr, kc = q - mm * cpr;
-      if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, kept[u], token_scale(mm));
-    }
-  }
-  const int cps = nst * 16, kept_end = U * nthr;
-  for (int sidx = tid; sidx < a.m * cps; sidx += nthr) {
-    const int mm = sidx / cps, kc = c0 + (sidx - mm * cps);
-    if (mm * cpr + kc < kept_end) continue;
-    typename XS::Raw r[1];
-    auto chunk = [&](int, int& m2, int& kabs) {
-      m2 = mm;
-      kabs = kc * 8;
-      return true;
-    };
-    xs.fetch(a, mm, kc * 8, r[0]);
-    settle_batch<XS, 1>(a, xs, r, chunk);
-    store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, xs.value(r[0]), token_scale(mm));
-  }
-}
 
 // The producer's published per-token maxima an FP8 item combines (StackDesc.xmax), or none.
 struct MaxIn {
@@ -580,9 +497,9 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
 
 // Stage what the item needs in LDS and stream its weight steps through the MFMAs. With
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
-// projection, same steps -- is still in place. With poller waves (NP > 0) they stage the
-// activation and leave after the staging barriers; `amax` is their zeroed FP8 scratch.
-template <class F, int WAVES, int NP, bool PIECES, class XS>
+// projection, same steps -- is still in place. `amax` is the zeroed FP8 scratch of the token
+// maxima (and, behind its 64 bytes, a norm stage's sums).
+template <class F, int WAVES, bool PIECES, class XS>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
                                           uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS], f32x4 (&acc)[1][1],
                                           uint32_t* amax, const MaxIn& mi = {}, const StackDesc* nd = nullptr,
@@ -591,69 +508,56 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
   const int step0 = it.step0, nst = it.nst, kwi = it.kwi, my = it.my;
-  const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
   if (!reuse) {
-    if constexpr (NP == 0) {
-      if (nd) {  // a residual add + RMSNorm stage (no poller waves: checked on the host)
-        double* css = reinterpret_cast<double*>(reinterpret_cast<char*>(amax) + 64);
-        const bool owner = it.tg == 0 && it.s == 0;
-        if (a.m * (a.k >> 3) <= (int)blockDim.x)  // one chunk per thread (every M = 1 stage)
-          stage_norm<F, 1>(*nd, lds, step0, nst, amax, css, owner, *nw);
-        else
-          stage_norm<F, kNormU>(*nd, lds, step0, nst, amax, css, owner, *nw);
-      } else if constexpr (FP8) {
-        bool done = false;
-        if constexpr (XS::POLLS) {
-          if (mi.p) {
-            stage_fp8_maxima(a, xs, mi, lds, step0, nst, amax);
-            done = true;
-          }
-        }
-        if (!done) stage_fp8_act(a, xs, lds, step0, nst, BlockTeam{}, amax);  // amax: zeroed, as the pollers' is
-      } else
-        stage_bf16<F>(a, xs, lds, step0, nst);
-    } else if (poller) {
-      if constexpr (FP8)
-        poll_stage_fp8<WAVES, NP>(a, xs, lds, step0, nst, amax);
+    if (nd) {  // a residual add + RMSNorm stage
+      double* css = reinterpret_cast<double*>(reinterpret_cast<char*>(amax) + 64);
+      const bool owner = it.tg == 0 && it.s == 0;
+      if (a.m * (a.k >> 3) <= (int)blockDim.x)  // one chunk per thread (every M = 1 stage)
+        stage_norm<F, 1>(*nd, lds, step0, nst, amax, css, owner, *nw);
       else
-        stage_bf16<F>(a, xs, lds, step0, nst, PollTeam<WAVES, NP>{});
+        stage_norm<F, kNormU>(*nd, lds, step0, nst, amax, css, owner, *nw);
     } else if constexpr (FP8) {
-      __syncthreads();  // the pollers' barrier between the row maxima and the codes
-    }
-  }
-  if (!poller) {
-    if constexpr (F::NSC == 0) {
-      // Read on every path, so the register is not left pending for the next item's prefetch.
-      const float scv = bf2f(it.scb);
-      if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
-    } else if (it.scpre) {
-      const int rows = 16 * a.rt, lg = __builtin_ctz(rows), total = nst * rows;
-      float* sc = reinterpret_cast<float*>(lds + a.off_sc);
-#pragma unroll
-      for (int u = 0; u < kScaleRegs; ++u) {
-        const int q = threadIdx.x + u * WAVES * 64;
-        const int rl = q & (rows - 1), st = q >> lg;
-        if (q < total) {
-          sc[(2 * st) * a.sc_stride + rl] = F::scale_of(it.scw[u] & 0xffffu);
-          sc[(2 * st + 1) * a.sc_stride + rl] = F::scale_of(it.scw[u] >> 16);
+      bool done = false;
+      if constexpr (XS::POLLS) {
+        if (mi.p) {
+          stage_fp8_maxima(a, xs, mi, lds, step0, nst, amax);
+          done = true;
         }
       }
-    } else {
-      stage_scales<F>(a, lds, it.tg, step0, nst, ComputeTeam<WAVES>{});
+      if (!done) stage_fp8_act(a, xs, lds, step0, nst, BlockTeam{}, amax);
+    } else
+      stage_bf16<F>(a, xs, lds, step0, nst);
+  }
+  if constexpr (F::NSC == 0) {
+    // Read on every path, so the register is not left pending for the next item's prefetch.
+    const float scv = bf2f(it.scb);
+    if (threadIdx.x < 16 * a.rt) reinterpret_cast<float*>(lds + a.off_sc)[threadIdx.x] = scv;
+  } else if (it.scpre) {
+    const int rows = 16 * a.rt, lg = __builtin_ctz(rows), total = nst * rows;
+    float* sc = reinterpret_cast<float*>(lds + a.off_sc);
+#pragma unroll
+    for (int u = 0; u < kScaleRegs; ++u) {
+      const int q = threadIdx.x + u * WAVES * 64;
+      const int rl = q & (rows - 1), st = q >> lg;
+      if (q < total) {
+        sc[(2 * st) * a.sc_stride + rl] = F::scale_of(it.scw[u] & 0xffffu);
+        sc[(2 * st + 1) * a.sc_stride + rl] = F::scale_of(it.scw[u] >> 16);
+      }
     }
+  } else {
+    stage_scales<F>(a, lds, it.tg, step0, nst, ComputeTeam<WAVES>{});
   }
   __syncthreads();
   // The token maxima are read (into the token scales) before that barrier: clear them for
   // the next staging, which the end-of-item barrier orders after this.
-  if constexpr (FP8 && NP == 0)
+  if constexpr (FP8)
     if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   if constexpr (needs_bias_totals<F>()) {
     if (!reuse) {
-      if (!poller) stage_bias<F, WAVES>(a, lds, nst);
+      stage_bias<F, WAVES>(a, lds, nst);
       __syncthreads();
     }
   }
-  if (poller) return;
   acc[0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
   int xoff[1], mrow[1];
   mrow[0] = min(lane & 15, a.m - 1);
@@ -690,7 +594,7 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
 // Combine the item's waves; then, per output pair: write it (np == 1), publish this piece's
 // partial sums (piece > 0), or add the other pieces' partials in piece order and write
 // (piece 0). Outputs go to y and, when a later projection reads them, to ywire. With MAXIMA
-// (FP8 chains without poller waves) and d.ymax, the writer of each tile's outputs also
+// (FP8 chains) and d.ymax, the writer of each tile's outputs also
 // publishes each token's largest magnitude among them.
 template <class F, bool SW, bool PIECES, bool MAXIMA = false, class Team = BlockTeam>
 __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const ExecItem& it,
@@ -848,30 +752,15 @@ __device__ __forceinline__ NextItem find_next(const StackDesc* calls, int ncalls
   return n;
 }
 
-// A poller wave's copy of a work item: the geometry staging needs, no loads.
-__device__ __forceinline__ void poll_item(const StackDesc& d, int p, int g, ExecItem& it) {
-  int step0, nst, piece, np;
-  share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
-  it.tg = g;
-  it.s = piece;
-  it.np = np;
-  it.step0 = step0;
-  it.nst = nst;
-  it.wt = it.kwi = it.my = it.last = it.wrow = 0;
-  it.scb = 0u;
-  it.scpre = false;
-}
-
-template <class F, int WAVES, int NP, bool DLDS, bool PIECES>
-__global__ void __launch_bounds__((WAVES + NP) * 64)
+template <class F, int WAVES, bool DLDS, bool PIECES>
+__global__ void __launch_bounds__(WAVES * 64)
 stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
              int desc_off, int lanes, int amax_off) {
   extern __shared__ __align__(16) char lds[];
   const int per_lane = gridDim.x / lanes;
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
-  const bool poller = NP > 0 && threadIdx.x >= WAVES * 64;
-  constexpr bool MAXIMA = std::is_same<F, FmtFP8>::value && NP == 0;  // published row-block maxima
+  constexpr bool MAXIMA = std::is_same<F, FmtFP8>::value;  // published row-block maxima
   uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 staging: per-token maxima
   if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
   const StackDesc* calls = gcalls;
@@ -889,31 +778,24 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
   int nc = -1, ng = 0;
   int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-  if (have) {
-    if (poller) poll_item(calls[nc], p, ng, nxt);
-    else prefetch_work<F, WAVES, PIECES>(calls[nc], p, ng, nxt, buf);
-  }
+  if (have) prefetch_work<F, WAVES, PIECES>(calls[nc], p, ng, nxt, buf);
   while (have) {
     const int c = nc;
     const StackDesc& d = calls[c];
     cur = nxt;
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire && !d.nw)
-      exec_main<F, WAVES, NP, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax,
-                                      MaxIn{NP == 0 ? d.xmax : nullptr, d.xmax_pitch, d.xmax_n, d.xmax_rt});
+      exec_main<F, WAVES, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax,
+                                  MaxIn{d.xmax, d.xmax_pitch, d.xmax_n, d.xmax_rt});
     else  // x in memory, or a norm stage (one call site: the kernel's code stays as small)
-      exec_main<F, WAVES, NP, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax, MaxIn{}, d.nw ? &d : nullptr,
-                                      &w);
+      exec_main<F, WAVES, PIECES>(d.a, XPlain{}, lds, cur, reuse, buf, acc, amax, MaxIn{}, d.nw ? &d : nullptr, &w);
     staged_c = c;
     staged_step0 = cur.step0;
     staged_nst = cur.nst;
     // Outputs first: later projections wait for them. Anything before them -- finding the
     // next item, issuing its loads (the stores would queue behind them) -- delays the chain
     // (measured: 60-160 us per decode step).
-    if (poller) {
-      __syncthreads();  // the barrier of acc_to_lds in exec_finish
-      if (threadIdx.x - WAVES * 64 < 16) amax[threadIdx.x - WAVES * 64] = 0u;  // for the next staging
-    } else if (d.sw) {
+    if (d.sw) {
       exec_finish<F, true, PIECES, MAXIMA>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
     } else {
       exec_finish<F, false, PIECES, MAXIMA>(d, lds, cur, acc, w, ComputeTeam<WAVES>{}, false);
@@ -922,45 +804,33 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     have = after.have;
     nc = after.c;
     ng = after.g;
-    if (have) {
-      if (poller) poll_item(calls[nc], p, ng, nxt);
-      else exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
-    }
+    if (have) exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     __syncthreads();  // LDS is reused by the next item
   }
 }
 
-template <class F, int WAVES, int NP>
+template <class F, int WAVES>
 const void* stack_fn2(bool dlds, bool pieces) {
   if (pieces)
-    return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true, true>)
-                : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false, true>);
-  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, true, false>)
-              : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, NP, false, false>);
-}
-
-// Compute and poller waves the executor is built for: 8 compute waves alone, or 4 with 0, 2 or
-// 4 pollers (at most two waves per SIMD: beside 8 compute waves, pollers would leave each
-// wave 168 registers and the compute path spills).
-bool stack_shape_ok(int waves, int pollers) {
-  return (waves == 8 && pollers == 0) || (waves == 4 && (pollers == 0 || pollers == 2 || pollers == 4));
+    return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, true, true>)
+                : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, false, true>);
+  return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, true, false>)
+              : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, false, false>);
 }
 
 template <class F>
-const void* stack_fn(int waves, int pollers, bool dlds, bool pieces) {
-  if (waves == 8) return stack_fn2<F, 8, 0>(dlds, pieces);
-  if (pollers == 2) return stack_fn2<F, 4, 2>(dlds, pieces);
-  if (pollers == 4) return stack_fn2<F, 4, 4>(dlds, pieces);
-  return stack_fn2<F, 4, 0>(dlds, pieces);
+const void* stack_fn(int waves, bool dlds, bool pieces) {
+  return waves == 8 ? stack_fn2<F, 8>(dlds, pieces) : stack_fn2<F, 4>(dlds, pieces);
 }
 
-// The kernel for a launch: `pieces` when some row block of the chain is cut into K pieces.
-const void* stack_fn_for(int fmt, int waves, int pollers, bool dlds, bool pieces) {
-  if (!stack_shape_ok(waves, pollers)) return nullptr;
+// The kernel for a launch of `waves` (4 or 8) waves per workgroup: `pieces` when some row block
+// of the chain is cut into K pieces.
+const void* stack_fn_for(int fmt, int waves, bool dlds, bool pieces) {
+  if (waves != 4 && waves != 8) return nullptr;
   switch (fmt) {
-    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, pollers, dlds, pieces);
-    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, pollers, dlds, pieces);
-    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, pollers, dlds, pieces);
+    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, dlds, pieces);
+    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, dlds, pieces);
+    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, dlds, pieces);
     default: return nullptr;
   }
 }
@@ -1088,26 +958,20 @@ extern "C" {
 int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
-                    int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
-                    qlx_stack_launch* launch) {
-  return qlx_stack_build_normed(fmt, m, calls, ncalls, nullptr, waves, groups_per_cu, pollers, desc, plans, arena,
+                    void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch) {
+  return qlx_stack_build_normed(fmt, m, calls, ncalls, nullptr, waves, groups_per_cu, desc, plans, arena,
                                 arena_bytes, launch);
 }
 
 int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
-                           int waves, int groups_per_cu, int pollers, void* desc, qlx_plan* plans, void* arena,
+                           int waves, int groups_per_cu, void* desc, qlx_plan* plans, void* arena,
                            long long* arena_bytes, qlx_stack_launch* launch) {
-  QLX_REQUIRE(stack_fn_for(fmt, 8, 0, false, false) != nullptr,
+  QLX_REQUIRE(stack_fn_for(fmt, 8, false, false) != nullptr,
               "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
   QLX_REQUIRE(m >= 1 && m <= 16, "the decode executor serves m = 1..16 (got %d)", m);
   QLX_REQUIRE(calls != nullptr && ncalls >= 1, "no projections");
   QLX_REQUIRE(groups_per_cu >= 1 && groups_per_cu <= 4, "groups_per_cu must be 1..4");
-  QLX_REQUIRE(pollers == -1 || pollers == 0 || pollers == 2 || pollers == 4, "pollers must be -1, 0, 2 or 4 (got %d)",
-              pollers);
-  if (pollers < 0) pollers = waves == 4 ? 4 : 0;
-  QLX_REQUIRE(stack_shape_ok(waves, pollers), "poller waves run beside 4 compute waves (waves=%d, pollers=%d)", waves,
-              pollers);
   const FmtInfo fi = stack_info(fmt);
   auto normed = [&](int c) { return norms != nullptr && norms[c].norm_w != nullptr; };
   // Shapes, and which earlier projection (if any) produces each activation. Outputs may not
@@ -1126,7 +990,6 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
                 "projection %d: NULL pointer (x must be NULL exactly when the input is a norm stage)", c);
     if (normed(c)) {
       QLX_REQUIRE(norms[c].resid != nullptr, "projection %d: a norm stage needs its residual", c);
-      QLX_REQUIRE(pollers == 0, "projection %d: norm stages run on workgroups without poller waves", c);
       QLX_REQUIRE(m * (q.k / 8) <= kNormU * waves * 64,
                   "projection %d: a norm stage takes m * k <= %d (one pass; m=%d, k=%d)", c, kNormU * waves * 64 * 8,
                   m, q.k);
@@ -1210,7 +1073,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
       // it was awaited): the planner charges those bytes 4x a weight byte (measured on the
       // Qwen3-4B FP8 chain, us per step at M = 8 / 16 by the factor: none 2914 / 3932, 1x 2641 /
       // 3930, 2x 2642 / 3475, 3x 2462 / 3490, 4x 2412 / 3488, 6x 2422 / 3483).
-      const bool slice_staged = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM && src[c] >= 0 && !normed(c);
+      const bool slice_staged = fmt == QLX_FMT_FP8 && m > kMaximaMinM && src[c] >= 0 && !normed(c);
       const double stage_bytes = slice_staged ? 4.0 * 4.0 * fi.kstep * m : 0.0;
       QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c], stage_bytes),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
@@ -1224,22 +1087,22 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     lds = desc_lds >= 0 ? (int)(items_end + desc_bytes) : items_end;
     pieces = false;
     for (int c = 0; c < ncalls; ++c) pieces |= sp[c].max_np > 1;
-    const void* fn = stack_fn_for(fmt, waves, pollers, desc_lds >= 0, pieces);
+    const void* fn = stack_fn_for(fmt, waves, desc_lds >= 0, pieces);
     if (lds > 64 * 1024) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       if (e != hipSuccess) return hip_status(e, "stack_build");
     }
     int occ = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (waves + pollers) * 64, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * 64, lds);
     if (e != hipSuccess) return hip_status(e, "stack_build");
     QLX_REQUIRE(occ >= 1, "the executor does not fit a CU with %d bytes of LDS", lds);
     if (occ >= lanes) break;
     lanes = occ;
   }
-  // FP8 chains of more than kMaximaMinM tokens without poller waves: a published output also
+  // FP8 chains of more than kMaximaMinM tokens: a published output also
   // carries its per-token maxima per weight tile, and a projection reading it combines those of
   // its k columns instead of reading whole rows for its token scales.
-  const bool maxima = fmt == QLX_FMT_FP8 && pollers == 0 && m > kMaximaMinM;
+  const bool maxima = fmt == QLX_FMT_FP8 && m > kMaximaMinM;
   auto tile_cols = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? 8 : 16; };  // outputs per tile
   auto max_pitch = [&](int c) {
     GemmArgs a = {};
@@ -1340,7 +1203,6 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     launch->lds_bytes = lds;
     launch->waves = waves;
     launch->desc_lds = desc_lds;
-    launch->pollers = pollers;
     launch->amax_off = amax_off;
     launch->pieces = pieces ? 1 : 0;
   }
@@ -1349,10 +1211,10 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
 
 int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
                   int* error, long long budget_us, void* stream) {
-  QLX_REQUIRE(launch != nullptr && stack_shape_ok(launch->waves, launch->pollers) && launch->grid >= 1,
+  QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1,
               "bad executor launch configuration");
   QLX_REQUIRE(launch->pieces == 0 || launch->pieces == 1, "launch.pieces must be 0 or 1 (got %d)", launch->pieces);
-  const void* fn = stack_fn_for(fmt, launch->waves, launch->pollers, launch->desc_lds >= 0, launch->pieces != 0);
+  const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0, launch->pieces != 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(desc && error && ncalls >= 1, "bad executor arguments");
   QLX_REQUIRE(launch->desc_lds < 0 || launch->desc_lds + (long long)ncalls * (long long)sizeof(StackDesc) <=
@@ -1368,7 +1230,7 @@ int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch*
   QLX_REQUIRE(lanes >= 1 && launch->grid % lanes == 0, "bad executor lanes");
   void* args[] = {(void*)&desc,     (void*)&ncalls, (void*)&epoch,   (void*)&error,
                   (void*)&ticks,    (void*)&desc_off, (void*)&lanes, (void*)&amax_off};
-  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3((launch->waves + launch->pollers) * 64), args,
+  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3(launch->waves * 64), args,
                                             (unsigned)launch->lds_bytes, (hipStream_t)stream);
   return hip_status(e, "stack_run");
 }

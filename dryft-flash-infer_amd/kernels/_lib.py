@@ -41,11 +41,10 @@ class StackCall(ctypes.Structure):
 
 
 class StackLaunch(ctypes.Structure):
-    """``qlx_stack_launch``: grid, LDS bytes, compute waves, descriptor LDS offset, lanes, poller
-    waves, the LDS offset of the FP8 row maxima, and whether row blocks are cut into K pieces."""
+    """``qlx_stack_launch``: grid, LDS bytes, waves, descriptor LDS offset, lanes, the LDS offset
+    of the FP8 row maxima, and whether row blocks are cut into K pieces."""
 
-    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "pollers", "amax_off",
-                                            "pieces")]
+    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "amax_off", "pieces")]
 
 
 class NormInput(ctypes.Structure):
@@ -108,9 +107,9 @@ SIGNATURES = {
     "qlx_add_norm_quant_fp8": ([_P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "qlx_swiglu": ([_P, _P, _I, _P, _I, _I, _P], _I),
     "qlx_stack_desc_size": ([], _I),
-    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _I, _P, _PLAN, _P, _PLL,
+    "qlx_stack_build": ([_I, _I, ctypes.POINTER(StackCall), _I, _I, _I, _P, _PLAN, _P, _PLL,
                          ctypes.POINTER(StackLaunch)], _I),
-    "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _I, _P,
+    "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _P,
                                 _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),

@@ -35,21 +35,15 @@ BUDGET_US = 2_000_000
 
 
 class DecodeStack:
-    """An ordered chain of projections of one format, for m = 1..16 tokens.
+    """An ordered chain of projections of one format, for m = 1..16 tokens, run by workgroups
+    of ``waves`` (4 or 8) waves, ``groups_per_cu`` of them per CU."""
 
-    Each workgroup has ``waves`` compute waves and ``pollers`` (0, 2 or 4) waves that only
-    read the activations earlier projections publish: a compute wave's read would wait for the
-    weight loads it keeps in flight."""
-
-    def __init__(self, fmt, m, waves=8, groups_per_cu=1, pollers=0):
+    def __init__(self, fmt, m, waves=8, groups_per_cu=1):
         if fmt not in _FMTS:
             raise ValueError(f"the decode executor serves {sorted(_FMTS)}, not {fmt!r}")
         if not 1 <= m <= 16:
             raise ValueError(f"the decode executor serves m = 1..16 (got {m})")
-        if pollers not in (0, 2, 4):
-            raise ValueError(f"pollers must be 0, 2 or 4 (got {pollers})")
         self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
-        self.pollers = pollers
         self.calls, self._keep = [], []
         self.norms = []
         self.desc = None
@@ -130,7 +124,7 @@ class DecodeStack:
         fmt = _FMTS[self.fmt]
         arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
-            opts = (self.waves, self.groups_per_cu, self.pollers)
+            opts = (self.waves, self.groups_per_cu)
             _lib.check(lib.qlx_stack_build_normed(fmt, self.m, arr, len(self.calls), norms, *opts, None, None, None,
                                                   arena_bytes, launch), "qlx_stack_build_normed")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)

@@ -297,22 +297,18 @@ int qlx_stack_desc_size(void);
 typedef struct qlx_stack_launch {
   int grid;        /* workgroups (all resident: cooperative launch) */
   int lds_bytes;   /* dynamic LDS per workgroup */
-  int waves;       /* compute waves per workgroup */
+  int waves;       /* waves per workgroup */
   int desc_lds;    /* byte offset of the descriptors' LDS copy, or -1 (read from memory) */
   int lanes;       /* workgroup sets: lane l runs projections l, l + lanes, ... */
-  int pollers;     /* waves per workgroup that only read and stage published activations */
   int amax_off;    /* LDS byte offset of the per-token FP8 maxima (64 bytes) */
   int pieces;      /* 1 when a row block of the chain is cut into K pieces (the kernel with their
                       reduction, whose registers otherwise go to deeper weight prefetch), else 0 */
 } qlx_stack_launch;
 
 /* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
- * for the executor: workgroups of `waves` (4 or 8) compute waves, `groups_per_cu` lanes of one
+ * for the executor: workgroups of `waves` (4 or 8) waves, `groups_per_cu` lanes of one
  * workgroup per CU (1..4; fewer if registers or LDS do not allow), lane l running projections
- * l, l + lanes, ... concurrently with the other lanes. `pollers` (0, 2 or 4; -1 lets the
- * library choose) adds that many waves per workgroup that only read the activations earlier
- * projections publish and stage them, so those reads never wait behind weight loads (0: the
- * compute waves read them). Writes the descriptors to host memory `desc`
+ * l, l + lanes, ... concurrently with the other lanes. Writes the descriptors to host memory `desc`
  * (ncalls * qlx_stack_desc_size() bytes; NULL to only size) and, if `plans` is not NULL, each
  * projection's plan (waves, kw; splits = the most K pieces of one row block). The chain keeps
  * published outputs and partial sums in `arena` (*arena_bytes of device memory, zeroed once
@@ -322,8 +318,7 @@ typedef struct qlx_stack_launch {
  * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
  * engine/kernels/cuda_jit.py:218-262): here the whole chain is one cooperative launch. */
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
-                    int pollers, void* desc, qlx_plan* plans, void* arena, long long* arena_bytes,
-                    qlx_stack_launch* launch);
+                    void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch);
 
 /* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors and `launch` its
  * launch configuration. The low 16 bits of `epoch` tag the values the run publishes: they must
@@ -355,18 +350,17 @@ typedef struct qlx_norm_input {
   int pad;
 } qlx_norm_input;
 
-/* qlx_stack_build with residual add + RMSNorm input stages (f1): where norms[c].norm_w is not
+/* qlx_stack_build with residual add + RMSNorm input stages: where norms[c].norm_w is not
  * NULL, projection c's input is bf16(bf16(r * rsqrt(mean(r^2) + eps)) * norm_w) with
  * r = bf16(resid + delta) (r = resid without delta), computed inside the launch by every
  * workgroup with work in the projection; calls[c].x is NULL exactly then. `resid` is memory the
  * chain does not write or an earlier stage's resid_out; `delta` is the whole output of an
  * earlier projection; resid_out / normed_out (optional) receive r and the input (FP8 W8A8:
- * quantized per token over the normed row). A norm stage needs no poller waves and one pass
- * over its rows: m * k <= 3 * 64 * waves * 8. norms may be NULL (= qlx_stack_build). Replaces
+ * quantized per token over the normed row). A norm stage makes one pass over its rows: m * k <= 3 * 64 * waves * 8. norms may be NULL (= qlx_stack_build). Replaces
  * the reference's plane consumers and residual + RMSNorm kernels between projections
  * (engine/kernels/norm.py:53-80, 125-154; engine/kernels/cuda_small.py:43-87). */
 int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
-                           int waves, int groups_per_cu, int pollers, void* desc, qlx_plan* plans, void* arena,
+                           int waves, int groups_per_cu, void* desc, qlx_plan* plans, void* arena,
                            long long* arena_bytes, qlx_stack_launch* launch);
 
 /* ---- QKV consumer and decode attention ----------------------------------------------- */

@@ -135,9 +135,9 @@ def test_decode_stack_contract_on_host():
     assert lib.qlx_stack_desc_size() >= 128
     out = [ctypes.c_longlong(0), ctypes.byref(_lib.StackLaunch())]
 
-    def build(fmt, m, calls, gpc=1, waves=8, pollers=0):
+    def build(fmt, m, calls, gpc=1, waves=8):
         arr = (_lib.StackCall * max(len(calls), 1))(*calls)
-        return lib.qlx_stack_build(fmt, m, arr, len(calls), waves, gpc, pollers, None, None, None, *out)
+        return lib.qlx_stack_build(fmt, m, arr, len(calls), waves, gpc, None, None, None, *out)
 
     ok = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 0)
     assert build(_lib.FMT_REF8, 1, [ok]) == _lib.QLX_EINVAL
@@ -145,10 +145,7 @@ def test_decode_stack_contract_on_host():
     assert build(_lib.FMT_W4A16, 1, []) == _lib.QLX_EINVAL
     assert build(_lib.FMT_FP8, 1, [ok], gpc=5) == _lib.QLX_EINVAL
     assert build(_lib.FMT_FP8, 1, [ok], waves=6) == _lib.QLX_EINVAL
-    # poller waves: 0, 2 or 4, and only beside 4 compute waves
-    assert build(_lib.FMT_FP8, 1, [ok], waves=4, pollers=3) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], waves=8, pollers=4) == _lib.QLX_EINVAL
-    assert build(_lib.FMT_FP8, 1, [ok], waves=4, pollers=6) == _lib.QLX_EINVAL
+    assert build(_lib.FMT_FP8, 1, [ok], waves=12) == _lib.QLX_EINVAL
     bad_k = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 500, _lib.MODE_BF16, 0)
     assert build(_lib.FMT_W8A16, 1, [bad_k]) == _lib.QLX_EINVAL
     bad_kw = _lib.StackCall(1 << 20, 1 << 21, 1 << 22, 1 << 23, 256, 512, _lib.MODE_BF16, 3)
@@ -164,21 +161,21 @@ def test_decode_stack_contract_on_host():
             DecodeStack(fmt, m)
     with pytest.raises(ValueError):
         DecodeStack("w8a16", 1).build()
-    launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 0)
+    launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0)
     assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, launch, 1, None, 10, None) == _lib.QLX_EINVAL
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, 0, 1 << 21, 10, None) == _lib.QLX_EINVAL
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0, 0)  # descriptor copy past the LDS
+    bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0)  # descriptor copy past the LDS
     assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    # pollers beside 8 compute waves; FP8 row maxima past the LDS or misaligned; an epoch whose
-    # low 16 bits (the tag of published values) are 0
-    for shape in ((8, 4, 0), (4, 4, 1020), (4, 4, 8)):
-        bad = _lib.StackLaunch(256, 1024, shape[0], -1, 1, shape[1], shape[2])
+    # 6 waves per workgroup; FP8 row maxima past the LDS or misaligned; an epoch whose low 16
+    # bits (the tag of published values) are 0
+    for waves, amax_off in ((6, 0), (4, 1020), (4, 8)):
+        bad = _lib.StackLaunch(256, 1024, waves, -1, 1, amax_off)
         assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    good = _lib.StackLaunch(256, 1024, 4, -1, 1, 4, 0)
+    good = _lib.StackLaunch(256, 1024, 4, -1, 1, 0)
     assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, good, 1 << 16, 1 << 21, 10, None) == _lib.QLX_EINVAL
     # the pieces flag selects the kernel with or without the K-piece reduction: 0 or 1 only
-    bad = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 0, 2)
+    bad = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 2)
     assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
     assert "pieces" in _lib.last_error()
 
@@ -213,17 +210,16 @@ def test_executor_refuses_graph_capture(monkeypatch):
 def test_norm_stage_contract_on_host():
     """The executor's residual + RMSNorm stages are checked before any device work: x must be
     NULL exactly for a norm stage, the delta must be the whole output of an earlier projection,
-    the residual may not be memory the chain writes, m * k must fit one staging pass, and the
-    workgroups may have no poller waves."""
+    the residual may not be memory the chain writes, and m * k must fit one staging pass."""
     from kernels import _lib
     import ctypes
     lib = _lib.lib()
     out = (ctypes.c_longlong(0), _lib.StackLaunch())
 
-    def build(m, calls, norms, waves=8, pollers=0):
+    def build(m, calls, norms, waves=8):
         arr = (_lib.StackCall * len(calls))(*calls)
         nrm = (_lib.NormInput * len(norms))(*norms)
-        return lib.qlx_stack_build_normed(_lib.FMT_FP8, m, arr, len(calls), nrm, waves, 1, pollers, None, None, None,
+        return lib.qlx_stack_build_normed(_lib.FMT_FP8, m, arr, len(calls), nrm, waves, 1, None, None, None,
                                           ctypes.byref(out[0]), ctypes.byref(out[1]))
 
     W, S, R, NW = 1 << 30, 1 << 31, 1 << 32, 1 << 33
@@ -242,9 +238,8 @@ def test_norm_stage_contract_on_host():
     assert build(1, [first, normed], [plain, bad_resid]) == _lib.QLX_EINVAL and "residual" in _lib.last_error()
     # m * k beyond one staging pass (3 chunks of 8 per thread of 8 waves: m <= 4 at k = 2560)
     assert build(5, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
-    # poller waves
-    assert build(1, [first, normed], [plain, good], waves=4, pollers=2) == _lib.QLX_EINVAL
-    assert "poller" in _lib.last_error()
+    # ... and at 4 waves per workgroup already m = 3 is beyond it (3 * 4 * 64 * 8 = 6144 < 3 * 2560)
+    assert build(3, [first, normed], [plain, good], waves=4) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
 
 
 def test_qkv_consumer_and_attention_contract_on_host():

@@ -65,12 +65,12 @@ def source(bufs, src):
     return bufs[src]
 
 
-def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, pollers=0, chain_def=None):
+def build_chain(fmt, m, seed, kw=0, waves=8, lanes=1, chain_def=None):
     quant = qlinear.FORMATS[fmt][0]
     bufs = {"x": rand((m, 1024), seed).to(DEV), "g": rand((m, 9728), seed + 1).to(DEV),
             "x2560": rand((m, 2560), seed + 2).to(DEV)}
     weights, raw = {}, {}
-    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes, pollers=pollers)
+    chain = DecodeStack(fmt, m, waves=waves, groups_per_cu=lanes)
     for idx, (name, n, k, src, sw) in enumerate(chain_def or CHAIN):
         w = rand((n, k), seed + 10 + idx, std=0.02).to(DEV)
         packed = quant(w)
@@ -117,9 +117,9 @@ def oracle_check(fmt, x_bits, packed, y, swiglu=False):
     return O.rel_l2(y.float().cpu().numpy(), ref)
 
 
-def run_chain_checks(fmt, m, waves=8, pollers=0):
-    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m, waves=waves, pollers=pollers)
-    assert chain.grid >= 256 and chain.lds > 0 and chain.launch.pollers == pollers
+def run_chain_checks(fmt, m, waves=8):
+    chain, bufs, weights, raw = build_chain(fmt, m, 100 * m, waves=waves)
+    assert chain.grid >= 256 and chain.lds > 0 and chain.launch.waves == waves
     for run in range(3):
         if run:
             bufs["x"].copy_(rand((m, 1024), 7 * run + m).to(DEV))
@@ -146,12 +146,12 @@ def test_chain_matches_single_calls_and_oracle(fmt, m):
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
-@pytest.mark.parametrize("m,pollers", [(1, 4), (5, 2), (16, 4)])
-def test_poller_chain_matches_single_calls_and_oracle(fmt, m, pollers):
-    """Poller waves staging the activations (m = 16 at FP8: more than one pass over each row
-    for the token maxima) give the same results as the single-call linears."""
-    print(f"decode stack pollers {fmt} m={m} pollers={pollers}", flush=True)
-    run_chain_checks(fmt, m, waves=4, pollers=pollers)
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_four_wave_chain_matches_single_calls_and_oracle(fmt, m):
+    """Workgroups of 4 waves (half the staging threads: m = 16 at FP8 takes more than one pass
+    over each row for the token maxima) give the same results as the single-call linears."""
+    print(f"decode stack 4 waves {fmt} m={m}", flush=True)
+    run_chain_checks(fmt, m, waves=4)
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
@@ -179,20 +179,19 @@ def test_layer_chain_without_pieces(fmt):
 
 
 @pytest.mark.parametrize("kw", [1, 2, 4, 8])
-@pytest.mark.parametrize("pollers", [0, 4])
-def test_every_tile_split_is_exact(kw, pollers):
+@pytest.mark.parametrize("fmt,waves", [("w4a16", 8), ("fp8", 4)])
+def test_every_tile_split_is_exact(kw, fmt, waves):
     """Forced waves-per-tile settings change the pieces, not the results' bound."""
-    print(f"decode stack kw={kw} pollers={pollers}", flush=True)
-    if pollers and kw == 8:
-        pytest.skip("8 waves per tile needs 8 compute waves, which take no pollers")
-    fmt = "fp8" if pollers else "w4a16"
-    chain, bufs, weights, _ = build_chain(fmt, 3, 77, kw=kw, waves=4 if pollers else 8, pollers=pollers)
+    print(f"decode stack kw={kw} {fmt} waves={waves}", flush=True)
+    if kw > waves:
+        pytest.skip("8 waves per tile need a workgroup of 8 waves")
+    chain, bufs, weights, _ = build_chain(fmt, 3, 77, kw=kw, waves=waves)
     assert all(c[1] == kw for c in chain.configs)
     assert chain.launch.pieces == int(any(c[3] > 1 for c in chain.configs))
     chain.run()
     torch.cuda.synchronize()
     assert not chain.failed()
-    check_against_single_calls(fmt, bufs, weights, ("kw", kw, pollers))
+    check_against_single_calls(fmt, bufs, weights, ("kw", kw, waves))
 
 
 @pytest.mark.parametrize("fmt,waves,lanes,m", [("fp8", 4, 3, 4), ("w4a16", 4, 2, 4), ("w8a16", 8, 2, 4),
@@ -214,13 +213,13 @@ def test_lanes_and_small_workgroups(fmt, waves, lanes, m):
         check_against_single_calls(fmt, bufs, weights, (fmt, waves, lanes, run))
 
 
-@pytest.mark.parametrize("waves,pollers,m", [(8, 0, 2), (4, 4, 2), (8, 0, 8)])
-def test_bounded_wait_gives_up_and_recovers(waves, pollers, m):
+@pytest.mark.parametrize("waves,m", [(8, 2), (4, 2), (8, 8)])
+def test_bounded_wait_gives_up_and_recovers(waves, m):
     """A zero wait budget makes the waits give up (forced from the host): the kernel still
     ends, flags the run, and after reset() a normal run is right again (FP8 at 8 tokens: the
     wait for the published token maxima too)."""
-    print(f"decode stack bounded wait waves={waves} pollers={pollers} m={m}", flush=True)
-    chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves, pollers=pollers)
+    print(f"decode stack bounded wait waves={waves} m={m}", flush=True)
+    chain, bufs, weights, _ = build_chain("fp8", m, 55, waves=waves)
     chain.run(budget_us=0)
     torch.cuda.synchronize()
     assert chain.failed()
