@@ -132,7 +132,9 @@ __host__ __device__ inline void share_item(int p, int g, int U, int pe, int gran
 // blocks are never cut into K pieces runs a kernel without the piece reduction, whose
 // registers allow FP8 a deeper prefetch. Measured on the Qwen3-4B M=1 chain (us per step):
 // FP8 1217 / 1223 / 1205 / 1203 / 1229 at 6 / 8 / 9 / 10 / 11 steps; W8A16 1383 / 1405 /
-// 1400 at 6 / 7 / 8; W4A16 1224 / 1242 at 4 / 5.
+// 1400 at 6 / 7 / 8; W4A16 1224 / 1242 at 4 / 5. FP8 with the piece reduction (chains of
+// more than 4 tokens) at 6 steps spilled 5 registers; at 4 it spills none (M = 8 / 16 chains
+// 2411-2416 / 3541-3548 us at 6, 2386-2393 / 3518-3522 at 4 or 5).
 template <class F, bool PIECES>
 struct ExecDepth {
   static constexpr int PF = 6;
@@ -140,6 +142,10 @@ struct ExecDepth {
 template <>
 struct ExecDepth<FmtFP8, false> {
   static constexpr int PF = 10;
+};
+template <>
+struct ExecDepth<FmtFP8, true> {
+  static constexpr int PF = 4;
 };
 template <bool PIECES>
 struct ExecDepth<FmtW4, PIECES> {
