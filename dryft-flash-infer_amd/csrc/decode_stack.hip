@@ -134,7 +134,8 @@ __host__ __device__ inline void share_item(int p, int g, int U, int pe, int gran
 // FP8 1217 / 1223 / 1205 / 1203 / 1229 at 6 / 8 / 9 / 10 / 11 steps; W8A16 1383 / 1405 /
 // 1400 at 6 / 7 / 8; W4A16 1224 / 1242 at 4 / 5. FP8 with the piece reduction (chains of
 // more than 4 tokens) at 6 steps spilled 5 registers; at 4 it spills none (M = 8 / 16 chains
-// 2411-2416 / 3541-3548 us at 6, 2386-2393 / 3518-3522 at 4 or 5).
+// 2411-2416 / 3541-3548 us at 6, 2386-2393 / 3518-3522 at 4 or 5); W4A16's at 4 spilled 14-20,
+// at 3 none (M = 8 chain 1541-1543 us at 4, 1478 at 3, 1484-1485 at 2).
 template <class F, bool PIECES>
 struct ExecDepth {
   static constexpr int PF = 6;
@@ -149,7 +150,7 @@ struct ExecDepth<FmtFP8, true> {
 };
 template <bool PIECES>
 struct ExecDepth<FmtW4, PIECES> {
-  static constexpr int PF = 4;
+  static constexpr int PF = PIECES ? 3 : 4;
 };
 
 // Group scales a workgroup's threads hold for one item (formats with per-group scales): up
