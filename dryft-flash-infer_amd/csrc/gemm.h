@@ -626,8 +626,8 @@ __host__ __device__ constexpr int stage_unroll() {
 }
 
 // The threads that stage and finish a work item, and how they wait for each other: the
-// whole workgroup and its barrier here; the decode executor's compute waves (without its
-// weight-loading waves) bring their own.
+// whole workgroup and its barrier here; the decode executor passes its own team (the same
+// threads, counted at compile time).
 struct BlockTeam {
   __device__ int tid() const { return threadIdx.x; }
   __device__ int size() const { return blockDim.x; }
