@@ -24,10 +24,17 @@
 //     epoch} with one device-coherent store each, and the reader polls exactly the words it
 //     needs until their epoch is the current run's. A dependency costs one store-to-load
 //     trip instead of a store, its acknowledgement, a counter update and a counter poll.
-//     Every run has a new nonzero epoch, so words left by earlier runs never match.
+//     Every run has a new nonzero epoch, so words left by earlier runs never match. The
+//     epoch lives in the arena's first words: each workgroup reads the last run's epoch at
+//     its start and uses the next one; the workgroup that finishes last (a ticket) stores it.
+//     The launch takes no per-run argument, so a run captures into a HIP graph and every
+//     replay is a new run.
 //   * Every wait is bounded by a per-run deadline on the 100 MHz real-time counter: a wait
 //     past it sets the error flag and moves on (that run's outputs are undefined), so the
-//     kernel always ends. Cooperative launch guarantees that every workgroup is resident.
+//     kernel always ends. The grid is one workgroup per CU per lane and the planner checks
+//     that this many fit the device at once (occupancy), so on an otherwise idle GPU every
+//     workgroup is resident; where other work holds CUs, waits run out the deadline rather
+//     than hang.
 #include <vector>
 
 #include "exec_common.h"
@@ -35,6 +42,7 @@
 namespace qlx {
 
 constexpr int kMaxPieces = 4;  // pieces of one row block (the reducer has all in flight)
+constexpr long long kArenaCtlBytes = 256;  // arena head: {last run's epoch, finish ticket}
 
 // One projection of the chain, as the executor reads it (from LDS when the chain's
 // descriptors fit next to the items' LDS: read once per launch instead of missing the
@@ -761,11 +769,15 @@ __device__ __forceinline__ NextItem find_next(const StackDesc* calls, int ncalls
 
 template <class F, int WAVES, bool DLDS, bool PIECES>
 __global__ void __launch_bounds__(WAVES * 64)
-stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, int* err, long long budget_ticks,
+stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, int* err, long long budget_ticks,
              int desc_off, int lanes, int amax_off) {
   extern __shared__ __align__(16) char lds[];
   const int per_lane = gridDim.x / lanes;
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
+  // This run's epoch: the next after the last finished run's, skipping low 16 bits of 0 (the
+  // tag of a zeroed arena).
+  uint32_t epoch = __hip_atomic_load(gmem(ctl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  if ((epoch & 0xffffu) == 0u) epoch += 1u;
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   constexpr bool MAXIMA = std::is_same<F, FmtFP8>::value;  // published row-block maxima
   uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 staging: per-token maxima
@@ -813,6 +825,15 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t epoch, i
     ng = after.g;
     if (have) exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     __syncthreads();  // LDS is reused by the next item
+  }
+  // The last workgroup to finish hands this run's epoch to the next run. Every workgroup read
+  // the previous one at its start, before it took its ticket here.
+  if (threadIdx.x == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(gmem(ctl + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1) {
+      __hip_atomic_store(gmem(ctl + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gmem(ctl), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -1014,12 +1035,22 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     }
     return false;
   };
+  // Everything the launch writes -- projection outputs, and the residual and normed input a
+  // stage writes back -- must be disjoint: two writers of one range race, and a stage's
+  // residual is looked up by the address an earlier stage wrote it to.
+  struct Range { const void* p; long long bytes; int call; const char* what; };
+  std::vector<Range> outs;
   for (int c = 0; c < ncalls; ++c) {
-    const long long ybytes = 2LL * m * nout(c);
-    for (int j = 0; j < ncalls; ++j) {
-      if (j != c) QLX_REQUIRE(!overlaps(calls[c].y, ybytes, calls[j].y, 2LL * m * nout(j)),
-                              "outputs of projections %d and %d overlap", c, j);
-    }
+    outs.push_back({calls[c].y, 2LL * m * nout(c), c, "output"});
+    if (normed(c) && norms[c].resid_out) outs.push_back({norms[c].resid_out, 2LL * m * calls[c].k, c, "resid_out"});
+    if (normed(c) && norms[c].normed_out) outs.push_back({norms[c].normed_out, 2LL * m * calls[c].k, c, "normed_out"});
+  }
+  for (size_t a = 0; a < outs.size(); ++a)
+    for (size_t b = a + 1; b < outs.size(); ++b)
+      QLX_REQUIRE(!overlaps(outs[a].p, outs[a].bytes, outs[b].p, outs[b].bytes),
+                  "the %s of projection %d and the %s of projection %d overlap", outs[a].what, outs[a].call,
+                  outs[b].what, outs[b].call);
+  for (int c = 0; c < ncalls; ++c) {
     if (normed(c)) {
       const qlx_norm_input& nd = norms[c];
       const long long rbytes = 2LL * m * calls[c].k;
@@ -1033,7 +1064,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
         QLX_REQUIRE(src[c] >= 0, "projection %d: the delta of a norm stage is the whole output of an earlier "
                     "projection", c);
       }
-      for (int j = 0; j < c; ++j)
+      for (int j = c - 1; j >= 0; --j)  // resid_out ranges are disjoint: at most one matches
         if (normed(j) && norms[j].resid_out && nd.resid == norms[j].resid_out && calls[j].k == calls[c].k) {
           rsrc[c] = j;
           rpublished[j] = 1;
@@ -1122,7 +1153,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     return a.rt;
   };
   // Arena: published outputs (and their maxima) and partial sums, 256-byte aligned regions.
-  long long off = 0;
+  long long off = kArenaCtlBytes;  // [0, 256): the run epoch and the finish ticket
   std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1), max_off(ncalls, -1), rpub_off(ncalls, -1);
   for (int c = 0; c < ncalls; ++c) {
     if (published[c]) {
@@ -1216,29 +1247,29 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   return QLX_OK;
 }
 
-int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
-                  int* error, long long budget_us, void* stream) {
+int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, void* arena, int* error,
+                  long long budget_us, void* stream) {
   QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1,
               "bad executor launch configuration");
   QLX_REQUIRE(launch->pieces == 0 || launch->pieces == 1, "launch.pieces must be 0 or 1 (got %d)", launch->pieces);
   const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0, launch->pieces != 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
-  QLX_REQUIRE(desc && error && ncalls >= 1, "bad executor arguments");
+  QLX_REQUIRE(desc && arena && error && ncalls >= 1, "bad executor arguments");
+  QLX_REQUIRE(reinterpret_cast<uintptr_t>(arena) % 256 == 0, "the arena must be 256-byte aligned");
   QLX_REQUIRE(launch->desc_lds < 0 || launch->desc_lds + (long long)ncalls * (long long)sizeof(StackDesc) <=
                                           launch->lds_bytes,
               "descriptor copy does not fit the launch's LDS");
   QLX_REQUIRE(launch->amax_off >= 0 && launch->amax_off % 16 == 0 && launch->amax_off + 64 <= launch->lds_bytes,
               "bad executor LDS layout");
-  QLX_REQUIRE((epoch & 0xffffu) != 0, "epoch %u: its low 16 bits tag published values and must not be 0 "
-              "(a zeroed arena carries tag 0)", epoch);
   QLX_REQUIRE(budget_us >= 0 && budget_us <= 600000000LL, "budget_us must be 0..600e6");
   long long ticks = budget_us * 100;  // the real-time counter runs at 100 MHz
   int desc_off = launch->desc_lds, lanes = launch->lanes, amax_off = launch->amax_off;
   QLX_REQUIRE(lanes >= 1 && launch->grid % lanes == 0, "bad executor lanes");
-  void* args[] = {(void*)&desc,     (void*)&ncalls, (void*)&epoch,   (void*)&error,
+  uint32_t* ctl = static_cast<uint32_t*>(arena);
+  void* args[] = {(void*)&desc,     (void*)&ncalls, (void*)&ctl,     (void*)&error,
                   (void*)&ticks,    (void*)&desc_off, (void*)&lanes, (void*)&amax_off};
-  hipError_t e = hipLaunchCooperativeKernel(fn, dim3(launch->grid), dim3(launch->waves * 64), args,
-                                            (unsigned)launch->lds_bytes, (hipStream_t)stream);
+  hipError_t e = hipLaunchKernel(fn, dim3(launch->grid), dim3(launch->waves * 64), args,
+                                 (size_t)launch->lds_bytes, (hipStream_t)stream);
   return hip_status(e, "stack_run");
 }
 

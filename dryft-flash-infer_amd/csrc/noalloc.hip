@@ -58,6 +58,10 @@ __global__ void __launch_bounds__(256) zero_ints(int* p, int count) {
 extern "C" int qlx_linear_skinny_noalloc(int fmt, const void* w, const void* w_scale, const void* x, void* y, int m,
                                          int n, int k, int mode, void* stream) {
   QLX_REQUIRE(w && w_scale && x && y, "linear_skinny_noalloc: NULL pointer");
+  // The formats qlx_linear_skinny serves; checked before the shared array is touched, so a
+  // rejected call enqueues nothing.
+  QLX_REQUIRE(fmt == QLX_FMT_W4A16 || fmt == QLX_FMT_W8A16,
+              "linear_skinny_noalloc serves W4A16 and W8A16 (format %d)", fmt);
   qlx_plan plan = {};
   int rc = qlx_plan_skinny(fmt, mode, m, n, k, &plan);
   if (rc != QLX_OK) return rc;

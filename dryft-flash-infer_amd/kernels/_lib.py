@@ -111,7 +111,7 @@ SIGNATURES = {
                          ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _P,
                                 _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)], _I),
-    "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), ctypes.c_uint, _P, _LL, _P], _I),
+    "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), _P, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
     "qlx_qkv_norm_rope": ([ctypes.POINTER(RopeArgs), _P], _I),
     "qlx_attention_workspace": ([_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_size_t)], _I),

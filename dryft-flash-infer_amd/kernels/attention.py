@@ -103,47 +103,81 @@ class DecodeAttention:
     @torch.no_grad()
     def tuned(self, keys, values, first_position, last_position, use_graph=True, key_scales=None,
               value_scales=None):
-        """Race the split counts once, before capturing decode (attention.py:227-280's contract).
+        """Pick the split count once, before decode is captured (the reference's contract,
+        engine/kernels/attention.py:227-280: every layer's cache at both ends of generation, a
+        candidate agrees with this object within 0.04 and is finite, the planned object stays
+        unless another is more than 5 % faster; returns the chosen object).
 
-        Every layer's cache is swept at both ends of generation; a candidate must agree with
-        this object's output within 0.04 and be finite, and the incumbent stays unless a
-        candidate is more than 5 % faster. Returns the chosen object.
+        Every split count is built and checked for agreement first. Each one admitted then gets
+        one timed program -- all layers' caches at both positions, extended to a 1 GiB rotation
+        so the Infinity Cache cannot serve the keys, captured as one HIP graph -- and the
+        programs run in rounds, each round in a rotated order, so a clock or thermal drift over
+        the race touches every candidate alike. The statistic is the median over rounds.
         """
-        from .timing import time_calls
+        from .timing import rotation
 
-        q = torch.randn(self.batch * self.tokens, self.n_q * self.head_dim, dtype=torch.bfloat16,
-                        device=self.out.device)
-        pos = torch.tensor([first_position], dtype=torch.int32, device=self.out.device)
-        operands = list(zip(keys, values, key_scales, value_scales)) if self.quant else list(zip(keys, values))
-        positions = sorted({first_position, last_position})
-        expected = []
-        for value in positions:
-            pos.fill_(value)
-            expected.append(self(q, *operands[0][:2], pos, *operands[0][2:]).clone())
+        device = self.out.device
+        gen = torch.Generator(device=device).manual_seed(0)
+        q = torch.randn(self.batch * self.tokens, self.n_q * self.head_dim, generator=gen, device=device)
+        q = q.to(torch.bfloat16)
+        ends = [torch.tensor([p], dtype=torch.int32, device=device) for p in sorted({first_position, last_position})]
+        scales = zip(key_scales, value_scales) if self.quant else ((None, None) for _ in keys)
+        caches = [(k, v, ks, vs) for (k, v), (ks, vs) in zip(zip(keys, values), scales)]
+        if not caches:
+            raise ValueError("tuned needs at least one layer's cache")
 
-        def measure(candidate):
-            total = 0.0
-            for value, want in zip(positions, expected):
-                pos.fill_(value)
-                got = candidate(q, *operands[0][:2], pos, *operands[0][2:])
-                if not torch.isfinite(got).all().item() or (got.float() - want.float()).abs().max().item() > 0.04:
-                    return float("inf")
-                total += time_calls(lambda kv: candidate(q, kv[0], kv[1], pos, *kv[2:]), operands, reps=1,
-                                    trials=3, use_graph=use_graph)
-            return total / len(positions)
+        def first_layer(attn):
+            k, v, ks, vs = caches[0]
+            return [attn(q, k, v, p, ks, vs).clone() for p in ends]
 
-        incumbent = measure(self)
-        best, elapsed = self, incumbent
-        for splits in (1, 2, 4, 8, 16, 32, 64):
-            if splits == self.splits:
-                continue
-            candidate = DecodeAttention(self.batch, self.n_kv, self.group, self.head_dim, self.capacity,
-                                        self.out.device, tokens=self.tokens, config=splits, quant=self.quant)
-            trial = measure(candidate)
-            if trial < elapsed:
-                best, elapsed = candidate, trial
-        if elapsed > incumbent * 0.95:
-            best, elapsed = self, incumbent
-        print(f"engine: attention splits={best.splits} {incumbent / elapsed:.2f}x vs planned {self.splits}",
+        planned = first_layer(self)
+        pool = [self] + [DecodeAttention(self.batch, self.n_kv, self.group, self.head_dim, self.capacity, device,
+                                         tokens=self.tokens, config=s, quant=self.quant)
+                         for s in (1, 2, 4, 8, 16, 32, 64) if s != self.splits]
+        admitted = []
+        for attn in pool:
+            outs = first_layer(attn)
+            if all(bool(torch.isfinite(o).all()) and float((o.float() - w.float()).abs().max()) <= 0.04
+                   for o, w in zip(outs, planned)):
+                admitted.append(attn)
+        if self not in admitted:  # cannot happen: the planned object is its own reference
+            admitted.insert(0, self)
+
+        work = rotation([(cache, p) for cache in caches for p in ends])
+        programs = []
+        for attn in admitted:
+            def sweep(attn=attn):
+                for (k, v, ks, vs), p in work:
+                    attn(q, k, v, p, ks, vs)
+            sweep()  # creates nothing lazily, but runs every operand once before a capture
+            if use_graph:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    sweep()
+                graph.replay()
+                programs.append(graph.replay)
+            else:
+                programs.append(sweep)
+        torch.cuda.synchronize()
+
+        rounds = 5
+        samples = [[] for _ in admitted]
+        for r in range(rounds):
+            order = [(i + r) % len(admitted) for i in range(len(admitted))]
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(order) + 1)]
+            marks[0].record()
+            for j, i in enumerate(order):
+                programs[i]()
+                marks[j + 1].record()
+            marks[-1].synchronize()
+            for j, i in enumerate(order):
+                samples[i].append(marks[j].elapsed_time(marks[j + 1]) / len(work))
+        medians = [sorted(v)[len(v) // 2] for v in samples]
+        fastest = min(range(len(admitted)), key=medians.__getitem__)
+        mine = admitted.index(self)
+        choice = fastest if medians[fastest] < 0.95 * medians[mine] else mine
+        chosen = admitted[choice]
+        print(f"engine: attention splits={chosen.splits} ({medians[choice] * 1e3:.1f} us per call; planned "
+              f"{self.splits}: {medians[mine] * 1e3:.1f} us; {len(admitted)}/{len(pool)} split counts agree)",
               file=sys.stderr)
-        return best
+        return chosen

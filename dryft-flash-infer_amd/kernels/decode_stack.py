@@ -1,4 +1,4 @@
-"""Decode-step executor: a chain of quantized projections run by one cooperative launch.
+"""Decode-step executor: a chain of quantized projections run by one launch.
 
 The reference replays a captured graph of per-projection launches whose weight loads
 overlap the previous kernel through programmatic dependent launch
@@ -47,7 +47,6 @@ class DecodeStack:
         self.calls, self._keep = [], []
         self.norms = []
         self.desc = None
-        self.epoch = 0
 
     def add(self, weight, x, y, swiglu=False, kw=0):
         """Append y = x @ W^T (or the SwiGLU of [gate; up] rows) to the chain. ``kw`` forces
@@ -140,22 +139,16 @@ class DecodeStack:
         self.launch = launch
         self.grid, self.lds = launch.grid, launch.lds_bytes
         self.device = device
-        self.epoch = 0
         return self
 
     def run(self, budget_us=BUDGET_US):
-        """Run the whole chain once on the current stream.
-
-        Not capturable into a graph: each run tags what it publishes with a new epoch passed
-        as a kernel argument, and every replay of a captured run would carry the same one, so
-        waiting workgroups would take the previous replay's values for this one's."""
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("DecodeStack.run cannot be captured into a graph: every run needs a new epoch")
+        """Run the whole chain once on the current stream. Capturable: the run's epoch (the tag
+        of what it publishes) is kept in the arena and advanced by the kernel, so every replay
+        of a captured run is a new run. Runs of one chain must not overlap (one stream)."""
         if self.desc is None:
             self.build()
-        self.epoch = self.epoch % 0xFFFF + 1  # its low 16 bits tag published values: 1..65535
         _lib.call("qlx_stack_run", _FMTS[self.fmt], _lib.ptr(self.desc), len(self.calls), ctypes.byref(self.launch),
-                  self.epoch, _lib.ptr(self.error), int(budget_us), _lib.stream(self.device))
+                  _lib.ptr(self.arena), _lib.ptr(self.error), int(budget_us), _lib.stream(self.device))
 
     def failed(self):
         """True if a wait of any run so far gave up (that run's outputs are undefined).

@@ -3,10 +3,8 @@
  *
  * Plain pointers and sizes only. Every pointer argument is device memory (HBM) unless
  * it says otherwise; `stream` is a hipStream_t (NULL = the default stream). No entry
- * point allocates, synchronises or reads device memory on the host, so every call except
- * qlx_stack_run is safe to capture into a hipGraph (a run's `epoch`
- * argument must differ from the previous run's, and every replay of a captured run would
- * repeat it). Each
+ * point allocates, synchronises or reads device memory on the host, so every call is safe to
+ * capture into a hipGraph. Each
  * returns QLX_OK (0) or a negative status; qlx_last_error() then holds a message
  * (thread-local).
  *
@@ -295,7 +293,7 @@ int qlx_stack_desc_size(void);
 
 /* Launch configuration of a chain, filled by qlx_stack_build, passed to qlx_stack_run. */
 typedef struct qlx_stack_launch {
-  int grid;        /* workgroups (all resident: cooperative launch) */
+  int grid;        /* workgroups (one per CU per lane; the planner checks they fit at once) */
   int lds_bytes;   /* dynamic LDS per workgroup */
   int waves;       /* waves per workgroup */
   int desc_lds;    /* byte offset of the descriptors' LDS copy, or -1 (read from memory) */
@@ -316,19 +314,22 @@ typedef struct qlx_stack_launch {
  * Outputs must not overlap each other or an input read from memory (EINVAL otherwise).
  * Replaces the reference's per-projection launches chained by programmatic dependent launch
  * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
- * engine/kernels/cuda_jit.py:218-262): here the whole chain is one cooperative launch. */
+ * engine/kernels/cuda_jit.py:218-262): here the whole chain is one launch. The arena's first
+ * 256 bytes hold the run epoch and a finish counter (zero in a fresh arena). */
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
                     void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch);
 
-/* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors and `launch` its
- * launch configuration. The low 16 bits of `epoch` tag the values the run publishes: they must
- * be nonzero and differ from the previous run's on the same arena (a counter over 1..65535).
- * `error` is one int32 in device memory, zero before the run: once a wait passes `budget_us`
- * microseconds from the run's start, every wait gives up, the first one writing (1 << kind) to
- * it (0: an input from an earlier projection, 1: a piece's partial sums), and that run's
- * outputs are undefined. Runs sharing an arena must not overlap. */
-int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, unsigned epoch,
-                  int* error, long long budget_us, void* stream);
+/* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors, `launch` its
+ * launch configuration and `arena` the arena they were built for (256-byte aligned). Each run
+ * tags what it publishes with the next epoch after the one the arena holds and stores it there
+ * when its last workgroup finishes, so the call has no per-run argument and captures into a
+ * hipGraph (every replay is a new run). `error` is one int32 in device memory, zero before the
+ * run: once a wait passes `budget_us` microseconds from the run's start, every wait gives up,
+ * the first one writing (1 << kind) to it (0: an input from an earlier projection, 1: a
+ * piece's partial sums), and that run's outputs are undefined. Runs sharing an arena must not
+ * overlap (same stream, or ordered). */
+int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, void* arena, int* error,
+                  long long budget_us, void* stream);
 
 /* ---- residual add + RMSNorm input stages of the decode-step executor ----------------- */
 

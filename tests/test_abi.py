@@ -162,21 +162,25 @@ def test_decode_stack_contract_on_host():
     with pytest.raises(ValueError):
         DecodeStack("w8a16", 1).build()
     launch = _lib.StackLaunch(256, 1024, 8, -1, 1, 0)
-    assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, launch, 1, None, 10, None) == _lib.QLX_EINVAL
-    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, 0, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    A, E = 1 << 21, 1 << 22  # arena (256-byte aligned) and error word
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, None, 1, launch, A, E, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, None, E, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, A, None, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, None, A, E, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 1, launch, A + 16, E, 10, None) == _lib.QLX_EINVAL
+    assert "aligned" in _lib.last_error()
     bad = _lib.StackLaunch(256, 1024, 8, 1000, 1, 0)  # descriptor copy past the LDS
-    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
-    # 6 waves per workgroup; FP8 row maxima past the LDS or misaligned; an epoch whose low 16
-    # bits (the tag of published values) are 0
+    assert lib.qlx_stack_run(_lib.FMT_W4A16, 1 << 20, 4, bad, A, E, 10, None) == _lib.QLX_EINVAL
+    # 6 waves per workgroup; FP8 row maxima past the LDS or misaligned
     for waves, amax_off in ((6, 0), (4, 1020), (4, 8)):
         bad = _lib.StackLaunch(256, 1024, waves, -1, 1, amax_off)
-        assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+        assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, A, E, 10, None) == _lib.QLX_EINVAL
+    # a budget past its limit
     good = _lib.StackLaunch(256, 1024, 4, -1, 1, 0)
-    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, good, 1 << 16, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, good, A, E, 700000000, None) == _lib.QLX_EINVAL
     # the pieces flag selects the kernel with or without the K-piece reduction: 0 or 1 only
     bad = _lib.StackLaunch(256, 1024, 8, -1, 1, 0, 2)
-    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, 1, 1 << 21, 10, None) == _lib.QLX_EINVAL
+    assert lib.qlx_stack_run(_lib.FMT_FP8, 1 << 20, 1, bad, A, E, 10, None) == _lib.QLX_EINVAL
     assert "pieces" in _lib.last_error()
 
 
@@ -194,17 +198,6 @@ def test_selection_api_mirrors_the_reference():
         ops = bad.pop("operands")
         with pytest.raises(ValueError):
             timing.time_calls(lambda w: None, ops, **bad)
-
-
-def test_executor_refuses_graph_capture(monkeypatch):
-    """The executor tags what a run publishes with an epoch passed as a kernel argument, so a
-    captured run would replay with the same tag: run() raises under capture (forced from the host:
-    no device work happens)."""
-    import torch
-    from kernels.decode_stack import DecodeStack
-    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    with pytest.raises(RuntimeError, match="captured"):
-        DecodeStack("fp8", 1).run()
 
 
 def test_norm_stage_contract_on_host():
@@ -240,6 +233,23 @@ def test_norm_stage_contract_on_host():
     assert build(5, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
     # ... and at 4 waves per workgroup already m = 3 is beyond it (3 * 4 * 64 * 8 = 6144 < 3 * 2560)
     assert build(3, [first, normed], [plain, good], waves=4) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
+    # Two layers that reuse one resid_out buffer (separate outputs y): two stages would write the
+    # same residual and a later stage could not tell which one it reads.
+    H0, H1 = 1 << 38, 1 << 39
+    third = _lib.StackCall(W, S, None, 1 << 41, 256, 2560, _lib.MODE_BF16, 0)
+    layer1 = _lib.NormInput(R, None, NW, H0, None, 1e-6, 0)
+    layer2 = _lib.NormInput(H0, 1 << 35, NW, H0, None, 1e-6, 0)             # writes H0 again
+    assert build(1, [first, normed, third], [plain, layer1, layer2]) == _lib.QLX_EINVAL
+    assert "resid_out" in _lib.last_error() and "overlap" in _lib.last_error()
+    # a stage's resid_out inside another projection's output, and a normed_out overlapping a resid_out
+    into_y = _lib.NormInput(R, None, NW, (1 << 35) + 64, None, 1e-6, 0)
+    assert build(1, [first, normed], [plain, into_y]) == _lib.QLX_EINVAL and "overlap" in _lib.last_error()
+    both = _lib.NormInput(R, None, NW, H0, H0 + 1024, 1e-6, 0)
+    assert build(1, [first, normed], [plain, both]) == _lib.QLX_EINVAL and "normed_out" in _lib.last_error()
+    # disjoint per-layer buffers pass every host check (and reach the device query)
+    layer2_ok = _lib.NormInput(H0, 1 << 35, NW, H1, None, 1e-6, 0)
+    status = build(1, [first, normed, third], [plain, layer1, layer2_ok])
+    assert status != _lib.QLX_EINVAL, _lib.last_error()
 
 
 def test_qkv_consumer_and_attention_contract_on_host():

@@ -204,19 +204,32 @@ def test_decode_attention_matches_oracle(batch, tokens, quant):
             assert rel_l2(got, want) <= 1e-2, (first, config)
 
 
-@pytest.mark.parametrize("tokens", [5, 8, 16])
-def test_decode_attention_many_query_rows(tokens):
-    """More than 16 query rows per KV head (speculative verification widths): 2-4 row tiles."""
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("tokens", [5, 8, 10, 16])
+def test_decode_attention_many_query_rows(tokens, quant):
+    """More than 16 query rows per KV head (speculative verification widths): 2, 2, 3 and 4 row
+    tiles (20, 32, 40, 64 rows at group 4), bf16 and INT8 caches. Past the live keys the bf16
+    cache holds NaN and the INT8 cache's scales hold NaN (the codes stay): no row may read them."""
     from kernels import DecodeAttention
     batch, capacity, group = 2, 300, 4
-    q, k, v, _, _ = attention_case(batch, tokens, capacity, 5 + tokens)
+    q, k, v, ks, vs = attention_case(batch, tokens, capacity, 5 + tokens, quant=quant)
     first = capacity - tokens - 7
     pos = torch.tensor([first], device="cuda", dtype=torch.int32)
-    want = oracle_attention(q, k, v, first, tokens, group)
+    want = oracle_attention(q, k, v, first, tokens, group, ks, vs)
+    kp, vp, ksp, vsp = k.clone(), v.clone(), ks, vs
+    if quant:
+        ksp, vsp = ks.clone(), vs.clone()
+        ksp[:, :, first + tokens:] = float("nan")
+        vsp[:, :, first + tokens:] = float("nan")
+    else:
+        kp[:, :, first + tokens:] = float("nan")
+        vp[:, :, first + tokens:] = float("nan")
     for config in (1, 8):
-        got = DecodeAttention(batch, 8, group, 128, capacity, "cuda", tokens=tokens, config=config)(
-            q, k, v, pos).float().cpu().numpy()
-        assert np.abs(got - want).max() <= 0.04 and rel_l2(got, want) <= 1e-2
+        print(f"attention rows: tokens {tokens} quant {quant} splits {config}", flush=True)
+        got = DecodeAttention(batch, 8, group, 128, capacity, "cuda", tokens=tokens, config=config, quant=quant)(
+            q, kp, vp, pos, ksp, vsp).float().cpu().numpy()
+        assert np.isfinite(got).all(), (tokens, quant, config)
+        assert np.abs(got - want).max() <= 0.04 and rel_l2(got, want) <= 1e-2, (tokens, quant, config)
 
 
 def test_decode_attention_long_context_and_determinism():

@@ -1,4 +1,4 @@
-"""GPU parity of the decode-step executor (one cooperative launch for a chain of projections).
+"""GPU parity of the decode-step executor (one launch for a chain of projections).
 
 The executor cuts each projection's K range into pieces of its own (balanced over the
 workgroups), so its fp32 sums are ordered differently from a single-call linear's: every
@@ -263,3 +263,31 @@ def test_chain_contract():
         DecodeStack("int8", 1)
     with pytest.raises(ValueError):
         DecodeStack("w4a16", 1).build()
+
+
+@pytest.mark.parametrize("fmt,m", [("fp8", 1), ("w4a16", 5), ("fp8", 8)])
+def test_captured_runs_replay_as_new_runs(fmt, m):
+    """A run captured into a HIP graph: each replay takes the next epoch from the arena, so it
+    waits for this replay's values, not the last one's. Replays alternate with eager input
+    changes, eager runs and synchronisations; every replay equals an eager run on its inputs."""
+    print(f"decode stack graph {fmt} m={m}", flush=True)
+    chain, bufs, weights, _ = build_chain(fmt, m, 500 + m)
+    chain.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain.run()
+    for rep in range(4):
+        bufs["x"].copy_(rand((m, 1024), 40 + rep).to(DEV))
+        bufs["g"].copy_(rand((m, 9728), 60 + rep).to(DEV))
+        for name, *_ in CHAIN:
+            bufs[name].fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert not chain.failed(), (rep, chain.failed_waits())
+        replayed = {name: bufs[name].clone() for name, *_ in CHAIN}
+        chain.run()
+        torch.cuda.synchronize()
+        for name, *_ in CHAIN:
+            assert torch.equal(bufs[name], replayed[name]), (fmt, m, rep, name)
+    check_against_single_calls(fmt, bufs, weights, (fmt, m, "graph"))

@@ -54,3 +54,6 @@ def test_noalloc_rejects_rows_past_its_tickets():
     p = ctypes.c_void_p(1 << 20)
     rc = lib.qlx_linear_skinny_noalloc(_lib.FMT_W4A16, p, p, p, p, 16, 16 * 16385, 256, _lib.MODE_BF16, None)
     assert rc == _lib.QLX_EINVAL and "exceeds" in _lib.last_error()
+    # FP8 has its own skinny entry point: rejected before the shared array is cleared
+    rc = lib.qlx_linear_skinny_noalloc(_lib.FMT_FP8, p, p, p, p, 16, 2560, 2560, _lib.MODE_BF16, None)
+    assert rc == _lib.QLX_EINVAL and "serves W4A16 and W8A16" in _lib.last_error()
