@@ -4,14 +4,17 @@
 One step is the quantized linear stream of one decode step at batch M: 36 layers x
 (qkv 2560->6144, o 4096->2560, gate_up 2560->2x9728 with the fused SwiGLU epilogue,
 down 9728->2560) plus the lm_head 2560->151936, each layer with its own synthetic
-weights (4.03 GB in FP8, so the 256 MB Infinity Cache cannot serve repeats). The
-projections form one dependent chain, as in a decode step: each layer's qkv reads the
-previous layer's down output, o reads the query part (first 4096 columns) of qkv's output
-(standing in for attention), gate_up reads o's output, down reads gate_up's, and the
-lm_head reads the last down output. Activations are resident in HBM.
+weights (4.03 GB in FP8, so the 256 MB Infinity Cache cannot serve repeats), wired as in a
+decode step: rmsnorm(h) -> qkv, o, residual + rmsnorm -> gate_up, down, residual + the next
+layer's rmsnorm -> qkv, the final norm -> lm_head. In this linear stack o reads the query
+columns of qkv where the attention output would be (same width, same dependency on qkv).
+Activations are resident in HBM.
 
-Two product paths run the chain: the single-call linears captured once in a HIP graph and
-replayed, and the decode-step executor (one cooperative launch for the whole chain).
+Two product paths run the linear stack: the single-call linears and norm kernels captured
+once in a HIP graph, and the decode-step executor (the whole chain, its residual + RMSNorm
+stages included, in one launch). ``decode_step`` times the real step with head norm + RoPE +
+KV-cache write and decode attention as well: the reference's own call sequence on the
+library (what Engine.generate runs), and executor launches split where attention sits.
 
 Prints one JSON line (the driver's contract). ``value`` is microseconds per step for
 the default workload, FP8 e4m3 W8A8 at M=1.
@@ -32,11 +35,18 @@ import torch  # noqa: E402
 
 PEAK_HBM = 8.0e12
 LAYERS = 36
+HIDDEN, EPS, THETA = 2560, 1e-6, 5e6
+#: Decode-step attention: the token at position CTX (a 512-token prompt) over
+#: caches of CAPACITY slots per sequence and KV head.
+CTX, CAPACITY = 512, 640
 PROJ = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
 LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
 #: Waves per executor workgroup.
 EXECUTOR_WAVES = 8
+#: Most tokens the executor's residual + RMSNorm input stages take (one pass over m x 2560
+#: values: m * 2560 <= 3 * 64 * 8 waves * 8).
+EXECUTOR_NORM_MAX_M = 4
 
 
 def log(*a):
@@ -57,97 +67,224 @@ def profiled_traffic(fmt, m, kernel="gate_up_swiglu"):
     return None
 
 
-class Stack:
-    """Quantized weights of every projection of the model, plus resident activations."""
+class Model:
+    """A Qwen3-4B-shaped decoder of one weight format: 36 layers of synthetic N(0, 0.02) weights
+    (qkv, o, gate_up, down) and the lm_head, each quantized and relaid through the reference's
+    own calls (``cuda_fp8.prepare(cuda_fp8.quantize(w, bits=..., fmt=...))``, engine.py:522-532);
+    RMSNorm weights 1 + 0.1 N(0, 1) (the reference's tests/test_engine.py:47-51); the hidden state
+    entering the step N(0, 1). With ``attention``, also the q/k head norms, bf16 RoPE tables
+    (theta 5e6) and per-layer bf16 KV caches holding ``ctx`` random keys and values, the step's
+    token at position ``ctx`` (a 512-token prompt)."""
 
-    def __init__(self, fmt, m, seed=0, layers=LAYERS):
-        from kernels import qlinear
-        self.fmt, self.m = fmt, m
-        self.quant, self.linear, _ = qlinear.FORMATS[fmt]
+    def __init__(self, fmt, m, seed=0, layers=LAYERS, attention=False, ctx=CTX, capacity=CAPACITY):
+        from kernels import cuda_fp8
+        self.fmt, self.m, self.layers = fmt, m, layers
+        bits = 4 if fmt == "w4a16" else 8
         gen = torch.Generator(device="cuda").manual_seed(seed)
-        self.calls = []  # (name, packed, k, swiglu)
-        for _ in range(layers):
-            for name, n, k in PROJ:
-                self.calls.append((name, self._make(gen, n, k), k, name == "gate_up"))
-        self.calls.append((LM_HEAD[0], self._make(gen, LM_HEAD[1], LM_HEAD[2]), LM_HEAD[2], False))
+
+        def weight(n, k):
+            w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+            prepared = cuda_fp8.prepare(cuda_fp8.quantize(w, bits=bits, fmt=fmt))
+            del w
+            return prepared
+
+        self.w = [{name: weight(n, k) for name, n, k in PROJ} for _ in range(layers)]
+        self.lm_head = weight(LM_HEAD[1], LM_HEAD[2])
+        #: (name, tiled weight, k, swiglu) of every projection, in step order
+        self.calls = [(name, self.w[i][name].tiles, k, name == "gate_up") for i in range(layers) for name, _, k in PROJ]
+        self.calls.append((LM_HEAD[0], self.lm_head.tiles, LM_HEAD[2], False))
+        ng = torch.Generator(device="cuda").manual_seed(seed + 2)
+        norm = lambda: (1.0 + 0.1 * torch.randn(HIDDEN, generator=ng, device="cuda")).to(torch.bfloat16)
+        self.norm_in = [norm() for _ in range(layers)]
+        self.norm_post = [norm() for _ in range(layers)]
+        self.norm_out = norm()
         xg = torch.Generator(device="cuda").manual_seed(seed + 1)
-        self.x = {k: torch.randn(m, k, generator=xg, device="cuda").to(torch.bfloat16)
-                  for k in (2560, 4096, 9728)}
+        self.h = torch.randn(m, HIDDEN, generator=xg, device="cuda").to(torch.bfloat16)
+        #: N(0, 1) activations of every input width (per-projection timings, the CPU baseline)
+        self.x = {k: torch.randn(m, k, generator=xg, device="cuda").to(torch.bfloat16) for k in (2560, 4096, 9728)}
+        self.attention = attention
+        if attention:
+            from kernels import DecodeAttention
+            head = lambda: torch.randn(128, generator=ng, device="cuda").to(torch.bfloat16)
+            self.q_norm = [head() for _ in range(layers)]
+            self.k_norm = [head() for _ in range(layers)]
+            inv = 1.0 / (THETA ** (torch.arange(0, 128, 2, dtype=torch.float32, device="cuda") / 128))
+            ang = torch.outer(torch.arange(capacity, dtype=torch.float32, device="cuda"), inv)
+            ang = torch.cat([ang, ang], dim=1)
+            self.cos, self.sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+            cg = torch.Generator(device="cuda").manual_seed(seed + 3)
+            self.k_cache = [torch.randn(m, 8, capacity, 128, generator=cg, device="cuda").to(torch.bfloat16)
+                            for _ in range(layers)]
+            self.v_cache = [torch.randn(m, 8, capacity, 128, generator=cg, device="cuda").to(torch.bfloat16)
+                            for _ in range(layers)]
+            self.positions = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+            self.attend = DecodeAttention(m, 8, 4, 128, capacity, "cuda")
         torch.cuda.synchronize()
 
-    def _make(self, gen, n, k):
-        from kernels import qlinear
-        w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-        packed = self.quant(w)
-        del w
-        return qlinear.prepare(packed, self.fmt)  # load-time relayout into MI355X tiles
+    # ---- the linear stack: every projection of a decode step, attention left out ----------
 
-    def run(self, which=None):
-        """``which`` = None: the whole chain, each projection reading its producer's output.
-        A projection name: every instance of it, on resident inputs (per-projection timing)."""
-        if which is not None:
-            for name, packed, k, sw in self.calls:
-                if name == which:
-                    self.linear(self.x[k], packed, swiglu=sw)
-            return
-        h = self.x[2560]
-        for name, packed, k, sw in self.calls:
-            if name == "qkv":
-                q = self.linear(h, packed)
-            elif name == "o":
-                q = self.linear(q[:, :4096].contiguous(), packed)
-            elif name == "gate_up":
-                q = self.linear(q, packed, swiglu=True)
-            else:  # down, lm_head
-                q = h = self.linear(h if name == "lm_head" else q, packed)
-
-    def executor(self, waves=EXECUTOR_WAVES, lanes=1):
-        """The same chain as one decode-step executor launch (outputs preallocated)."""
+    def linear_chain(self):
+        """The decode step's projections as one executor launch, with its residual adds and
+        RMSNorms as input stages (engine.py:866-918: rmsnorm(h) -> qkv, residual + o ->
+        rmsnorm -> gate_up, residual + down -> the next layer's rmsnorm -> qkv, the final norm ->
+        lm_head). o reads the query columns of qkv in place of the attention output (same width
+        and the same dependency on qkv). ``wiring`` records every projection's input."""
         from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m, waves=waves, groups_per_cu=lanes)
-        self.outs = []
-        h = self.x[2560]
-        q = None
-        for name, packed, k, sw in self.calls:
-            y = torch.empty((self.m, packed.rows // 2 if sw else packed.rows), dtype=torch.bfloat16, device="cuda")
-            x = {"qkv": h, "o": None if q is None else q[:, :4096], "gate_up": q, "down": q, "lm_head": h}[name]
-            chain.add(packed, x, y, swiglu=sw)
-            self.outs.append(y)
-            q = y
-            if name == "down":
-                h = y
-        return chain.build()
-
-    def norm_executor(self, eps=1e-6):
-        """The decode step with its residual adds and RMSNorms as input stages of the executor:
-        qkv <- rmsnorm(h), gate_up <- rmsnorm(h + o), the next qkv and the lm_head <-
-        rmsnorm(h + o + down) (FP8: the normed input quantized per token in the same stage)."""
-        from kernels.decode_stack import DecodeStack
-        chain = DecodeStack(self.fmt, self.m)
-        gen = torch.Generator(device="cuda").manual_seed(77)
+        chain = DecodeStack(self.fmt, self.m, waves=EXECUTOR_WAVES)
         new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
-        norm_w = lambda: (1.0 + 0.1 * torch.randn(2560, generator=gen, device="cuda")).to(torch.bfloat16)
-        self.norm_keep = []
-        resid, delta, q, h0 = self.x[2560], None, None, None
-        for name, packed, k, sw in self.calls:
-            y = new(packed.rows // 2 if sw else packed.rows)
-            if name in ("qkv", "lm_head"):
-                r_out, w = new(2560), norm_w()
-                chain.add_normed(packed, resid, y, w, eps, delta=delta, resid_out=r_out)
-                self.norm_keep += [r_out, w]
-                h0 = r_out
-            elif name == "gate_up":
-                r_out, w = new(2560), norm_w()
-                chain.add_normed(packed, h0, y, w, eps, delta=q, resid_out=r_out, swiglu=True)
-                self.norm_keep += [r_out, w]
+        self.outs, self.wiring = [], []
+        resid, delta, q = self.h, None, None
+        for i, (name, tiled, k, sw) in enumerate(self.calls):
+            layer = i // 4
+            y = new(tiled.rows // 2 if sw else tiled.rows)
+            if name in ("qkv", "lm_head", "gate_up"):
+                w = {"qkv": self.norm_in[min(layer, self.layers - 1)], "lm_head": self.norm_out,
+                     "gate_up": self.norm_post[min(layer, self.layers - 1)]}[name]
+                r_out = new(HIDDEN)
+                chain.add_normed(tiled, resid, y, w, EPS, delta=delta, resid_out=r_out, swiglu=sw)
+                self.wiring.append({"resid": resid, "delta": delta, "w": w, "resid_out": r_out})
                 resid = r_out
             else:
-                chain.add(packed, q[:, :4096] if name == "o" else q, y)
-                if name == "down":
-                    delta = y
-            self.norm_keep.append(y)
+                x = q[:, :4096] if name == "o" else q
+                chain.add(tiled, x, y)
+                self.wiring.append({"x": x})
+            if name in ("o", "down"):
+                delta = y
+            self.outs.append(y)
             q = y
         return chain.build()
+
+    def linear_step(self):
+        """The same chain as single calls (the library's linears and norm kernels), for a
+        graph: FP8 W8A8 takes the fused residual + RMSNorm + per-token quantize
+        (``qlinear.add_norm_quant_fp8``) in front of qkv, gate_up and the lm_head."""
+        from kernels import norm, qlinear
+        from kernels.cuda_small import rms_norm
+        linear = qlinear.FORMATS[self.fmt][1]
+        fp8 = self.fmt == "fp8"
+
+        def normed_linear(resid, delta, w, tiled, swiglu=False):
+            if fp8:
+                r, xq, sx = qlinear.add_norm_quant_fp8(resid, delta, w, EPS)
+                return (resid if r is None else r), qlinear.linear_fp8_w8a8_quantized(xq, sx, tiled, swiglu=swiglu)
+            if delta is None:
+                return resid, linear(rms_norm(resid, w, EPS), tiled, swiglu=swiglu)
+            r, x = norm.add_rms_norm(resid, delta, w, EPS)
+            return r, linear(x, tiled, swiglu=swiglu)
+
+        def step():
+            resid, delta = self.h, None
+            for i in range(self.layers):
+                w = self.w[i]
+                resid, qkv = normed_linear(resid, delta, self.norm_in[i], w["qkv"].tiles)
+                o = linear(qkv[:, :4096].contiguous(), w["o"].tiles)
+                resid, act = normed_linear(resid, o, self.norm_post[i], w["gate_up"].tiles, swiglu=True)
+                delta = linear(act, w["down"].tiles)
+            return normed_linear(resid, delta, self.norm_out, self.lm_head.tiles)[1]
+        return step
+
+    # ---- the real decode step: attention included -----------------------------------------
+
+    def engine_step(self):
+        """One decode step as the reference engine runs it (engine.py:866-918, 972-986), every
+        call through the reference's own signatures on this model's weights: rms_norm, then per
+        layer ``cuda_fp8.matmul`` (qkv), ``qkv_norm_rope_to_cache``, ``DecodeAttention``,
+        ``cuda_fp8.matmul_add_norm`` (o; up to 16 rows, else matmul + add_rms_norm),
+        ``cuda_fp8.gate_up_swiglu``, ``cuda_fp8.matmul_add_norm`` (down, into the next norm),
+        and ``cuda_fp8.matmul`` for the lm_head."""
+        from kernels import cuda_fp8, norm, qkv_norm_rope_to_cache
+        from kernels.cuda_small import rms_norm
+        fused = self.m <= 16
+        scratch = {n: cuda_fp8.add_norm_scratch(self.m, HIDDEN, "cuda") for n in ("o", "down")} if fused else None
+
+        def add_project_norm(name, src, prepared, resid, w):
+            if fused:
+                return cuda_fp8.matmul_add_norm(src, prepared, resid, w, EPS, scratch[name])
+            return norm.add_rms_norm(resid, cuda_fp8.matmul(src, prepared), w, EPS)
+
+        def step():
+            x = self.h
+            normed = rms_norm(x, self.norm_in[0], EPS)
+            for i in range(self.layers):
+                w = self.w[i]
+                qkv = cuda_fp8.matmul(normed, w["qkv"])
+                q = qkv_norm_rope_to_cache(qkv, 32, 8, self.q_norm[i], self.k_norm[i], self.cos, self.sin,
+                                           self.positions, 1, self.k_cache[i], self.v_cache[i], EPS)
+                att = self.attend(q, self.k_cache[i], self.v_cache[i], self.positions)
+                x, normed = add_project_norm("o", att, w["o"], x, self.norm_post[i])
+                inner = cuda_fp8.gate_up_swiglu(normed, w["gate_up"])
+                following = self.norm_in[i + 1] if i + 1 < self.layers else self.norm_out
+                x, normed = add_project_norm("down", inner, w["down"], x, following)
+            return cuda_fp8.matmul(normed, self.lm_head)
+        return step
+
+    def executor_step(self):
+        """The same decode step with its projections on the executor, split where attention
+        sits: one launch for rmsnorm -> qkv of layer 0, then per layer the head norm + RoPE +
+        cache write and attention, then one launch for o, rmsnorm -> gate_up, down and the next
+        layer's rmsnorm -> qkv (the last: the final norm -> lm_head). 37 executor launches and
+        36 x (rope, attention) in one graph."""
+        from kernels import qkv_norm_rope_to_cache
+        from kernels.decode_stack import DecodeStack
+        new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
+        self.seg_keep = []
+        qkv_out = [new(6144) for _ in range(self.layers)]
+        segments = []
+        chain = DecodeStack(self.fmt, self.m, waves=EXECUTOR_WAVES)
+        r0 = new(HIDDEN)
+        chain.add_normed(self.w[0]["qkv"].tiles, self.h, qkv_out[0], self.norm_in[0], EPS, resid_out=r0)
+        segments.append(chain.build())
+        resid = r0
+        for i in range(self.layers):
+            w = self.w[i]
+            chain = DecodeStack(self.fmt, self.m, waves=EXECUTOR_WAVES)
+            o, act, down, r1 = new(HIDDEN), new(9728), new(HIDDEN), new(HIDDEN)
+            chain.add(w["o"].tiles, self.attend.out, o)
+            chain.add_normed(w["gate_up"].tiles, resid, act, self.norm_post[i], EPS, delta=o, resid_out=r1,
+                             swiglu=True)
+            chain.add(w["down"].tiles, act, down)
+            r2 = new(HIDDEN)
+            if i + 1 < self.layers:
+                chain.add_normed(self.w[i + 1]["qkv"].tiles, r1, qkv_out[i + 1], self.norm_in[i + 1], EPS,
+                                 delta=down, resid_out=r2)
+            else:
+                self.logits = new(LM_HEAD[1])
+                chain.add_normed(self.lm_head.tiles, r1, self.logits, self.norm_out, EPS, delta=down, resid_out=r2)
+            segments.append(chain.build())
+            self.seg_keep += [o, act, down, r1, r2]
+            resid = r2
+        self.segments = segments
+
+        def step():
+            segments[0].run()
+            for i in range(self.layers):
+                q = qkv_norm_rope_to_cache(qkv_out[i], 32, 8, self.q_norm[i], self.k_norm[i], self.cos, self.sin,
+                                           self.positions, 1, self.k_cache[i], self.v_cache[i], EPS)
+                self.attend(q, self.k_cache[i], self.v_cache[i], self.positions)
+                segments[i + 1].run()
+        return step
+
+    def attention_only(self):
+        """The step's rope + attention calls alone (the same calls as in the steps above)."""
+        from kernels import qkv_norm_rope_to_cache
+        qkv = torch.randn(self.m, 6144, device="cuda").to(torch.bfloat16)
+
+        def step():
+            for i in range(self.layers):
+                q = qkv_norm_rope_to_cache(qkv, 32, 8, self.q_norm[i], self.k_norm[i], self.cos, self.sin,
+                                           self.positions, 1, self.k_cache[i], self.v_cache[i], EPS)
+                self.attend(q, self.k_cache[i], self.v_cache[i], self.positions)
+        return step
+
+    # ---- per projection --------------------------------------------------------------------
+
+    def run(self, which):
+        """Every instance of one projection, single calls on resident N(0, 1) inputs."""
+        from kernels import qlinear
+        linear = qlinear.FORMATS[self.fmt][1]
+        for name, tiled, k, sw in self.calls:
+            if name == which:
+                linear(self.x[k], tiled, swiglu=sw)
 
     def bytes_alg(self, which=None):
         """Algorithmic bytes: weight codes + scales + M*K*2 (x in) + M*N_out*2 (y out)."""
@@ -313,64 +450,108 @@ def time_fn(fn, reps, warmup, trials=5):
     return statistics.median(res)
 
 
-def measure_stack(fmt, m, steps, warmup, breakdown=True):
-    stack = Stack(fmt, m)
-    g = graph_of(stack.run)
-    ms_graph = median_graph_ms(g, steps, warmup)
+def timed_step(fn, steps, warmup):
+    """us per step of ``fn`` captured once in a HIP graph and replayed (median of 5 trials)."""
+    g = graph_of(fn)
+    us = median_graph_ms(g, steps, warmup) * 1e3
     del g
-    out = {"graph_us": ms_graph * 1e3}
-    if m <= 16:
-        # the same chain as one executor launch
-        try:
-            chain = stack.executor()
-        except ValueError as e:  # the builder's own limits (LDS, shapes): no such launch here
-            out["executor_unsupported"] = str(e)
-        else:
-            ms_exec = time_fn(chain.run, steps, warmup)
-            if chain.failed():
-                raise RuntimeError("decode executor: a wait gave up")
-            out["executor_us"] = ms_exec * 1e3
-            out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": chain.waves,
-                                      "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
-            del chain
-    if m <= 4:
-        # the full decode step's linear path with its residual adds and RMSNorms fused into the
-        # projections' input stages; not the headline, which is the linears alone
-        try:
-            chain = stack.norm_executor()
-        except ValueError as e:  # the builder's own limits
-            chain = None
-            out["norm_chain_unsupported"] = str(e)
-        if chain is not None:
-            ms_norm = time_fn(chain.run, steps, warmup)
-            if chain.failed():
-                raise RuntimeError("executor with norm stages: a wait gave up")
-            out["norm_chain_us"] = round(ms_norm * 1e3, 2)
-            del chain
-    cands = {"graph": ms_graph * 1e3, "executor": out.get("executor_us", 1e30)}
+    return us
+
+
+def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
+    """The decode-step linear stack of one format at batch m, by two product paths: the
+    executor (one launch, m <= 4: its norm stages make one pass over m x 2560 values) and a
+    graph of single calls; ``us`` is the faster. With ``decode_step``, also the real decode
+    step, attention included: through the reference's signatures (the path Engine.generate
+    runs) and, where the executor applies, executor launches split at attention."""
+    model = Model(fmt, m, attention=decode_step)
+    out = {"graph_us": timed_step(model.linear_step(), steps, warmup)}
+    if m <= EXECUTOR_NORM_MAX_M:
+        chain = model.linear_chain()
+        out["executor_us"] = timed_step(chain.run, steps, warmup)
+        if chain.failed():
+            raise RuntimeError("decode executor: a wait gave up")
+        out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": chain.waves,
+                                  "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
+        del chain
+    cands = {"graph": out["graph_us"], "executor": out.get("executor_us", 1e30)}
     out["path"] = min(cands, key=cands.get)
-    ms = cands[out["path"]] / 1e3
-    out.update({
-        "us": ms * 1e3,
-        "weight_GB": stack.weight_bytes() / 1e9,
-        "alg_GB": stack.bytes_alg() / 1e9,
-    })
-    out["effective_weight_GBps"] = stack.weight_bytes() / (ms * 1e-3) / 1e9
-    out["alg_GBps"] = stack.bytes_alg() / (ms * 1e-3) / 1e9
+    us = cands[out["path"]]
+    out.update({"us": us, "weight_GB": model.weight_bytes() / 1e9, "alg_GB": model.bytes_alg() / 1e9})
+    out["effective_weight_GBps"] = model.weight_bytes() / (us * 1e-6) / 1e9
+    out["alg_GBps"] = model.bytes_alg() / (us * 1e-6) / 1e9
     out["hbm_frac"] = out["alg_GBps"] * 1e9 / PEAK_HBM
+    if decode_step:
+        ds = {"engine_path_us": round(timed_step(model.engine_step(), steps, warmup), 2)}
+        if m <= EXECUTOR_NORM_MAX_M:
+            step = model.executor_step()
+            ds["executor_path_us"] = round(timed_step(step, steps, warmup), 2)
+            if any(seg.failed() for seg in model.segments):
+                raise RuntimeError("decode step executor: a wait gave up")
+            del step
+            model.segments = None
+        ds["rope_and_attention_alone_us"] = round(timed_step(model.attention_only(), steps, warmup), 2)
+        ds["context_keys"] = CTX + 1
+        out["decode_step"] = ds
     if breakdown:
         per = {}
         for name, _, _ in PROJ + [LM_HEAD]:
-            gp = graph_of(lambda: stack.run(name))
-            cnt = stack.count(name)
+            gp = graph_of(lambda: model.run(name))
+            cnt = model.count(name)
             reps = max(3, steps // 2) if name != "lm_head" else max(10, steps)
             t = median_graph_ms(gp, reps, 2, trials=3) / cnt
-            b = stack.bytes_alg(name) / cnt
+            b = model.bytes_alg(name) / cnt
             per[name] = {"us": round(t * 1e3, 2), "alg_MB": round(b / 1e6, 3),
                          "GBps": round(b / (t * 1e-3) / 1e9, 1)}
             del gp
         out["per_projection"] = per
-    return stack, out
+    return model, out
+
+
+def measure_config1(reps=20, cpu=True):
+    """the W8A16 GEMV of the down shape at M = 1 (K = 9728, N = 2560), its
+    inputs drawn exactly as specified -- one CPU generator seeded 0: W int8 randint(-127, 128),
+    then bf16 scales U(0.001, 0.02), then x bf16 N(0, 1) -- and copied to the GPU; timed as
+    single calls over 41 copies of the weight (1.02 GB, past the Infinity Cache) replayed as one
+    HIP graph; with the reference's torch CPU dequantize + matmul on the same inputs."""
+    import math
+    from kernels import qlinear
+    g = torch.Generator().manual_seed(0)
+    q = torch.randint(-127, 128, (2560, 9728), generator=g).to(torch.int8)
+    s = (torch.rand(2560, generator=g) * (0.02 - 0.001) + 0.001).to(torch.bfloat16)
+    x = torch.randn(1, 9728, generator=g).to(torch.bfloat16)
+    tiled = qlinear.prepare((q.cuda(), s.cuda()), "w8a16")
+    per = tiled.bytes_moved()
+    copies = math.ceil((1 << 30) / per)
+    ws = [tiled] + [qlinear.Tiled(tiled.weight.clone(), tiled.scale.clone(), tiled.rows, tiled.k, "w8a16")
+                    for _ in range(copies - 1)]
+    xd = x.cuda()
+
+    def run():
+        for w in ws:
+            qlinear.linear_w8a16(xd, w)
+    us = timed_step(run, reps, 2) / len(ws)
+    alg = per + 9728 * 2 + 2560 * 2
+    out = {"us": round(us, 2), "alg_bytes": alg, "GBps": round(alg / us / 1e3, 1),
+           "hbm_frac": round(alg / us / 1e3 / (PEAK_HBM / 1e9), 4),
+           "effective_weight_GBps": round(per / us / 1e3, 1), "weight_copies": len(ws)}
+    del ws
+    if cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import cpu_baseline as cb
+        runs = []
+        for _ in range(7):
+            t0 = time.perf_counter()
+            cb.matmul("w8a16", x, cb.DEQUANT["w8a16"](q, s))
+            runs.append(time.perf_counter() - t0)
+        cpu_us = statistics.median(runs[2:]) * 1e6
+        out["cpu_baseline"] = {"us": round(cpu_us, 1), "unit": "us per call", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": "torch CPU dequantize + matmul on the same inputs, median "
+                                                         "of 5 after 2"}
+    log(f"config 1 W8A16 GEMV down M=1: {us:.2f} us, {alg / us / 1e3:.0f} GB/s "
+        f"({100 * alg / us / 1e3 / (PEAK_HBM / 1e9):.1f} % of 8 TB/s)")
+    torch.cuda.empty_cache()
+    return out
 
 
 PEAK_BF16_MFMA = 2.5e15  # dense bf16 MFMA, MI355X
@@ -587,21 +768,24 @@ def main():
               flush=True)
         return
 
-    stack, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick)
+    model, head = measure_stack(args.workload, args.m, args.steps, args.warmup, breakdown=not args.quick,
+                                decode_step=not args.quick)
     log(f"{args.workload} M={args.m}: {head['us']:.1f} us/step ({head['path']}; graph {head['graph_us']:.1f}, "
         f"executor {head.get('executor_us', float('nan')):.1f}), "
         f"{head['effective_weight_GBps']:.0f} GB/s weights, {100 * head['hbm_frac']:.1f}% of 8 TB/s")
+    if "decode_step" in head:
+        log(f"{args.workload} M={args.m} decode step with attention: {head['decode_step']}")
 
     fmt_name = {'fp8': 'FmtFP8', 'w4a16': 'FmtW4', 'w8a16': 'FmtW8'}[args.workload]
     if head["path"] == "executor":
-        # The whole step is one launch of the executor: its algorithmic bytes over its time.
+        # The whole linear stack is one launch of the executor: its algorithmic bytes over its time.
         el = head["executor_launch"]
         kname = f"stack_kernel<{fmt_name}, {el['waves']}, {str(el['desc_lds']).lower()}, {str(el['pieces']).lower()}>"
         roofline = {
             "bound": "hbm", "achieved": round(head["alg_GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4),
             "traffic": profiled_traffic(args.workload, args.m, el["kind"]),
-            "kernel": f"{kname} (the whole chain, M={args.m})",
+            "kernel": f"{kname} (the whole linear stack with its norm stages, M={args.m})",
             "us_per_launch": round(head["us"], 2), "alg_MB_per_launch": round(head["alg_GB"] * 1e3, 3),
         }
     else:
@@ -609,9 +793,9 @@ def main():
         # averaged over its 36 launches in one graph.
         dom = head.get("per_projection", {}).get("gate_up")
         if dom is None:
-            gp = graph_of(lambda: stack.run("gate_up"))
-            t = median_graph_ms(gp, max(3, args.steps // 2), 2, trials=3) / stack.count("gate_up")
-            b = stack.bytes_alg("gate_up") / stack.count("gate_up")
+            gp = graph_of(lambda: model.run("gate_up"))
+            t = median_graph_ms(gp, max(3, args.steps // 2), 2, trials=3) / model.count("gate_up")
+            b = model.bytes_alg("gate_up") / model.count("gate_up")
             dom = {"us": t * 1e3, "alg_MB": b / 1e6, "GBps": b / (t * 1e-3) / 1e9}
         roofline = {
             "bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
@@ -626,32 +810,39 @@ def main():
     extra["stack_frac_of_stream_floor"] = round(head["alg_GBps"] / extra["stream_floor_GBps"], 4)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(stack)
+        cpu = cpu_baseline(model)
         log(f"cpu baseline {args.workload} M={args.m}: {cpu['value'] / 1e3:.1f} ms per step, matmul only "
             f"{cpu['matmul_only_us'] / 1e3:.1f} ms ({cpu['cores']} threads, {cpu['cpu_model']})")
-    del stack
+    del model
     torch.cuda.empty_cache()
     if not args.quick:
-        # BASELINE configs 2 and 3 per projection (single calls, 36 distinct weights per
-        # projection in one graph): FP8 W8A8 at M = 1, 8; W4A16 at M = 1, 4, 8 with the lm_head.
+        extra["config1_w8a16_gemv_down_m1"] = measure_config1(max(5, args.steps), cpu=not args.no_cpu)
+        # BASELINE configs 2, 3 and 5: the other formats and batches. Per projection (single
+        # calls, 36 distinct weights per projection in one graph): FP8 W8A8 at M = 1, 8; W4A16 at
+        # M = 1, 4, 8 with the lm_head. Stacks and decode steps: each format at batch 1 and 32.
         per_cfg = {"config2_fp8_w8a8": {}, "config3_w4a16": {}}
         if args.workload == "fp8" and args.m == 1 and "per_projection" in head:
             per_cfg["config2_fp8_w8a8"]["M1"] = head["per_projection"]
-        for fmt, m in (("w4a16", 1), ("w4a16", 4), ("fp8", 8), ("w4a16", 8)):
+        runs = [("w4a16", 1), ("w8a16", 1), ("w4a16", 4), ("fp8", 8), ("w4a16", 8),
+                ("fp8", 32), ("w4a16", 32), ("w8a16", 32)]
+        for fmt, m in runs:
             if (fmt, m) == (args.workload, args.m):
                 continue
-            st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=True)
-            per = res.pop("per_projection")
+            per_proj = fmt != "w8a16" and m <= 8
+            st, res = measure_stack(fmt, m, max(5, args.steps // 2), 2, breakdown=per_proj,
+                                    decode_step=m in (1, 32))
+            if per_proj:
+                per = res.pop("per_projection")
+                per_cfg["config2_fp8_w8a8" if fmt == "fp8" else "config3_w4a16"][f"M{m}"] = per
             if (fmt, m) == ("w4a16", 1) and not args.no_cpu:
                 res["cpu_baseline"] = cpu_baseline(st)
                 log(f"cpu baseline w4a16 M=1: {res['cpu_baseline']['value'] / 1e3:.1f} ms per step "
                     f"({res['cpu_baseline']['cores']} threads)")
-            per_cfg["config2_fp8_w8a8" if fmt == "fp8" else "config3_w4a16"][f"M{m}"] = per
             if m != 4:
                 extra[f"{fmt}_M{m}_stack"] = {k: (round(v, 4 if k == "hbm_frac" else 2) if isinstance(v, float) else v)
                                               for k, v in res.items()}
-            log(f"{fmt} M={m}: {res['us']:.1f} us/step, {100 * res['hbm_frac']:.1f}% of 8 TB/s; per projection "
-                + ", ".join(f"{n} {v['us']:.1f} us" for n, v in per.items()))
+            log(f"{fmt} M={m}: {res['us']:.1f} us/step ({res['path']}), {100 * res['hbm_frac']:.1f}% of 8 TB/s"
+                + (f"; decode step {res['decode_step']}" if "decode_step" in res else ""))
             del st
             torch.cuda.empty_cache()
         extra["per_projection_single_calls"] = per_cfg
@@ -671,18 +862,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {"fp8": "fp8e4m3", "w4a16": "int4xbf16", "w8a16": "int8xbf16"}[args.workload],
-        "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) activations)",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) hidden state, RMSNorm weights "
+                "1+0.1N(0,1))",
         "config": {
-            "workload": f"Qwen3-4B decode-step linear stack, {args.workload}, 36 layers x "
-                        f"(qkv, o, gate_up+SwiGLU, down) + lm_head, one dependent chain",
+            "workload": f"Qwen3-4B decode-step linear stack, {args.workload}: 36 layers x (rmsnorm -> qkv, o, "
+                        f"residual + rmsnorm -> gate_up+SwiGLU, down) + final norm -> lm_head, one dependent "
+                        f"chain; o reads the query columns of qkv where attention sits (the step with "
+                        f"attention: extra.decode_step)",
             "m": args.m, "hidden": 2560, "intermediate": 9728, "vocab": 151936, "layers": LAYERS,
             "weight_GB": round(head["weight_GB"], 4), "alg_GB": round(head["alg_GB"], 4),
             "path": head["path"],
         },
         "paths_us": {"graph_of_single_calls": round(head["graph_us"], 2),
-                     "executor": round(head["executor_us"], 2) if "executor_us" in head else None,
-                     # the step with its residual adds and RMSNorms fused into the input stages
-                     "executor_with_norm_stages": head.get("norm_chain_us")},
+                     "executor": round(head["executor_us"], 2) if "executor_us" in head else None},
+        "decode_step": head.get("decode_step"),
         "effective_weight_GBps": round(head["effective_weight_GBps"], 1),
         "hbm_frac": round(head["hbm_frac"], 4),
         "roofline": roofline,

@@ -1,9 +1,15 @@
-"""The chain bench.py times, checked: ``bench.Stack(fmt, 1).executor()`` -- 36 Qwen3-4B layers
-(qkv, o on the query columns of qkv, gate_up with the fused SwiGLU, down) and the 151936-row
-lm_head, 145 projections in one executor launch -- in FP8 W8A8 and W4A16 at M = 1.
+"""The chain bench.py times, checked: ``bench.Model(fmt, 1).linear_chain()`` -- 36 Qwen3-4B
+layers (rmsnorm -> qkv, o on the query columns of qkv, residual + rmsnorm -> gate_up with the
+fused SwiGLU, down, residual into the next layer's rmsnorm) and the final norm -> 151936-row
+lm_head, 145 projections and 73 residual + RMSNorm stages in one executor launch -- in FP8 W8A8
+and W4A16 at M = 1.
 
+* every stage's residual (written to its resid_out) bit-exact against the oracle's residual
+  add, on the chain's own residual and delta;
 * every one of the 145 outputs against the single-call linear on the executor's own input
-  (the input the chain published, read back), within one bf16 rounding step;
+  within one bf16 rounding step: a plain input read back, a normed input recomputed by the
+  oracle's RMSNorm (bit-exact with the stage, tests/test_gpu_norm_stages.py) from the chain's
+  own residual;
 * layers 0, 17 and 35 (all four projections) and 32 spread 16-row tiles of the lm_head against
   the CPU oracle at relative L2 <= 1e-2 (the north star's bound);
 * identical bits on a second run, and on a replay of the run captured in a HIP graph.
@@ -28,14 +34,27 @@ def bits16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def inputs_of(stack):
-    """The input tensor of every call of the chain, as Stack.executor wires them."""
-    xs, h, q = [], stack.x[2560], None
-    for (name, _, _, _), y in zip(stack.calls, stack.outs):
-        xs.append({"qkv": h, "o": None if q is None else q[:, :4096], "gate_up": q, "down": q, "lm_head": h}[name])
-        q = y
-        if name == "down":
-            h = y
+def dev_bits(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to("cuda")
+
+
+def inputs_of(model):
+    """The input of every projection of the chain: plain inputs as wired, normed inputs from the
+    oracle's residual add + RMSNorm of the chain's own residual and delta. Checks each stage's
+    residual output bit for bit on the way."""
+    xs = []
+    for i, wire in enumerate(model.wiring):
+        if "x" in wire:
+            xs.append(wire["x"])
+            continue
+        w = bits16(wire["w"])
+        if wire["delta"] is None:
+            r = bits16(wire["resid"])
+            normed = O.rms_norm(r, w, bench.EPS)
+        else:
+            r, normed = O.add_rms_norm(bits16(wire["resid"]), bits16(wire["delta"]), w, bench.EPS)
+        assert np.array_equal(bits16(wire["resid_out"]), r), (i, "residual")
+        xs.append(dev_bits(normed))
     return xs
 
 
@@ -55,8 +74,8 @@ def oracle_rows(fmt, tiled, x, rows=None):
 @pytest.mark.parametrize("fmt", ["fp8", "w4a16"])
 def test_bench_chain_matches_single_calls_and_oracle(fmt):
     print(f"bench chain {fmt}: building 36 layers + lm_head", flush=True)
-    stack = bench.Stack(fmt, 1)
-    chain = stack.executor()
+    stack = bench.Model(fmt, 1)
+    chain = stack.linear_chain()
     assert len(chain.calls) == 4 * bench.LAYERS + 1
     chain.run()
     torch.cuda.synchronize()
@@ -67,6 +86,7 @@ def test_bench_chain_matches_single_calls_and_oracle(fmt):
     assert not chain.failed(), chain.failed_waits()
     for i, (y, f) in enumerate(zip(stack.outs, first)):
         assert torch.equal(y, f), (fmt, i, "deterministic")
+        assert bool(torch.isfinite(y).all()), (fmt, i, "finite")
     # a captured run replays as a new run (the epoch advances on the device)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -82,6 +102,7 @@ def test_bench_chain_matches_single_calls_and_oracle(fmt):
 
     linear = qlinear.FORMATS[fmt][1]
     xs = inputs_of(stack)
+    print(f"bench chain {fmt}: 73 stage residuals bit-exact against the oracle", flush=True)
     worst = 0.0
     for i, ((name, tiled, k, sw), x, y) in enumerate(zip(stack.calls, xs, stack.outs)):
         want = linear(x.contiguous(), tiled, swiglu=sw).float()
