@@ -7,7 +7,7 @@
 // projections are 5-25 MB, so per-launch latency (launch, first loads, activation staging,
 // epilogue) costs as much as the weight stream itself.
 //
-// Here one cooperative launch runs the whole chain on `lanes` sets of workgroups, one
+// Here one launch runs the whole chain on `lanes` sets of workgroups, one
 // workgroup per CU in each; lane l runs projections l, l + lanes, ... so a CU works on
 // several projections at once and their memory latencies overlap.
 //   * Work: a projection's weight is cut into row blocks of rt tiles, each ns K steps long.
