@@ -464,8 +464,11 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     graph of single calls; ``us`` is the faster. With ``decode_step``, also the real decode
     step, attention included: through the reference's signatures (the path Engine.generate
     runs) and, where the executor applies, executor launches split at attention."""
+    from kernels import decode_tuning
     model = Model(fmt, m, attention=decode_step)
-    out = {"graph_us": timed_step(model.linear_step(), steps, warmup)}
+    single = model.linear_step()
+    out = {"graph_us": timed_step(single, steps, warmup)}
+    out["path"] = "graph"
     if m <= EXECUTOR_NORM_MAX_M:
         chain = model.linear_chain()
         out["executor_us"] = timed_step(chain.run, steps, warmup)
@@ -473,10 +476,12 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
             raise RuntimeError("decode executor: a wait gave up")
         out["executor_launch"] = {"kind": "stack", "grid": chain.grid, "lds": chain.lds, "waves": chain.waves,
                                   "desc_lds": chain.launch.desc_lds >= 0, "pieces": chain.launch.pieces != 0}
+        # the library's whole-step race picks the path (graph of single calls is the incumbent)
+        out["path"], race = decode_tuning.race_steps({"graph": single, "executor": chain.run}, "graph",
+                                                     rounds=5, replays=4)
+        out["race_ms"] = {k: round(v, 4) for k, v in race.items()}
         del chain
-    cands = {"graph": out["graph_us"], "executor": out.get("executor_us", 1e30)}
-    out["path"] = min(cands, key=cands.get)
-    us = cands[out["path"]]
+    us = out["executor_us"] if out["path"] == "executor" else out["graph_us"]
     out.update({"us": us, "weight_GB": model.weight_bytes() / 1e9, "alg_GB": model.bytes_alg() / 1e9})
     out["effective_weight_GBps"] = model.weight_bytes() / (us * 1e-6) / 1e9
     out["alg_GBps"] = model.bytes_alg() / (us * 1e-6) / 1e9

@@ -10,7 +10,7 @@ library ``libqlinear.so``; there is no CPU or Triton fallback, and ops raise if 
 library is missing or the tensors are not on the GPU.
 """
 
-from . import _lib, attention, cuda_fp8, cuda_int8, cuda_small, fp8, gemm, norm, qlinear, rope, swiglu, timing  # noqa: F401
+from . import _lib, attention, cuda_fp8, cuda_int8, cuda_small, decode_tuning, fp8, gemm, norm, qlinear, rope, swiglu, timing  # noqa: F401
 from .attention import DecodeAttention  # noqa: F401
 from .rope import (  # noqa: F401
     kv_norm_rope_to_cache, q_norm_rope, qkv_norm_rope_to_cache, qkv_planes_norm_rope_to_cache,

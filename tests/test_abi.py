@@ -298,3 +298,19 @@ def test_qkv_consumer_and_attention_contract_on_host():
     pos = torch.zeros(1, dtype=torch.int32)
     with pytest.raises(ValueError, match="GPU"):
         rope.q_norm_rope(qkv, 32, torch.ones(128, dtype=torch.bfloat16), cos, cos, pos, 1, 1e-6)
+
+
+def test_decode_tuning_mirrors_the_reference():
+    """kernels.decode_tuning keeps the reference's entry point (engine/kernels/decode_tuning.py:17)
+    and its conditions for not racing (checked on the host: no device work happens)."""
+    import inspect
+    import types
+    from kernels import decode_tuning
+    assert list(inspect.signature(decode_tuning.tune_output_projection).parameters)[0] == "engine"
+    base = dict(graph=object(), draft=False, batch=1, integer_mlp=False, families={"o": "fp8"},
+                partial_config={"o": (8, 4, 1, 1, 0)})
+    for change in (dict(graph=None), dict(draft=True), dict(batch=17), dict(integer_mlp=True),
+                   dict(families={"o": "bf16"}), dict(partial_config={})):
+        assert decode_tuning.tune_output_projection(types.SimpleNamespace(**{**base, **change})) is False
+    with pytest.raises(ValueError):
+        decode_tuning.race_steps({"a": lambda: None}, incumbent="b")

@@ -135,3 +135,48 @@ def test_matmul_add_norm_single_launch(kind, name):
             r_want, y_want = O.add_rms_norm(bits16(residual), delta, bits16(gain), 1e-6)
             assert np.array_equal(bits16(res), r_want), (kind, name, batch)
             assert np.array_equal(bits16(normed), y_want), (kind, name, batch)
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w8a16", "fp8"])
+@pytest.mark.parametrize("m", [1, 8, 17])
+def test_reference_signatures_on_north_star_weights(fmt, m):
+    """The engine's call sites (engine.py:881-906, 950-951) on north-star weights: weights from
+    ``cuda_fp8.prepare(cuda_fp8.quantize(w, bits, fmt=...))``, then ``cuda_fp8.matmul`` (o and
+    qkv), ``matmul_partials`` with the reference's split-K configs (planes summed in slice
+    order == the reduced matmul's fp32 sum within one bf16 rounding, ``splits`` = plane count)
+    and ``gate_up_swiglu`` (gate_up with the fused SwiGLU), each against the oracle's product at
+    rel-L2 <= 1e-2. 17 tokens take the skinny GEMM behind the same signatures."""
+    bits = 4 if fmt == "w4a16" else 8
+    for name in ("qkv", "o", "gate_up"):
+        print(f"reference signatures {fmt} {name} m={m}", flush=True)
+        n, k = QWEN[name]
+        w = weight(name, SEEDS[name] + 100)
+        packed = cuda_fp8.quantize(w, bits=bits, fmt=fmt)
+        prepared = cuda_fp8.prepare(packed)
+        assert prepared.bits == bits and prepared.k == k and prepared.rows == n
+        x = acts(m, k, 90 + m + len(name))
+        swiglu = name == "gate_up"
+        rows = sample_rows(n, swiglu)
+        want = oracle_rows(fmt, packed[:2], rows, bits16(x), swiglu)
+        if swiglu:
+            y = cuda_fp8.gate_up_swiglu(x.to(DEV), prepared, config=(8, 1, 1, 1, 0))
+            err = O.rel_l2(y.float().cpu().numpy()[:, rows], want)
+            assert tuple(y.shape) == (m, n // 2) and err <= 1e-2, (fmt, name, m, err)
+            continue
+        y = cuda_fp8.matmul(x.to(DEV), prepared, config=(8, 1))
+        err = O.rel_l2(y.float().cpu().numpy()[:, rows], want)
+        assert tuple(y.shape) == (m, n) and err <= 1e-2, (fmt, name, m, err)
+        if m > 16:
+            continue  # split-K planes are a decode-kernel output (B <= 16 here)
+        for config in ((8, 2, 1, 1, 0), (4, 4, 1, 1, 2), (8, 16, 1, 1, 2)):
+            planes = cuda_fp8.matmul_partials(x.to(DEV), prepared, config)
+            assert planes.dtype == torch.float32 and tuple(planes.shape[1:]) == (m, n)
+            assert planes.shape[0] == cuda_fp8.splits(prepared, m, config), (fmt, name, config)
+            total = planes[0].clone()
+            for p in planes[1:]:
+                total += p
+            err = O.rel_l2(total.cpu().numpy()[:, rows], want)
+            assert err <= 1e-2, (fmt, name, m, config, err)
+            diff = (total.bfloat16().float() - y.float()).abs()
+            tol = 2.0 ** -7 * y.float().abs() + 2.0 ** -9 * y.float().abs().amax(dim=1, keepdim=True)
+            assert bool((diff <= tol).all()), (fmt, name, m, config, "planes vs matmul")
