@@ -513,6 +513,34 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     return model, out
 
 
+def measure_projection(fmt, name, m, reps):
+    """Single calls of one Qwen3-4B projection in one format at batch m, over enough distinct
+    weights to cover >= 1 GiB (so the Infinity Cache serves none of them), replayed as one HIP
+    graph: us per call and algorithmic GB/s. For counter profiles of the decode kernel."""
+    import math
+    from kernels import qlinear
+    n, k = {nm: (nn, kk) for nm, nn, kk in PROJ + [LM_HEAD]}[name]
+    quant, linear, _ = qlinear.FORMATS[fmt]
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    first = qlinear.prepare(quant(w), fmt)
+    del w
+    per = first.bytes_moved()
+    ws = [first] + [qlinear.Tiled(first.weight.clone(), first.scale.clone(), n, k, fmt)
+                    for _ in range(math.ceil((1 << 30) / per) - 1)]
+    x = torch.randn(m, k, generator=gen, device="cuda").to(torch.bfloat16)
+    sw = name == "gate_up"
+
+    def run():
+        for t in ws:
+            linear(x, t, swiglu=sw)
+    us = timed_step(run, reps, 2) / len(ws)
+    alg = per + m * k * 2 + m * (n // 2 if sw else n) * 2
+    log(f"{fmt} {name} M={m}: {us:.2f} us per call, {alg / us / 1e3:.0f} GB/s ({len(ws)} weights)")
+    return {"fmt": fmt, "projection": name, "m": m, "us": round(us, 2), "alg_MB": round(alg / 1e6, 3),
+            "GBps": round(alg / us / 1e3, 1), "weights": len(ws)}
+
+
 def measure_config1(reps=20, cpu=True):
     """the W8A16 GEMV of the down shape at M = 1 (K = 9728, N = 2560), its
     inputs drawn exactly as specified -- one CPU generator seeded 0: W int8 randint(-127, 128),
@@ -748,6 +776,9 @@ def main():
     ap.add_argument("--only-attention", action="store_true",
                     help="only the QKV consumer and decode attention figures: one JSON line, for profiling "
                          "(not the driver's line)")
+    ap.add_argument("--only-projection", choices=[n for n, _, _ in PROJ] + [LM_HEAD[0]],
+                    help="only single calls of one projection (--workload, --m) over >= 1 GiB of distinct "
+                         "weights: one JSON line, for counter profiles (not the driver's line)")
     ap.add_argument("--only-reference-formats", action="store_true",
                     help="only the reference formats' cuda_fp8.matmul figures: one JSON line (not the driver's line)")
     args = ap.parse_args()
@@ -763,6 +794,10 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.only_config4:
         print(json.dumps({"config4_w4_gate_up_swiglu_down": measure_config4(max(3, args.steps // 4))}), flush=True)
+        return
+    if args.only_projection:
+        print(json.dumps({"single_calls": measure_projection(args.workload, args.only_projection, args.m,
+                                                             max(3, args.steps))}), flush=True)
         return
     if args.only_reference_formats:
         print(json.dumps({"reference_formats_cuda_fp8_matmul": measure_reference_formats(max(3, args.steps // 2))}),

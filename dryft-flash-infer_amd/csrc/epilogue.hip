@@ -33,8 +33,22 @@ residual_planes_kernel(const uint16_t* __restrict__ x, const float* __restrict__
   out[i] = f2bf(bf2f(x[i]) + round_bf(acc));
 }
 
+// Chunks of 8 values a thread of add_rms_norm_kernel loads at once (n <= 256 * 8 * 8 = 16384).
+constexpr int kNormChunks = 8;
+
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
 // delta: bf16 [rows][n] or (planes != null) fp32 planes [splits][rows][n]; res may be null
-// (plain rms_norm of x). One workgroup of 256 threads per row.
+// (plain rms_norm of x). One workgroup of 256 threads per row. When n % 8 == 0 every thread
+// issues all of its 16-byte loads (x, delta or each plane, w) before it uses any, so a row
+// costs one memory round trip per input rather than one per value a thread holds.
 __global__ void __launch_bounds__(256)
 add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
                     const float* __restrict__ planes, int splits, const uint16_t* __restrict__ w,
@@ -49,22 +63,87 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
   // Sum of squares in fp64: each square of a bf16 value is exact there and so is the sum of
   // a hidden row's worth, which makes the scale independent of the summation order.
   double ss = 0.0;
-  for (int c = threadIdx.x; c < n; c += 256) {
-    float r = bf2f(x[base + c]);
-    if (add) {
-      float d;
-      if (planes) {
-        d = 0.f;
-        for (int s = 0; s < splits; ++s) d += planes[(size_t)s * rows * n + base + c];
-        d = round_bf(d);
-      } else {
-        d = bf2f(delta[base + c]);
+  const bool vec = (n & 7) == 0;
+  if (vec) {
+    const int nc = n >> 3;
+    uint4 xv[kNormChunks], dv[kNormChunks];
+#pragma unroll
+    for (int u = 0; u < kNormChunks; ++u) {
+      const int c = threadIdx.x + u * 256;
+      if (c < nc) {
+        xv[u] = ld16(x + base + 8 * c);
+        if (delta) dv[u] = ld16(delta + base + 8 * c);
       }
-      r = round_bf(r + d);
-      if (res) res[base + c] = f2bf(r);
     }
-    rbuf[c] = r;
-    ss += (double)r * (double)r;
+    float d[kNormChunks][8];
+    if (planes) {  // slice-order fp32 sums, each slice's loads of every chunk issued together
+#pragma unroll
+      for (int u = 0; u < kNormChunks; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[u][i] = 0.f;
+      for (int sl = 0; sl < splits; ++sl) {
+        const float* pl = planes + (size_t)sl * rows * n + base;
+        u32x4 pv[kNormChunks][2];
+#pragma unroll
+        for (int u = 0; u < kNormChunks; ++u) {
+          const int c = threadIdx.x + u * 256;
+          if (c < nc) {
+            pv[u][0] = *reinterpret_cast<const u32x4*>(pl + 8 * c);
+            pv[u][1] = *reinterpret_cast<const u32x4*>(pl + 8 * c + 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kNormChunks; ++u) {
+          const int c = threadIdx.x + u * 256;
+          if (c < nc)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d[u][i] += __uint_as_float(pv[u][i >> 2][i & 3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kNormChunks; ++u) {
+      const int c = threadIdx.x + u * 256;
+      if (c >= nc) continue;
+      const uint32_t xs[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+      float r[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = bf2f((xs[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+      if (add) {
+        const uint32_t ds[4] = {dv[u].x, dv[u].y, dv[u].z, dv[u].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float dd = planes ? round_bf(d[u][i]) : bf2f((ds[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+          r[i] = round_bf(r[i] + dd);
+        }
+        if (res)
+          *reinterpret_cast<u32x4*>(res + base + 8 * c) =
+              u32x4{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        rbuf[8 * c + i] = r[i];
+        ss += (double)r[i] * (double)r[i];
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < n; c += 256) {
+      float r = bf2f(x[base + c]);
+      if (add) {
+        float d;
+        if (planes) {
+          d = 0.f;
+          for (int sl = 0; sl < splits; ++sl) d += planes[(size_t)sl * rows * n + base + c];
+          d = round_bf(d);
+        } else {
+          d = bf2f(delta[base + c]);
+        }
+        r = round_bf(r + d);
+        if (res) res[base + c] = f2bf(r);
+      }
+      rbuf[c] = r;
+      ss += (double)r * (double)r;
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -73,10 +152,35 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
   const double total = ((part[0] + part[1]) + part[2]) + part[3];
   // mean rounded to fp32, + eps and 1/sqrt in fp32, as torch's rsqrt(mean + eps)
   const float scale = 1.0f / sqrtf((float)(total / (double)n) + eps);
-  for (int c = threadIdx.x; c < n; c += 256) {
-    const float v = round_bf(round_bf(rbuf[c] * scale) * bf2f(w[c]));
-    rbuf[c] = v;
-    if (y) y[base + c] = f2bf(v);
+  if (vec) {
+    const int nc = n >> 3;
+    uint4 wv[kNormChunks];
+#pragma unroll
+    for (int u = 0; u < kNormChunks; ++u) {
+      const int c = threadIdx.x + u * 256;
+      if (c < nc) wv[u] = ld16(w + 8 * c);
+    }
+#pragma unroll
+    for (int u = 0; u < kNormChunks; ++u) {
+      const int c = threadIdx.x + u * 256;
+      if (c >= nc) continue;
+      const uint32_t ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[i] = round_bf(round_bf(rbuf[8 * c + i] * scale) * bf2f((ws[i >> 1] >> (16 * (i & 1))) & 0xffffu));
+        rbuf[8 * c + i] = v[i];
+      }
+      if (y)
+        *reinterpret_cast<u32x4*>(y + base + 8 * c) =
+            u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
+    }
+  } else {
+    for (int c = threadIdx.x; c < n; c += 256) {
+      const float v = round_bf(round_bf(rbuf[c] * scale) * bf2f(w[c]));
+      rbuf[c] = v;
+      if (y) y[base + c] = f2bf(v);
+    }
   }
   if (q8) {
     // FP8 per-token activation quantize of the normed row (every value is a bf16 value):

@@ -58,6 +58,8 @@ struct GemmArgs {
   int sc_stride;     // floats per staged scale row ([step*nsc + j][16*rt])
   int xb_stride;     // floats per token in xb ([m][sps*nsc])
   int tblocks;       // skinny GEMM: 2 = two 32-token blocks in one launch (else 0)
+  int off_red;       // persistent kernel: LDS offset of the waves' partial sums (apart from x)
+  int off_bt;        // persistent kernel: LDS offset of the code-bias totals [step][group][MT][16]
   int pm;            // skinny GEMM token blocks: rows of a K-slice plane (the whole batch)
   // Fused residual add + RMSNorm (qlx_linear_add_norm): y receives delta = bf16(x W^T)
   // with device-coherent stores; the workgroup that completes the last row block adds
@@ -242,11 +244,16 @@ struct FmtW4 {
     }
     return t4;
   }
-  template <int MT>
+  // BMODE 0: the code-bias chain runs with every step; 1: it runs and its totals go to the
+  // LDS table at a.off_bt ([step][group][MT][16 tokens]); 2: the totals are read back from that
+  // table instead (a persistent workgroup's later items: same activation, same steps). All
+  // rows of the bias chain's A operand are equal, so every row of its result is the same value.
+  template <int MT, int BMODE = 0>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int rowl) {
     const float* sc = reinterpret_cast<const float*>(lds + a.off_sc);
+    float* bt = reinterpret_cast<float*>(const_cast<char*>(lds) + a.off_bt);
     // The code bias: the same MFMA chain with every code at the bias, on the fragments the
     // step reads anyway -- bias_chain's value bit for bit (same operands, same order), with no
     // staging pass, barrier or LDS table before the first step.
@@ -269,7 +276,18 @@ struct FmtW4 {
         for (int mt = 0; mt < MT; ++mt) {
           const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
           tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
-          tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
+          if constexpr (BMODE < 2)
+            tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
+        }
+      }
+      const int bti = (srel * 2 + j) * MT * 16 + (lane & 15);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (BMODE == 1) {
+          if (lane < 16) bt[bti + mt * 16] = tb[mt][0];
+        } else if constexpr (BMODE == 2) {
+          const float v = bt[bti + mt * 16];
+          tb[mt] = f32x4{v, v, v, v};
         }
       }
       const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + (srel * 2 + j) * a.sc_stride + rowl);
@@ -313,10 +331,12 @@ struct FmtW8 {
     }
     return t4;
   }
-  template <int MT>
+  // BMODE as in FmtW4::compute (one bias total per step: [step][MT][16 tokens]).
+  template <int MT, int BMODE = 0>
   __device__ static void compute(f32x4 (&acc)[MT], const uint4* c, const char* lds,
                                  const GemmArgs& a, int srel, int lane, const int (&xoff)[MT],
                                  const int (&mrow)[MT], int) {
+    float* bt = reinterpret_cast<float*>(const_cast<char*>(lds) + a.off_bt);
     // The code bias as in FmtW4::compute: bias_chain's value bit for bit, from the same fragments.
     const uint4 avb = {0x43004300u, 0x43004300u, 0x43004300u, 0x43004300u};  // bf16 128
     f32x4 tmp[MT], tb[MT];
@@ -335,8 +355,19 @@ struct FmtW8 {
         for (int mt = 0; mt < MT; ++mt) {
           const uint4 bv = *reinterpret_cast<const uint4*>(lds + xoff[mt] + kb + t * 16);
           tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), tmp[mt], 0, 0, 0);
-          tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
+          if constexpr (BMODE < 2)
+            tb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(bv), tb[mt], 0, 0, 0);
         }
+      }
+    }
+    const int bti = srel * MT * 16 + (lane & 15);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (BMODE == 1) {
+        if (lane < 16) bt[bti + mt * 16] = tb[mt][0];
+      } else if constexpr (BMODE == 2) {
+        const float v = bt[bti + mt * 16];
+        tb[mt] = f32x4{v, v, v, v};
       }
     }
 #pragma unroll
@@ -1116,15 +1147,31 @@ __device__ __forceinline__ float swiglu_bf(float g, float u) {
 // Stage the activation (from xs), then stream the item's weight steps through the MFMAs into
 // acc. On return the weight buffer is free (the next item may be prefetched into it) and LDS
 // still holds what the epilogue needs.
-template <class F, int MT, int RW, int WAVES, class XS>
+// One K step of the wave's MFMA work; BMODE (formats with the fused code bias only) as in
+// FmtW4::compute.
+template <class F, int MT, int BMODE>
+__device__ __forceinline__ void compute_step(f32x4 (&acc)[MT], const uint4* c, const char* lds, const GemmArgs& a,
+                                             int srel, int lane, const int (&xoff)[MT], const int (&mrow)[MT],
+                                             int rowl) {
+  if constexpr (BMODE == 0)
+    F::template compute<MT>(acc, c, lds, a, srel, lane, xoff, mrow, rowl);
+  else
+    F::template compute<MT, BMODE>(acc, c, lds, a, srel, lane, xoff, mrow, rowl);
+}
+
+// Stage the item's activation slice (unless `stage_x` is false: a persistent workgroup's later
+// items find it in place) and scales, then run its steps. BMODE as in FmtW4::compute.
+template <class F, int MT, int RW, int WAVES, class XS, int BMODE = 0>
 __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char* lds, const Item<RW>& it,
-                                          uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS], f32x4 (&acc)[RW][MT]) {
+                                          uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS], f32x4 (&acc)[RW][MT],
+                                          bool stage_x = true) {
   constexpr int PF = PipeDepth<RW>::PF;
   const int lane = threadIdx.x & 63;
   const int tg = it.tg, step0 = it.step0, nst = it.nst, wt = it.wt, kwi = it.kwi, my = it.my;
 
   // ---- prologue
-  if constexpr (std::is_same<F, FmtFP8>::value) {
+  if (!stage_x) {
+  } else if constexpr (std::is_same<F, FmtFP8>::value) {
     bool pre = false;  // quantized beforehand: x holds e4m3 codes, xs the token scales
     if constexpr (std::is_same<XS, XPlain>::value) pre = a.xs != nullptr;
     if (pre)
@@ -1140,8 +1187,10 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
   stage_scales<F>(a, lds, tg, step0, nst);
   __syncthreads();
   if constexpr (needs_bias_totals<F>()) {
-    stage_bias<F, WAVES>(a, lds, nst);
-    __syncthreads();
+    if (stage_x) {
+      stage_bias<F, WAVES>(a, lds, nst);
+      __syncthreads();
+    }
   }
 
   // ---- main loop
@@ -1165,7 +1214,7 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
       const int srel = kwi + (j0 + p) * a.kw;
 #pragma unroll
       for (int r = 0; r < RW; ++r)
-        F::template compute<MT>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
+        compute_step<F, MT, BMODE>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
       // Refill the slot just consumed (same registers: no copies across the loop edge),
       // and keep the refill here rather than letting the scheduler sink it to the end.
       const int nxt = min(step0 + kwi + (j0 + p + PF) * a.kw, it.last);
@@ -1181,7 +1230,7 @@ __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char*
       const int srel = kwi + (j0 + p) * a.kw;
 #pragma unroll
       for (int r = 0; r < RW; ++r)
-        F::template compute<MT>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
+        compute_step<F, MT, BMODE>(acc[r], buf[p][r], lds, a, srel, lane, xoff, mrow, (wt * RW + r) * 16 + 4 * (lane >> 4));
     }
   }
 
@@ -1360,6 +1409,72 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   f32x4 acc[RW][MT];
   item_main<F, MT, RW, WAVES>(a, XPlain{}, lds, it, buf, acc);
   item_finish<F, MT, RW, WAVES, SW, AN>(a, lds, it, acc);
+}
+
+// Epilogue of the persistent kernel: the waves' sums go to their own LDS area (a.off_red), so
+// the staged activation stays for the workgroup's next item; bf16 or SwiGLU outputs (whole K,
+// whole 16-row tiles).
+template <class F, int MT, int RW, int WAVES, bool SW>
+__device__ __forceinline__ void persist_finish(const GemmArgs& a, char* lds, const Item<RW>& it,
+                                               const f32x4 (&acc)[RW][MT]) {
+  char* red = lds + a.off_red;
+  acc_to_lds<MT, RW>(red, acc, BlockTeam{}, false);  // the area's last readers passed a barrier since
+  constexpr int rows_out = SW ? 8 : 16;
+  const int per_tile = (rows_out / 2) * a.m;
+  const int total = a.rt * per_tile;
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int tl = idx / per_tile, rem = idx - tl * per_tile;
+    const int mm = rem / (rows_out / 2), nl = 2 * (rem - mm * (rows_out / 2));
+    const int tile = it.tg * a.rt + tl;
+    if (tile >= a.ntiles) continue;
+    if constexpr (SW) {
+      const float g0 = tile_value<F, MT, RW>(a, red, lds, tl, nl, mm);
+      const float u0 = tile_value<F, MT, RW>(a, red, lds, tl, nl + 8, mm);
+      const float g1 = tile_value<F, MT, RW>(a, red, lds, tl, nl + 1, mm);
+      const float u1 = tile_value<F, MT, RW>(a, red, lds, tl, nl + 9, mm);
+      store_pair(y, (size_t)mm * a.half + 8 * tile + nl, swiglu_bf(g0, u0), swiglu_bf(g1, u1));
+    } else {
+      const float v0 = tile_value<F, MT, RW>(a, red, lds, tl, nl, mm);
+      const float v1 = tile_value<F, MT, RW>(a, red, lds, tl, nl + 1, mm);
+      store_pair(y, (size_t)mm * a.n + 16 * tile + nl, v0, v1);
+    }
+  }
+}
+
+// A single call as a persistent launch: workgroup b takes row blocks b, b + grid, ... (whole
+// K). The activation (FP8: its codes and token scales) is staged once; the next row block's
+// first weight steps are issued before the current one's epilogue, so the weight stream does
+// not stop at row-block boundaries and no workgroup launch sits between them. Formats with the
+// fused code bias compute its totals on the first row block only (BMODE 1) and read them back
+// on the rest (BMODE 2): bit-identical sums, about half the MFMAs. The launch guarantees every
+// workgroup at least two row blocks, so each first row block is a whole one.
+template <class F, int MT, int RW, int WAVES, bool SW>
+__global__ void __launch_bounds__(WAVES * 64) gemm_persist_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  constexpr bool CACHE = std::is_same<F, FmtW4>::value || std::is_same<F, FmtW8>::value;
+  int tg = blockIdx.x;
+  Item<RW> it;
+  uint4 buf[PipeDepth<RW>::PF][RW][F::LOADS];
+  item_prefetch<F, RW>(a, tg, 0, it, buf);
+  f32x4 acc[RW][MT];
+  for (bool first = true;; first = false) {
+    if constexpr (CACHE) {
+      if (first)
+        item_main<F, MT, RW, WAVES, XPlain, 1>(a, XPlain{}, lds, it, buf, acc, true);
+      else
+        item_main<F, MT, RW, WAVES, XPlain, 2>(a, XPlain{}, lds, it, buf, acc, false);
+    } else {
+      item_main<F, MT, RW, WAVES, XPlain, 0>(a, XPlain{}, lds, it, buf, acc, first);
+    }
+    const int nt = tg + (int)gridDim.x;
+    const Item<RW> cur = it;
+    if (nt < a.tile_groups) item_prefetch<F, RW>(a, nt, 0, it, buf);
+    persist_finish<F, MT, RW, WAVES, SW>(a, lds, cur, acc);
+    if (nt >= a.tile_groups) break;
+    tg = nt;
+    __syncthreads();  // scales and partial sums are restaged for the next row block
+  }
 }
 
 }  // namespace qlx

@@ -80,12 +80,73 @@ hipError_t allow_lds(int lds) {
   return e;
 }
 
+// Persistent single calls (gemm_persist_kernel): workgroups per CU, or 0 where the format keeps
+// one workgroup per row block. Measured on the 151936-row lm_head at M = 1 (us per call over
+// 1 GiB of distinct weights): W4A16 54.5 as one workgroup per row block, 45.0 with one
+// persistent workgroup per CU, 45.9 with two; FP8 68.1 / 67.2 / 64.9; W8A16 70.8 / 72.6 /
+// 73.3 (before the bias-total cache).
+template <class F>
+constexpr int persist_per_cu() {
+  if constexpr (std::is_same<F, FmtW4>::value) return 1;
+  if constexpr (std::is_same<F, FmtFP8>::value) return 2;
+  return 0;
+}
+
+inline int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 0;
+  return cus[dev];
+}
+
+// Launch the persistent kernel when the call suits it: whole K (one slice), bf16 or SwiGLU
+// output, whole 16-row tiles, and at least two row blocks per workgroup. Returns false (nothing
+// launched) otherwise.
+template <class F, int MT, int RW, int WAVES>
+bool launch_persist(const GemmArgs& a, int lds, hipStream_t st, hipError_t* err) {
+  constexpr int wpc = persist_per_cu<F>();
+  if constexpr (wpc == 0) {
+    return false;
+  } else {
+    if (a.splits != 1 || a.an_counter || a.n % 16 || (a.mode != QLX_MODE_BF16 && a.mode != QLX_MODE_SWIGLU))
+      return false;
+    const int cus = device_cus();
+    const int grid = cus * wpc;
+    if (cus <= 0 || a.tile_groups < 2 * grid) return false;
+    constexpr int NJ = std::is_same<F, FmtW4>::value ? 2 : (std::is_same<F, FmtW8>::value ? 1 : 0);
+    GemmArgs b = a;
+    b.off_red = round16(lds);
+    b.off_bt = b.off_red + WAVES * RW * 16 * 16 * MT * 4;
+    const int total = b.off_bt + a.nsteps * NJ * MT * 16 * 4;
+    if (total > kLdsLimit) return false;
+    const void* fn = a.mode == QLX_MODE_SWIGLU
+                         ? reinterpret_cast<const void*>(&gemm_persist_kernel<F, MT, RW, WAVES, true>)
+                         : reinterpret_cast<const void*>(&gemm_persist_kernel<F, MT, RW, WAVES, false>);
+    static int allowed[2] = {64 * 1024, 64 * 1024};  // per instantiation: [SwiGLU]
+    int& ok = allowed[a.mode == QLX_MODE_SWIGLU];
+    if (total > ok) {
+      if ((*err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, total)) != hipSuccess)
+        return true;
+      ok = total;
+    }
+    if (a.mode == QLX_MODE_SWIGLU)
+      gemm_persist_kernel<F, MT, RW, WAVES, true><<<grid, WAVES * 64, total, st>>>(b);
+    else
+      gemm_persist_kernel<F, MT, RW, WAVES, false><<<grid, WAVES * 64, total, st>>>(b);
+    *err = hipGetLastError();
+    return true;
+  }
+}
+
 // AN_OK: this format's entry points include the fused add-norm (qlx_linear_add_norm), which
 // launches the AN instantiation when a.an_counter is set.
 template <class F, int MT, int RW, int WAVES, bool AN_OK>
 hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   const int grid = a.tile_groups * a.splits;
   hipError_t e;
+  if (launch_persist<F, MT, RW, WAVES>(a, lds, st, &e)) return e;
   if constexpr (AN_OK) {
     if (a.an_counter) {
       if ((e = allow_lds<F, MT, RW, WAVES, false, true>(lds)) != hipSuccess) return e;
