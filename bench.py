@@ -189,18 +189,25 @@ class Model:
         """One decode step as the reference engine runs it (engine.py:866-918, 972-986), every
         call through the reference's own signatures on this model's weights: rms_norm, then per
         layer ``cuda_fp8.matmul`` (qkv), ``qkv_norm_rope_to_cache``, ``DecodeAttention``,
-        ``cuda_fp8.matmul_add_norm`` (o; up to 16 rows, else matmul + add_rms_norm),
-        ``cuda_fp8.gate_up_swiglu``, ``cuda_fp8.matmul_add_norm`` (down, into the next norm),
-        and ``cuda_fp8.matmul`` for the lm_head."""
-        from kernels import cuda_fp8, norm, qkv_norm_rope_to_cache
+        ``cuda_fp8.matmul_add_norm`` or ``matmul`` + ``add_rms_norm`` for o (whichever a race of
+        whole captured steps picks, as the engine races them; only the latter past 16 rows),
+        ``cuda_fp8.gate_up_swiglu``, the same for down (into the next norm), and
+        ``cuda_fp8.matmul`` for the lm_head."""
+        from kernels import cuda_fp8, decode_tuning, norm, qkv_norm_rope_to_cache
         from kernels.cuda_small import rms_norm
-        fused = self.m <= 16
-        scratch = {n: cuda_fp8.add_norm_scratch(self.m, HIDDEN, "cuda") for n in ("o", "down")} if fused else None
+        scratch = {n: cuda_fp8.add_norm_scratch(self.m, HIDDEN, "cuda") for n in ("o", "down")}
+        fused = [False]
 
         def add_project_norm(name, src, prepared, resid, w):
-            if fused:
+            if fused[0]:
                 return cuda_fp8.matmul_add_norm(src, prepared, resid, w, EPS, scratch[name])
             return norm.add_rms_norm(resid, cuda_fp8.matmul(src, prepared), w, EPS)
+
+        def variant(use_fused):
+            def run():
+                fused[0] = use_fused  # read while the step is captured
+                step()
+            return run
 
         def step():
             x = self.h
@@ -216,7 +223,16 @@ class Model:
                 following = self.norm_in[i + 1] if i + 1 < self.layers else self.norm_out
                 x, normed = add_project_norm("down", inner, w["down"], x, following)
             return cuda_fp8.matmul(normed, self.lm_head)
-        return step
+
+        # The engine's choice for o and down (engine.py:881-918, its fused_out race): the fused
+        # GEMM + residual add + RMSNorm (up to 16 rows) or the GEMM and a separate add-norm,
+        # raced as whole captured steps.
+        if self.m > 16:
+            return variant(False)
+        choice, _ = decode_tuning.race_steps({"separate": variant(False), "fused": variant(True)}, "separate",
+                                             rounds=3, replays=2)
+        self.engine_choice = choice
+        return variant(choice == "fused")
 
     def executor_step(self):
         """The same decode step with its projections on the executor, split where attention
@@ -488,6 +504,7 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     out["hbm_frac"] = out["alg_GBps"] * 1e9 / PEAK_HBM
     if decode_step:
         ds = {"engine_path_us": round(timed_step(model.engine_step(), steps, warmup), 2)}
+        ds["engine_path_add_norm"] = getattr(model, "engine_choice", "separate")
         if m <= EXECUTOR_NORM_MAX_M:
             step = model.executor_step()
             ds["executor_path_us"] = round(timed_step(step, steps, warmup), 2)

@@ -1028,8 +1028,8 @@ __device__ __forceinline__ uint4 load8_plain(const uint16_t* p, size_t e) {
 // last row block: res = bf16(resid + delta), normed = bf16(bf16(res * rsqrt(mean res^2 + eps)) * w)
 // (the fused epilogue of engine/kernels/cuda_fp8.py:1339-1374 with the rounding of
 // engine/kernels/reference.py:19-28; the same arithmetic as qlx_add_rms_norm). Each token row
-// is taken by a group of G threads (a power of two), which reads it 8 values at a time in two
-// passes: the sum of squares (fp64, reduced over the group in a fixed order), then the outputs.
+// is taken by a group of G threads (a power of two), which reads it 8 values at a time: the sum
+// of squares (fp64, reduced over the group in a fixed order), then the outputs.
 __device__ __noinline__ void add_norm_tail(const GemmArgs& a) {
   __shared__ double s_part[16];
   const int tid = threadIdx.x;
@@ -1052,8 +1052,72 @@ __device__ __noinline__ void add_norm_tail(const GemmArgs& a) {
       r[e] = round_bf(bf2f(xb) + bf2f(db));
     }
   };
-  constexpr int U = 4;  // chunks in flight per thread
+  // Rows of up to kTailChunks chunks per thread (the hidden width at M <= 8) take one pass:
+  // delta, residual and norm weight are loaded together and kept in registers, so the tail is
+  // one memory round trip; wider rows stream twice.
+  constexpr int U = 4;  // chunks in flight per thread (two-pass rows)
+  constexpr int kTailChunks = 6;
   double ss = 0.0;
+  uint16_t* ro = reinterpret_cast<uint16_t*>(a.res_out);
+  uint16_t* yo = reinterpret_cast<uint16_t*>(a.normed);
+  auto row_total = [&](double part_ss) {
+    const int lanes = G < 64 ? G : 64;
+    for (int o = lanes >> 1; o > 0; o >>= 1) part_ss += __shfl_xor(part_ss, o, 64);
+    double total = part_ss;
+    if (G > 64) {  // a row spans G / 64 waves: their sums in wave order
+      const int wpg = G >> 6;
+      if ((tid & 63) == 0) s_part[tid >> 6] = part_ss;
+      __syncthreads();
+      total = 0.0;
+      if (live)
+        for (int w = 0; w < wpg; ++w) total += s_part[mm * wpg + w];
+    }
+    return total;
+  };
+  auto write_chunk = [&](int c, const float (&r)[8], uint4 w, float scale) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t rb[4], yb[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float w0 = bf2f(ws[e >> 1] & 0xffffu), w1 = bf2f(ws[e >> 1] >> 16);
+      rb[e >> 1] = bf16_pair(r[e], r[e + 1]);
+      yb[e >> 1] = bf16_pair(round_bf(round_bf(r[e] * scale) * w0), round_bf(round_bf(r[e + 1] * scale) * w1));
+    }
+    *gmem(reinterpret_cast<u32x4*>(ro + base + (size_t)c * 8)) = u32x4{rb[0], rb[1], rb[2], rb[3]};
+    *gmem(reinterpret_cast<u32x4*>(yo + base + (size_t)c * 8)) = u32x4{yb[0], yb[1], yb[2], yb[3]};
+  };
+  if (nch <= kTailChunks * G) {
+    uint4 d[kTailChunks], x[kTailChunks], w[kTailChunks];
+#pragma unroll
+    for (int u = 0; u < kTailChunks; ++u) {
+      const int c = gi + u * G;
+      if (live && c < nch) {
+        d[u] = load8_coherent(dl, base + (size_t)c * 8);
+        x[u] = load8_plain(xr, base + (size_t)c * 8);
+        w[u] = load8_plain(wn, (size_t)c * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTailChunks; ++u) {
+      if (live && gi + u * G < nch) {
+        float r[8];
+        residual(x[u], d[u], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (double)r[e] * (double)r[e];
+      }
+    }
+    const double total = row_total(ss);
+    const float scale = 1.0f / sqrtf((float)(total / (double)a.n) + a.eps);
+#pragma unroll
+    for (int u = 0; u < kTailChunks; ++u) {
+      if (live && gi + u * G < nch) {
+        float r[8];
+        residual(x[u], d[u], r);
+        write_chunk(gi + u * G, r, w[u], scale);
+      }
+    }
+    return;
+  }
   for (int c0 = gi; live && c0 < nch; c0 += U * G) {
     uint4 d[U], x[U];
 #pragma unroll
@@ -1074,21 +1138,9 @@ __device__ __noinline__ void add_norm_tail(const GemmArgs& a) {
       }
     }
   }
-  const int lanes = G < 64 ? G : 64;
-  for (int o = lanes >> 1; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  double total = ss;
-  if (G > 64) {  // a row spans G / 64 waves: their sums in wave order
-    const int wpg = G >> 6;
-    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
-    __syncthreads();
-    total = 0.0;
-    if (live)
-      for (int w = 0; w < wpg; ++w) total += s_part[mm * wpg + w];
-  }
+  const double total = row_total(ss);
   // mean rounded to fp32, + eps and 1/sqrt in fp32, as torch's rsqrt(mean + eps)
   const float scale = 1.0f / sqrtf((float)(total / (double)a.n) + a.eps);
-  uint16_t* ro = reinterpret_cast<uint16_t*>(a.res_out);
-  uint16_t* yo = reinterpret_cast<uint16_t*>(a.normed);
   for (int c0 = gi; live && c0 < nch; c0 += U * G) {
     uint4 d[U], x[U], w[U];
 #pragma unroll
@@ -1106,16 +1158,7 @@ __device__ __noinline__ void add_norm_tail(const GemmArgs& a) {
       if (c < nch) {
         float r[8];
         residual(x[u], d[u], r);
-        const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-        uint32_t rb[4], yb[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float w0 = bf2f(ws[e >> 1] & 0xffffu), w1 = bf2f(ws[e >> 1] >> 16);
-          rb[e >> 1] = bf16_pair(r[e], r[e + 1]);
-          yb[e >> 1] = bf16_pair(round_bf(round_bf(r[e] * scale) * w0), round_bf(round_bf(r[e + 1] * scale) * w1));
-        }
-        *gmem(reinterpret_cast<u32x4*>(ro + base + (size_t)c * 8)) = u32x4{rb[0], rb[1], rb[2], rb[3]};
-        *gmem(reinterpret_cast<u32x4*>(yo + base + (size_t)c * 8)) = u32x4{yb[0], yb[1], yb[2], yb[3]};
+        write_chunk(c, r, w[u], scale);
       }
     }
   }
