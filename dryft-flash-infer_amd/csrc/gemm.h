@@ -945,9 +945,16 @@ __device__ __forceinline__ void load_chunk(uint4 (&c)[F::LOADS], const GemmArgs&
   }
 }
 
-template <int RW>
+template <class F, int RW>
 struct PipeDepth {
   static constexpr int PF = RW == 1 ? 4 : 2;  // steps in flight per wave (each 2 KB for RW = 1)
+};
+// W4A16 at one tile per wave: 3 steps. Measured on single calls at M = 1 (us, 4 / 3 steps):
+// lm_head 45.5 / 43.4, gate_up 11.25 / 11.0, down 8.36 / 7.9, qkv 6.13 / 6.6 (2 steps: 45.4,
+// 11.4, 7.8, 6.3); its dequantization keeps more registers live per step than the 8-bit formats.
+template <>
+struct PipeDepth<FmtW4, 1> {
+  static constexpr int PF = 3;
 };
 
 // Per-wave state of one work item, fixed by item_prefetch: row block tg, steps
@@ -964,8 +971,8 @@ struct Item {
 template <class F, int RW>
 __device__ __forceinline__ void item_prefetch_range(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
                                                     Item<RW>& it,
-                                                    uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
-  constexpr int PF = PipeDepth<RW>::PF;
+                                                    uint4 (&buf)[PipeDepth<F, RW>::PF][RW][F::LOADS]) {
+  constexpr int PF = PipeDepth<F, RW>::PF;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   it.tg = tg;
   it.s = s;
@@ -991,7 +998,7 @@ __device__ __forceinline__ void item_prefetch_range(const GemmArgs& a, int tg, i
 // Work item (tg, s) of a launch whose row blocks are cut into a.splits equal K slices.
 template <class F, int RW>
 __device__ __forceinline__ void item_prefetch(const GemmArgs& a, int tg, int s, Item<RW>& it,
-                                              uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS]) {
+                                              uint4 (&buf)[PipeDepth<F, RW>::PF][RW][F::LOADS]) {
   const int step0 = s * a.sps;
   item_prefetch_range<F, RW>(a, tg, step0, min(a.nsteps, step0 + a.sps) - step0, s, a.splits, it, buf);
 }
@@ -1206,9 +1213,9 @@ __device__ __forceinline__ void compute_step(f32x4 (&acc)[MT], const uint4* c, c
 // items find it in place) and scales, then run its steps. BMODE as in FmtW4::compute.
 template <class F, int MT, int RW, int WAVES, class XS, int BMODE = 0>
 __device__ __forceinline__ void item_main(const GemmArgs& a, const XS& xs, char* lds, const Item<RW>& it,
-                                          uint4 (&buf)[PipeDepth<RW>::PF][RW][F::LOADS], f32x4 (&acc)[RW][MT],
+                                          uint4 (&buf)[PipeDepth<F, RW>::PF][RW][F::LOADS], f32x4 (&acc)[RW][MT],
                                           bool stage_x = true) {
-  constexpr int PF = PipeDepth<RW>::PF;
+  constexpr int PF = PipeDepth<F, RW>::PF;
   const int lane = threadIdx.x & 63;
   const int tg = it.tg, step0 = it.step0, nst = it.nst, wt = it.wt, kwi = it.kwi, my = it.my;
 
@@ -1447,7 +1454,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_kernel(GemmArgs a) {
   int tg, s;
   block_coords(a, blockIdx.x, tg, s);
   Item<RW> it;
-  uint4 buf[PipeDepth<RW>::PF][RW][F::LOADS];
+  uint4 buf[PipeDepth<F, RW>::PF][RW][F::LOADS];
   item_prefetch<F, RW>(a, tg, s, it, buf);
   f32x4 acc[RW][MT];
   item_main<F, MT, RW, WAVES>(a, XPlain{}, lds, it, buf, acc);
@@ -1498,7 +1505,7 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_persist_kernel(GemmArgs a) {
   constexpr bool CACHE = std::is_same<F, FmtW4>::value || std::is_same<F, FmtW8>::value;
   int tg = blockIdx.x;
   Item<RW> it;
-  uint4 buf[PipeDepth<RW>::PF][RW][F::LOADS];
+  uint4 buf[PipeDepth<F, RW>::PF][RW][F::LOADS];
   item_prefetch<F, RW>(a, tg, 0, it, buf);
   f32x4 acc[RW][MT];
   for (bool first = true;; first = false) {
