@@ -118,7 +118,10 @@ class Model:
             self.v_cache = [torch.randn(m, 8, capacity, 128, generator=cg, device="cuda").to(torch.bfloat16)
                             for _ in range(layers)]
             self.positions = torch.tensor([ctx], dtype=torch.int32, device="cuda")
-            self.attend = DecodeAttention(m, 8, 4, 128, capacity, "cuda")
+            # planned, then raced over the split counts at both ends of generation before the
+            # step is captured, as the engine does (engine.py:840-845)
+            self.attend = DecodeAttention(m, 8, 4, 128, capacity, "cuda").tuned(
+                self.k_cache, self.v_cache, ctx, capacity - 1)
         torch.cuda.synchronize()
 
     # ---- the linear stack: every projection of a decode step, attention left out ----------
@@ -505,6 +508,7 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     if decode_step:
         ds = {"engine_path_us": round(timed_step(model.engine_step(), steps, warmup), 2)}
         ds["engine_path_add_norm"] = getattr(model, "engine_choice", "separate")
+        ds["attention_splits"] = model.attend.splits
         if m <= EXECUTOR_NORM_MAX_M:
             step = model.executor_step()
             ds["executor_path_us"] = round(timed_step(step, steps, warmup), 2)
