@@ -520,16 +520,13 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
         ds["context_keys"] = CTX + 1
         out["decode_step"] = ds
     if breakdown:
+        # single calls of each projection over >= 1 GiB of distinct weights (the Infinity Cache
+        # serves none of them)
         per = {}
         for name, _, _ in PROJ + [LM_HEAD]:
-            gp = graph_of(lambda: model.run(name))
-            cnt = model.count(name)
-            reps = max(3, steps // 2) if name != "lm_head" else max(10, steps)
-            t = median_graph_ms(gp, reps, 2, trials=3) / cnt
-            b = model.bytes_alg(name) / cnt
-            per[name] = {"us": round(t * 1e3, 2), "alg_MB": round(b / 1e6, 3),
-                         "GBps": round(b / (t * 1e-3) / 1e9, 1)}
-            del gp
+            r = measure_projection(fmt, name, m, max(3, steps // 2))
+            per[name] = {"us": r["us"], "alg_MB": r["alg_MB"], "GBps": r["GBps"]}
+            torch.cuda.empty_cache()
         out["per_projection"] = per
     return model, out
 
