@@ -44,9 +44,9 @@ LM_HEAD = ("lm_head", 151936, 2560)
 METRIC = "µs per decode-step linear stack + effective weight GB/s (% HBM peak), M=1"
 #: Waves per executor workgroup.
 EXECUTOR_WAVES = 8
-#: Most tokens the executor's residual + RMSNorm input stages take (one pass over m x 2560
-#: values: m * 2560 <= 3 * 64 * 8 waves * 8).
-EXECUTOR_NORM_MAX_M = 4
+#: Most tokens the decode executor takes (its residual + RMSNorm input stages run in passes
+#: of whole token rows).
+EXECUTOR_NORM_MAX_M = 16
 
 
 def log(*a):
@@ -479,8 +479,8 @@ def timed_step(fn, steps, warmup):
 
 def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     """The decode-step linear stack of one format at batch m, by two product paths: the
-    executor (one launch, m <= 4: its norm stages make one pass over m x 2560 values) and a
-    graph of single calls; ``us`` is the faster. With ``decode_step``, also the real decode
+    executor (one launch, m <= 16) and a graph of single calls; ``us`` is the path the
+    library's whole-step race picks. With ``decode_step``, also the real decode
     step, attention included: through the reference's signatures (the path Engine.generate
     runs) and, where the executor applies, executor launches split at attention."""
     from kernels import decode_tuning

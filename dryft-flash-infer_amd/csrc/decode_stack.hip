@@ -364,9 +364,16 @@ __device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs
   }
 }
 
-// Chunks of 8 values each thread holds through a norm stage: the stage is one pass over its
-// rows (m * k / 8 <= kNormU * threads, checked on the host).
+// Chunks of 8 values each thread holds through a pass of a norm stage. A pass takes as many
+// whole token rows as fit (k / 8 <= kNormU * threads, checked on the host); more tokens take
+// more passes.
 constexpr int kNormU = 3;
+
+// Token rows one pass of a norm stage takes.
+__host__ __device__ inline int norm_pass_tokens(int m, int k, int u, int threads) {
+  const int t = (u * threads) / (k >> 3);
+  return t < m ? t : m;
+}
 
 // Residual add + RMSNorm input stage of an item (see StackDesc.nw): every workgroup with work in
 // the projection computes r and the normed input from the same words in the same order -- the
@@ -374,14 +381,15 @@ constexpr int kNormU = 3;
 // lanes in a fixed tree; mean rounded to fp32, scale = 1 / sqrt(mean + eps) in fp32; input
 // bf16(bf16(r * scale) * w) (norm.py:53-80, reference.py:13-28) -- and stages its slice of that
 // input like any activation (FP8: quantized per token over the whole normed row). The owner
-// (row block 0) also writes r and the input and publishes r. `css` holds m * k / 8 + 16 doubles.
+// (row block 0) also writes r and the input and publishes r. Tokens t0 .. t0 + tn - 1 (one
+// pass); `css` holds tn * k / 8 + 16 doubles.
 template <class F, int U>
-__device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
-                                           double* css, bool owner, const Waits& w) {
+__device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
+                                                double* css, bool owner, const Waits& w, int t0, int tn) {
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const GemmArgs& a = d.a;
   const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
-  const int cpr = a.k >> 3, total = a.m * cpr;
+  const int cpr = a.k >> 3, total = tn * cpr;
   const bool has_delta = d.xwire != nullptr, rwire = d.rwire != nullptr;
   const XWire dx(has_delta ? d.xwire : nullptr, has_delta ? d.xpitch : 0, a.m, w);
   const XWire rx(rwire ? d.rwire : nullptr, rwire ? a.k : 0, a.m, w);
@@ -389,6 +397,7 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
     const int q = tid + u * nthr;
     mm = q / cpr;
     kabs = (q - mm * cpr) * 8;
+    mm += t0;
     return q < total;
   };
   XWire::Raw rd[U], rr[U];
@@ -440,7 +449,7 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
   }
   __syncthreads();
   double* tot = css + total;
-  for (int t = tid >> 6; t < a.m; t += nthr >> 6) {  // token t's total, by one wave
+  for (int t = tid >> 6; t < tn; t += nthr >> 6) {  // token t0 + t's total, by one wave
     double sum = 0.0;
     for (int c = lane; c < cpr; c += 64) sum += css[t * cpr + c];
 #pragma unroll
@@ -451,7 +460,7 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
   // The normed input of chunk u (and its largest magnitude): mean rounded to fp32, + eps and
   // 1/sqrt in fp32, as torch's rsqrt(mean + eps).
   auto normed_chunk = [&](int u, int mm, float& mx) {
-    const float scale = 1.0f / sqrtf((float)(tot[mm] / (double)a.k) + d.eps);
+    const float scale = 1.0f / sqrtf((float)(tot[mm - t0] / (double)a.k) + d.eps);
     const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
     uint32_t o[4];
     mx = 0.f;
@@ -496,7 +505,7 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
     __syncthreads();
     float* sx = reinterpret_cast<float*>(lds + a.off_sx);
     auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
-    for (int i = tid; i < a.m; i += nthr) sx[i] = token_scale(i);
+    for (int i = tid; i < tn; i += nthr) sx[t0 + i] = token_scale(t0 + i);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int mm, kabs;
@@ -507,6 +516,19 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
           store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, normed_chunk(u, mm, mx), token_scale(mm));
       }
     }
+  }
+}
+
+
+// The whole stage: its token rows in passes of norm_pass_tokens (one pass at M = 1..4 with
+// k = 2560 and 8 waves). A pass's LDS sums are reused by the next after a barrier.
+template <class F, int U>
+__device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
+                                           double* css, bool owner, const Waits& w) {
+  const int tpp = norm_pass_tokens(d.a.m, d.a.k, U, blockDim.x);
+  for (int t0 = 0; t0 < d.a.m; t0 += tpp) {
+    if (t0) __syncthreads();
+    stage_norm_pass<F, U>(d, lds, step0, nst, amax, css, owner, w, t0, min(tpp, d.a.m - t0));
   }
 }
 
@@ -1018,10 +1040,10 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
                 "projection %d: NULL pointer (x must be NULL exactly when the input is a norm stage)", c);
     if (normed(c)) {
       QLX_REQUIRE(norms[c].resid != nullptr, "projection %d: a norm stage needs its residual", c);
-      QLX_REQUIRE(m * (q.k / 8) <= kNormU * waves * 64,
-                  "projection %d: a norm stage takes m * k <= %d (one pass; m=%d, k=%d)", c, kNormU * waves * 64 * 8,
-                  m, q.k);
-      css_doubles = std::max(css_doubles, m * (q.k / 8) + 16);
+      QLX_REQUIRE(q.k / 8 <= kNormU * waves * 64,
+                  "projection %d: a norm stage takes k <= %d (one token row per pass; k=%d)", c, kNormU * waves * 64 * 8,
+                  q.k);
+      css_doubles = std::max(css_doubles, norm_pass_tokens(m, q.k, kNormU, waves * 64) * (q.k / 8) + 16);
     }
   }
   auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };

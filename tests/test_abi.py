@@ -229,10 +229,14 @@ def test_norm_stage_contract_on_host():
     # a residual the chain writes
     bad_resid = _lib.NormInput(1 << 35, None, NW, None, None, 1e-6, 0)
     assert build(1, [first, normed], [plain, bad_resid]) == _lib.QLX_EINVAL and "residual" in _lib.last_error()
-    # m * k beyond one staging pass (3 chunks of 8 per thread of 8 waves: m <= 4 at k = 2560)
-    assert build(5, [first, normed], [plain, good]) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
-    # ... and at 4 waves per workgroup already m = 3 is beyond it (3 * 4 * 64 * 8 = 6144 < 3 * 2560)
-    assert build(3, [first, normed], [plain, good], waves=4) == _lib.QLX_EINVAL and "norm stage" in _lib.last_error()
+    # a token row beyond one staging pass (3 chunks of 8 per thread: k <= 12288 at 8 waves, 6144 at 4)
+    wide = _lib.StackCall(W, S, 1 << 34, 1 << 35, 6400, 6400, _lib.MODE_BF16, 0)   # y = 1 << 35, 6400 wide
+    wide_normed = _lib.StackCall(W, S, None, 1 << 36, 256, 6400, _lib.MODE_BF16, 0)
+    assert build(1, [wide, wide_normed], [plain, good], waves=4) == _lib.QLX_EINVAL
+    assert "norm stage" in _lib.last_error()
+    # many token rows are fine (several passes), so these pass every host check
+    for m, waves in ((5, 8), (16, 8), (3, 4)):
+        assert build(m, [first, normed], [plain, good], waves=waves) != _lib.QLX_EINVAL, _lib.last_error()
     # Two layers that reuse one resid_out buffer (separate outputs y): two stages would write the
     # same residual and a later stage could not tell which one it reads.
     H0, H1 = 1 << 38, 1 << 39

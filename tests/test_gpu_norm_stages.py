@@ -18,12 +18,12 @@ from test_gpu_decode_stack import DEV, bits16, oracle_check, rand
 pytestmark = pytest.mark.gpu
 
 
-def build_norm_chain(fmt, m, seed, layers=2):
+def build_norm_chain(fmt, m, seed, layers=2, waves=8):
     """`layers` Qwen3-4B layers with their residual adds and RMSNorms inside the chain, then a
     final norm into a small head: qkv <- rmsnorm(h); o; gate_up <- rmsnorm(h + o); down; the next
     qkv <- rmsnorm(h + o + down); ..."""
     quant = qlinear.FORMATS[fmt][0]
-    chain = DecodeStack(fmt, m)
+    chain = DecodeStack(fmt, m, waves=waves)
     bufs = {"h_in": rand((m, 2560), seed).to(DEV)}
     weights, raw, stages = {}, {}, []
     eps = 1e-6
@@ -65,15 +65,18 @@ def build_norm_chain(fmt, m, seed, layers=2):
     return chain, bufs, weights, raw, stages
 
 
-@pytest.mark.parametrize("fmt,m", [("fp8", 1), ("w4a16", 1), ("w8a16", 1), ("fp8", 2), ("w4a16", 3), ("fp8", 4)])
-def test_decode_layers_with_residual_and_norm(fmt, m):
+@pytest.mark.parametrize("fmt,m,waves", [("fp8", 1, 8), ("w4a16", 1, 8), ("w8a16", 1, 8), ("fp8", 2, 8),
+                                         ("w4a16", 3, 8), ("fp8", 4, 8), ("w4a16", 8, 8), ("fp8", 8, 8),
+                                         ("w8a16", 16, 8), ("fp8", 16, 8), ("fp8", 3, 4), ("w4a16", 5, 4)])
+def test_decode_layers_with_residual_and_norm(fmt, m, waves):
     """Residual add + RMSNorm (+ FP8 per-token quantize) as input stages of the executor (one
-    chunk per thread at M = 1, three from M = 2 at k = 2560): every stage's residual and normed
-    input are bit-exact against the oracle on the chain's own inputs, every projection agrees
-    with the single-call linear on its stage's normed input (and o / down with the oracle), and
-    two runs are bitwise equal."""
-    print(f"norm chain {fmt} m={m}", flush=True)
-    chain, bufs, weights, raw, stages = build_norm_chain(fmt, m, 700 + m)
+    chunk per thread at M = 1, three from M = 2 at k = 2560; past four token rows per pass --
+    M > 4 at 8 waves, M > 2 at 4 -- in several passes of whole token rows): every stage's
+    residual and normed input are bit-exact against the oracle on the chain's own inputs, every
+    projection agrees with the single-call linear on its stage's normed input (and o / down with
+    the oracle), and two runs are bitwise equal."""
+    print(f"norm chain {fmt} m={m} waves={waves}", flush=True)
+    chain, bufs, weights, raw, stages = build_norm_chain(fmt, m, 700 + m, waves=waves)
     linear = qlinear.FORMATS[fmt][1]
     for run in range(2):
         if run:
