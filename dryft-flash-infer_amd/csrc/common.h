@@ -145,6 +145,43 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Lane values moved by one DPP pattern; lanes without a source (or in rows the row mask
+// leaves out) read 0. DPP moves cost no LDS round trip, unlike the shuffles above.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROWS, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROWS, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
+
+// Sum (fp64) and maximum (fp32, of values >= 0) of the 64 lanes, valid in lane 63: inclusive
+// prefix sums within rows of 16 (row_shr 1, 2, 4, 8), then lane 15 of rows 0 and 2 into rows 1
+// and 3 (row_bcast:15), then lane 31 into rows 2 and 3 (row_bcast:31). A fixed order: the
+// same inputs give the same bits.
+__device__ __forceinline__ double wave_sum_last(double v) {
+  v += dpp_f64<0x111, 0xf>(v);
+  v += dpp_f64<0x112, 0xf>(v);
+  v += dpp_f64<0x114, 0xf>(v);
+  v += dpp_f64<0x118, 0xf>(v);
+  v += dpp_f64<0x142, 0xa>(v);
+  v += dpp_f64<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ float wave_max_last(float v) {
+  v = fmaxf(v, dpp_f32<0x111, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x112, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x114, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x118, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x142, 0xa>(v));
+  v = fmaxf(v, dpp_f32<0x143, 0xc>(v));
+  return v;
+}
+
 // ---- error reporting --------------------------------------------------------------------
 
 void set_error(const char* fmt, ...);

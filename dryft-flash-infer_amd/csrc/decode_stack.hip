@@ -364,66 +364,84 @@ __device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs
   }
 }
 
-// Chunks of 8 values each thread holds through a pass of a norm stage. A pass takes as many
-// whole token rows as fit (k / 8 <= kNormU * threads, checked on the host); more tokens take
-// more passes.
+// Chunks of 8 values each thread holds through a pass of a norm stage. A token row's chunks
+// take norm_row_slots(k) slots (k / 8 rounded up to whole waves, so the 64 slots of a wave in
+// one round belong to one token); a pass takes as many whole rows as fit kNormU slots per
+// thread (one row at least, checked on the host); more tokens take more passes.
 constexpr int kNormU = 3;
+__host__ __device__ inline int norm_row_slots(int k) { return ((k >> 3) + 63) & ~63; }
 
 // Token rows one pass of a norm stage takes.
 __host__ __device__ inline int norm_pass_tokens(int m, int k, int u, int threads) {
-  const int t = (u * threads) / (k >> 3);
+  const int t = (u * threads) / norm_row_slots(k);
   return t < m ? t : m;
 }
 
+// LDS (doubles) a norm stage's wave sums and wave maxima take: one of each per wave and round.
+__host__ __device__ inline int norm_lds_doubles(int waves) { return 2 * kNormU * waves; }
+
 // Residual add + RMSNorm input stage of an item (see StackDesc.nw): every workgroup with work in
 // the projection computes r and the normed input from the same words in the same order -- the
-// sum of r^2 per token in fp64, per 8-value chunk, then the token's chunks lane-strided and the
-// lanes in a fixed tree; mean rounded to fp32, scale = 1 / sqrt(mean + eps) in fp32; input
+// sum of r^2 per token in fp64: per 8-value chunk, then per wave (wave_sum_last), then the
+// waves in slot order; mean rounded to fp32, scale = 1 / sqrt(mean + eps) in fp32; input
 // bf16(bf16(r * scale) * w) (norm.py:53-80, reference.py:13-28) -- and stages its slice of that
-// input like any activation (FP8: quantized per token over the whole normed row). The owner
-// (row block 0) also writes r and the input and publishes r. Tokens t0 .. t0 + tn - 1 (one
-// pass); `css` holds tn * k / 8 + 16 doubles.
+// input like any activation (FP8: quantized per token over the whole normed row, its maximum
+// taken per wave the same way). The squares of bf16 values are exact in fp64 and their sums
+// agree to the last fp64 bits in any order, below what rounding the mean to fp32 can see. The
+// owner (row block 0) also writes r and the input and publishes r. Tokens t0 .. t0 + tn - 1
+// (one pass); `css` holds norm_lds_doubles(waves) doubles.
 template <class F, int U>
-__device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
-                                                double* css, bool owner, const Waits& w, int t0, int tn) {
+__device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, int step0, int nst, double* css,
+                                                bool owner, const Waits& w, int t0, int tn) {
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const GemmArgs& a = d.a;
-  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
-  const int cpr = a.k >> 3, total = tn * cpr;
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, nw = nthr >> 6;
+  const int cpr = a.k >> 3, cpw = norm_row_slots(a.k), slots = tn * cpw;
   const bool has_delta = d.xwire != nullptr, rwire = d.rwire != nullptr;
   const XWire dx(has_delta ? d.xwire : nullptr, has_delta ? d.xpitch : 0, a.m, w);
   const XWire rx(rwire ? d.rwire : nullptr, rwire ? a.k : 0, a.m, w);
-  auto chunk = [&](int u, int& mm, int& kabs) {
+  // Round u: slot q = tid + u * threads = 64 (u * waves + wave) + lane, token q / cpw, chunk
+  // q % cpw (slots past the row's cpr chunks hold nothing).
+  int tok[U], kab[U];
+  bool on[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
     const int q = tid + u * nthr;
-    mm = q / cpr;
-    kabs = (q - mm * cpr) * 8;
-    mm += t0;
-    return q < total;
+    tok[u] = q / cpw;
+    kab[u] = (q - tok[u] * cpw) * 8;
+    on[u] = q < slots && kab[u] < a.k;
+    tok[u] += t0;
+  }
+  auto chunk = [&](int u, int& mm, int& kabs) {
+    mm = tok[u];
+    kabs = kab[u];
+    return on[u];
   };
   XWire::Raw rd[U], rr[U];
   uint4 rp[U], wv[U], rv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    int mm, kabs;
-    if (chunk(u, mm, kabs)) {
-      if (has_delta) dx.fetch(a, mm, kabs, rd[u]);
+    if (on[u]) {
+      if (has_delta) dx.fetch(a, tok[u], kab[u], rd[u]);
       if (rwire) {
-        rx.fetch(a, mm, kabs, rr[u]);
+        rx.fetch(a, tok[u], kab[u], rr[u]);
       } else {
         const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(d.rmem) +
-                                                              (size_t)mm * a.k + kabs));
+                                                              (size_t)tok[u] * a.k + kab[u]));
         rp[u] = uint4{t[0], t[1], t[2], t[3]};
       }
-      const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(d.nw) + kabs));
+      const u32x4 t = *gmem(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(d.nw) + kab[u]));
       wv[u] = uint4{t[0], t[1], t[2], t[3]};
     }
   }
   if (has_delta) settle_batch<XWire, U>(a, dx, rd, chunk);
   if (rwire) settle_batch<XWire, U>(a, rx, rr, chunk);
+  const int wave = tid >> 6;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    int mm, kabs;
-    if (chunk(u, mm, kabs)) {
+    double ss = 0.0;
+    rv[u] = uint4{0u, 0u, 0u, 0u};
+    if (on[u]) {
       const uint4 x = rwire ? rx.value(rr[u]) : rp[u];
       uint4 r = x;
       if (has_delta) {
@@ -437,84 +455,102 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
       }
       rv[u] = r;
       const uint32_t rs[4] = {r.x, r.y, r.z, r.w};
-      double ss = 0.0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const double lo = bf2f(rs[i] & 0xffffu), hi = bf2f(rs[i] >> 16);
         ss += lo * lo;
         ss += hi * hi;
       }
-      css[tid + u * nthr] = ss;
     }
+    ss = wave_sum_last(ss);
+    if (lane == 63 && u * nthr < slots) css[u * nw + wave] = ss;
   }
   __syncthreads();
-  double* tot = css + total;
-  for (int t = tid >> 6; t < tn; t += nthr >> 6) {  // token t0 + t's total, by one wave
-    double sum = 0.0;
-    for (int c = lane; c < cpr; c += 64) sum += css[t * cpr + c];
+  // Each thread adds up the wave sums of its tokens, in slot order (entry e = u * waves + wave
+  // covers slots 64 e .. 64 e + 63, all of one token).
+  constexpr int E = U * 8;
+  const int ne = min(U * nw, (slots + 63) >> 6);
+  double ws[E];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if (lane == 0) tot[t] = sum;
+  for (int e = 0; e < E; ++e) ws[e] = e < ne ? css[e] : 0.0;
+  // entries of token t (relative): [t * wpr, (t + 1) * wpr)
+  const int wpr = cpw >> 6;
+  int e0[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) e0[u] = (tok[u] - t0) * wpr;
+  float scale[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    double tot = 0.0;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (e < ne && e >= e0[u] && e < e0[u] + wpr) tot += ws[e];
+    scale[u] = 1.0f / sqrtf((float)(tot / (double)a.k) + d.eps);
   }
-  __syncthreads();
-  // The normed input of chunk u (and its largest magnitude): mean rounded to fp32, + eps and
-  // 1/sqrt in fp32, as torch's rsqrt(mean + eps).
-  auto normed_chunk = [&](int u, int mm, float& mx) {
-    const float scale = 1.0f / sqrtf((float)(tot[mm - t0] / (double)a.k) + d.eps);
-    const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+  // The normed input (kept for the codes) and, for FP8, its largest magnitude per wave.
+  uint4 yv[U];
+  float mx[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws2[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
     uint32_t o[4];
-    mx = 0.f;
+    float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale) * bf2f(ws[i] & 0xffffu));
-      const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale) * bf2f(ws[i] >> 16));
+      const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale[u]) * bf2f(ws2[i] & 0xffffu));
+      const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale[u]) * bf2f(ws2[i] >> 16));
       o[i] = bf16_pair(y0, y1);
-      mx = fmaxf(mx, fmaxf(fabsf(y0), fabsf(y1)));
+      m = fmaxf(m, fmaxf(fabsf(y0), fabsf(y1)));
     }
-    return uint4{o[0], o[1], o[2], o[3]};
-  };
+    yv[u] = uint4{o[0], o[1], o[2], o[3]};
+    mx[u] = on[u] ? m : 0.f;
+  }
   const int c0 = step0 * (F::KSTEP / 8), c1 = c0 + nst * (F::KSTEP / 8);  // the slice's chunks of a row
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    int mm, kabs;
-    if (chunk(u, mm, kabs)) {
-      float mx;
-      const uint4 y = normed_chunk(u, mm, mx);
-      const uint32_t o[4] = {y.x, y.y, y.z, y.w};
-      if constexpr (!FP8) {
-        const int kc = kabs >> 3;
-        if (kc >= c0 && kc < c1)
-          *reinterpret_cast<uint4*>(lds + mm * a.xstride + (kabs - step0 * F::KSTEP) * 2) = F::order(y);
-      }
-      if (owner) {
-        const size_t e = (size_t)mm * a.k + kabs;
-        if (d.rout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.rout) + e)) =
-                        u32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w};
-        if (d.nout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.nout) + e)) =
-                        u32x4{o[0], o[1], o[2], o[3]};
-        if (d.rpub) {
-          const uint32_t rs2[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+    if (!on[u]) continue;
+    const int mm = tok[u], kabs = kab[u];
+    if constexpr (!FP8) {
+      const int kc = kabs >> 3;
+      if (kc >= c0 && kc < c1)
+        *reinterpret_cast<uint4*>(lds + mm * a.xstride + (kabs - step0 * F::KSTEP) * 2) = F::order(yv[u]);
+    }
+    if (owner) {
+      const size_t e = (size_t)mm * a.k + kabs;
+      if (d.rout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.rout) + e)) =
+                      u32x4{rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+      if (d.nout) *gmem(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(d.nout) + e)) =
+                      u32x4{yv[u].x, yv[u].y, yv[u].z, yv[u].w};
+      if (d.rpub) {
+        const uint32_t rs2[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) wire_store_pair(d.rpub + (e >> 1) + i, rs2[i], w.epoch);
-        }
+        for (int i = 0; i < 4; ++i) wire_store_pair(d.rpub + (e >> 1) + i, rs2[i], w.epoch);
       }
-      if constexpr (FP8) atomicMax(&amax[mm], __float_as_uint(mx));
     }
   }
   if constexpr (FP8) {  // the codes of the slice, at the token scales of the whole normed rows
-    __syncthreads();
-    float* sx = reinterpret_cast<float*>(lds + a.off_sx);
-    auto token_scale = [&](int mm) { return fmaxf(__uint_as_float(amax[mm]) / 448.f, 1e-12f); };
-    for (int i = tid; i < tn; i += nthr) sx[t0 + i] = token_scale(t0 + i);
+    float* wm = reinterpret_cast<float*>(css + kNormU * 8);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      int mm, kabs;
-      if (chunk(u, mm, kabs)) {
-        const int kc = kabs >> 3;
-        float mx;
-        if (kc >= c0 && kc < c1)
-          store_e4m3_chunk(lds + mm * a.xstride + (kc - c0) * 8, normed_chunk(u, mm, mx), token_scale(mm));
-      }
+      const float m = wave_max_last(mx[u]);
+      if (lane == 63 && u * nthr < slots) wm[u * nw + wave] = m;
+    }
+    __syncthreads();
+    float wmx[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) wmx[e] = e < ne ? wm[e] : 0.f;
+    float* sx = reinterpret_cast<float*>(lds + a.off_sx);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float m = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (e < ne && e >= e0[u] && e < e0[u] + wpr) m = fmaxf(m, wmx[e]);
+      const float ts = fmaxf(m / 448.f, 1e-12f);
+      if (!on[u]) continue;
+      if (kab[u] == 0) sx[tok[u]] = ts;
+      const int kc = kab[u] >> 3;
+      if (kc >= c0 && kc < c1) store_e4m3_chunk(lds + tok[u] * a.xstride + (kc - c0) * 8, yv[u], ts);
     }
   }
 }
@@ -523,12 +559,12 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
 // The whole stage: its token rows in passes of norm_pass_tokens (one pass at M = 1..4 with
 // k = 2560 and 8 waves). A pass's LDS sums are reused by the next after a barrier.
 template <class F, int U>
-__device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int step0, int nst, uint32_t* amax,
-                                           double* css, bool owner, const Waits& w) {
+__device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int step0, int nst, double* css, bool owner,
+                                           const Waits& w) {
   const int tpp = norm_pass_tokens(d.a.m, d.a.k, U, blockDim.x);
   for (int t0 = 0; t0 < d.a.m; t0 += tpp) {
     if (t0) __syncthreads();
-    stage_norm_pass<F, U>(d, lds, step0, nst, amax, css, owner, w, t0, min(tpp, d.a.m - t0));
+    stage_norm_pass<F, U>(d, lds, step0, nst, css, owner, w, t0, min(tpp, d.a.m - t0));
   }
 }
 
@@ -549,10 +585,10 @@ __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char*
     if (nd) {  // a residual add + RMSNorm stage
       double* css = reinterpret_cast<double*>(reinterpret_cast<char*>(amax) + 64);
       const bool owner = it.tg == 0 && it.s == 0;
-      if (a.m * (a.k >> 3) <= (int)blockDim.x)  // one chunk per thread (every M = 1 stage)
-        stage_norm<F, 1>(*nd, lds, step0, nst, amax, css, owner, *nw);
+      if (a.m * norm_row_slots(a.k) <= (int)blockDim.x)  // one chunk per thread (every M = 1 stage)
+        stage_norm<F, 1>(*nd, lds, step0, nst, css, owner, *nw);
       else
-        stage_norm<F, kNormU>(*nd, lds, step0, nst, amax, css, owner, *nw);
+        stage_norm<F, kNormU>(*nd, lds, step0, nst, css, owner, *nw);
     } else if constexpr (FP8) {
       bool done = false;
       if constexpr (XS::POLLS) {
@@ -1040,10 +1076,10 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
                 "projection %d: NULL pointer (x must be NULL exactly when the input is a norm stage)", c);
     if (normed(c)) {
       QLX_REQUIRE(norms[c].resid != nullptr, "projection %d: a norm stage needs its residual", c);
-      QLX_REQUIRE(q.k / 8 <= kNormU * waves * 64,
+      QLX_REQUIRE(norm_row_slots(q.k) <= kNormU * waves * 64,
                   "projection %d: a norm stage takes k <= %d (one token row per pass; k=%d)", c, kNormU * waves * 64 * 8,
                   q.k);
-      css_doubles = std::max(css_doubles, norm_pass_tokens(m, q.k, kNormU, waves * 64) * (q.k / 8) + 16);
+      css_doubles = std::max(css_doubles, norm_lds_doubles(8));
     }
   }
   auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };
