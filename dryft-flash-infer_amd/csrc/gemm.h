@@ -60,6 +60,7 @@ struct GemmArgs {
   int tblocks;       // skinny GEMM: 2 = two 32-token blocks in one launch (else 0)
   int off_red;       // persistent kernel: LDS offset of the waves' partial sums (apart from x)
   int off_bt;        // persistent kernel: LDS offset of the code-bias totals [step][group][MT][16]
+  int off_ring;      // ring kernel: LDS offset of the waves' weight rings [wave][slot][LOADS KB]
   int pm;            // skinny GEMM token blocks: rows of a K-slice plane (the whole batch)
   // Fused residual add + RMSNorm (qlx_linear_add_norm): y receives delta = bf16(x W^T)
   // with device-coherent stores; the workgroup that completes the last row block adds
@@ -1524,6 +1525,212 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_persist_kernel(GemmArgs a) {
     if (nt >= a.tile_groups) break;
     tg = nt;
     __syncthreads();  // scales and partial sums are restaged for the next row block
+  }
+}
+
+// ---- persistent single calls with a direct-to-LDS weight ring (4-bit weights) ---------
+//
+// The register pipeline keeps PipeDepth steps in flight per wave, and 4-bit weights, whose
+// dequantization holds many registers, get 3: 48 KB per CU, too few bytes to cover HBM
+// latency. Here each wave streams its steps into a ring of D slots in LDS instead
+// (global_load_lds_dwordx4: lane i's 16 bytes land at slot + 16 i, counted by vmcnt like any
+// load), D steps ahead of its MFMAs, and the ring runs on across row blocks: a workgroup's
+// steps form one sequence, so the next row block's first steps are in flight while the current
+// one finishes. The row block's group scales come the same way, one row block ahead, into a
+// double buffer. One 16-row tile per wave over the whole K (kw = 1), so a wave's outputs need
+// no cross-wave sum and are stored from its registers. The arithmetic and its order are the
+// register pipeline's (FmtW4::compute): the outputs are bit-identical.
+//
+// Waits are explicit. Every LDS access of the steady state is an assembler instruction, and
+// global loads are all LDS DMA: a compiler-visible LDS access after an LDS DMA would make the
+// compiler wait for every DMA in flight. A ring slot is read after s_waitcnt vmcnt((D - 1) *
+// LOADS): the D - 1 later steps may still be out. Loads complete in order, and anything else
+// issued in between (scales, stores) only makes that wait longer, never short.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+__device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ float ds_read4f(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void ds_write4f(uint32_t addr, float v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left open).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 0..63");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier that waits for this wave's LDS operations but not for its loads in flight
+// (a __syncthreads fence would wait for the ring's DMA); the memory clobber keeps the compiler
+// from moving memory operations across it.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void dma16(const void* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 2);
+}
+__device__ __forceinline__ void dma4(const void* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+}
+
+// LDS of the ring kernel, after the activation (a.off_sc .. : [2][scale words] raw scale
+// pairs, then the code-bias totals [step][2][16] floats, then the rings [wave][D][2 KB]).
+__host__ __device__ inline int ring_scale_words(int nsteps, int rt) { return (nsteps * 16 * rt + 63) & ~63; }
+
+template <int WAVES, bool BM1>
+__device__ __forceinline__ void ring_step_w4(f32x4& acc, const u32x4 (&c)[2], uint32_t xa, uint32_t sa, uint32_t ba,
+                                             int lane) {
+  // xa: this lane's activation bytes of the step (token row, lane group), sa: its four rows'
+  // scale pairs of the step, ba: the step's code-bias totals (its token column).
+  u32x4 bv[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bv[j][t] = ds_read16(xa + j * 256 + t * 16);
+  u32x4 sp = ds_read16(sa);
+  float bt[2] = {0.f, 0.f};
+  if constexpr (!BM1) {
+    bt[0] = ds_read4f(ba);
+    bt[1] = ds_read4f(ba + 64);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(bv[0][0]), "+v"(bv[0][1]), "+v"(bv[0][2]), "+v"(bv[0][3]), "+v"(bv[1][0]), "+v"(bv[1][1]),
+                 "+v"(bv[1][2]), "+v"(bv[1][3]), "+v"(bt[0]), "+v"(bt[1]), "+v"(sp)
+               :
+               : "memory");
+  const uint4 avb = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    f32x4 tmp = {0.f, 0.f, 0.f, 0.f}, tb = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t wd[4] = {c[j][0], c[j][1], c[j][2], c[j][3]};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 av;
+      av.x = nib_pair(wd[t], 0);
+      av.y = nib_pair(wd[t], 4);
+      av.z = nib_pair(wd[t], 8);
+      av.w = nib_pair(wd[t], 12);
+      const uint4 b = uint4{bv[j][t][0], bv[j][t][1], bv[j][t][2], bv[j][t][3]};
+      tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(b), tmp, 0, 0, 0);
+      if constexpr (BM1) tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avb), as_bf16x8(b), tb, 0, 0, 0);
+    }
+    if constexpr (BM1) {
+      // Through a VALU copy (an identity DPP move): the compiler pads an MFMA result's readers
+      // with the wait states it needs, but not an assembler statement's.
+      const float v = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(tb[0]), 0xe4, 0xf, 0xf, false));
+      if (lane < 16) ds_write4f(ba + j * 64, v);
+    } else {
+      tb = f32x4{bt[j], bt[j], bt[j], bt[j]};
+    }
+    // scale of row i, group j: half j of the row's pair (bf16 bits)
+    f32x4 s4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s4[i] = bf2f(j ? sp[i] >> 16 : sp[i] & 0xffffu);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(s4[i], tmp[i] - tb[i], acc[i]);
+  }
+}
+
+template <int WAVES, int D, int WPC>
+__global__ void __launch_bounds__(WAVES * 64, WPC * WAVES / 4) gemm_ring_w4_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  static_assert(D >= 2 && (D - 1) * 2 <= 63, "vmcnt holds at most 63");
+  using F = FmtW4;
+  constexpr int L = F::LOADS, SLOT = L * 1024;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = gridDim.x, ns = a.nsteps, rows = 16 * a.rt;
+  const int nitems = (a.tile_groups - (int)blockIdx.x + G - 1) / G;  // row blocks b, b + G, ...
+  const int total = nitems * ns;                                      // this wave's steps
+  const int sw = ring_scale_words(ns, a.rt);
+  char* sbuf = lds + a.off_sc;  // [2][sw] scale pairs
+  char* ring = lds + a.off_ring + wave * (D * SLOT);
+  const uint32_t ring_a = lds_addr(ring) + lane * 16;
+  const uint32_t* ws = reinterpret_cast<const uint32_t*>(a.ws);
+  // The scale pairs of row block `item` into buffer `item & 1`, word q = step * rows + row;
+  // each DMA moves 64 words, and this wave moves every WAVES-th of them.
+  auto scales = [&](int item) {
+    const int tg = (int)blockIdx.x + item * G;
+    char* dst = sbuf + (item & 1) * (sw * 4);
+    for (int t = wave; t * 64 < sw; t += WAVES) {
+      int q = t * 64 + lane;
+      q = q < ns * rows ? q : ns * rows - 1;  // lanes past the end reread the last word
+      const int st = q / rows, rl = q - st * rows, tile = tg * a.rt + (rl >> 4);
+      const int row = weight_row(a, tile < a.ntiles ? tile : a.ntiles - 1, rl & 15);
+      dma4(ws + (size_t)row * (a.k >> 8) + st, dst + t * 256);
+    }
+  };
+  auto wrow_of = [&](int item) {
+    const int tile = ((int)blockIdx.x + item * G) * a.rt + wave;
+    return weight_row(a, tile < a.ntiles ? tile : a.ntiles - 1, lane & 15);  // past the end: dropped
+  };
+  int ig = 0, ii = 0, is = 0, iw = wrow_of(0);  // next step to issue: row block ii, step is
+  auto issue = [&]() {
+    char* slot = ring + (ig % D) * SLOT;
+#pragma unroll
+    for (int j = 0; j < L; ++j) dma16(F::chunk_ptr(a, iw, is, lane, j), slot + j * 1024);
+    ++ig;
+    if (++is == ns) {
+      is = 0;
+      if (++ii < nitems) iw = wrow_of(ii);
+    }
+  };
+  // Prologue: row block 0's scales, the activation (its LDS writes wait for nothing else in
+  // flight), then the ring's first D steps (the launch guarantees total >= D).
+  scales(0);
+  stage_bf16<F>(a, XPlain{}, lds, 0, ns);
+#pragma unroll
+  for (int p = 0; p < D; ++p) issue();
+  wait_vm<D * L>();  // this wave's scale DMAs, issued before the ring's
+  barrier_lds();
+  const int mrow = min(lane & 15, a.m - 1);
+  const uint32_t xa0 = lds_addr(lds) + mrow * a.xstride + (lane >> 4) * 64;
+  const uint32_t bt0 = lds_addr(lds) + a.off_bt + (lane & 15) * 4;
+  const int rowl = wave * 16 + 4 * (lane >> 4);
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+  for (int item = 0, g = 0; item < nitems; ++item) {
+    if (item + 1 < nitems) scales(item + 1);
+    const int ig0 = ig;
+    const uint32_t sa0 = lds_addr(sbuf) + (item & 1) * (sw * 4) + rowl * 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < ns; ++s, ++g) {
+      if (ig - g == D)
+        wait_vm<(D - 1) * L>();
+      else
+        wait_vm<0>();
+      u32x4 c[L];
+#pragma unroll
+      for (int j = 0; j < L; ++j) c[j] = ds_read16(ring_a + (g % D) * SLOT + j * 1024);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(c[0]), "+v"(c[1]) : : "memory");
+      if (ig < total) issue();  // the slot just read is free again
+      const uint32_t xa = xa0 + s * 512, sa = sa0 + s * rows * 4, ba = bt0 + s * 128;
+      if (item == 0)
+        ring_step_w4<WAVES, true>(acc, c, xa, sa, ba, lane);
+      else
+        ring_step_w4<WAVES, false>(acc, c, xa, sa, ba, lane);
+    }
+    // Outputs from registers: lane (r, c) holds rows 4 (lane >> 4) .. + 3 of the wave's tile
+    // for token lane & 15 (0 + v: a -0 sum leaves as +0, as the LDS sum in tile_value does).
+    const int tile = ((int)blockIdx.x + item * G) * a.rt + wave, mm = lane & 15;
+    if (tile < a.ntiles && mm < a.m) {
+      const int r0 = 16 * tile + 4 * (lane >> 4);
+      if (r0 + 1 < a.n) store_pair(y, (size_t)mm * a.n + r0, 0.f + acc[0], 0.f + acc[1]);
+      if (r0 + 3 < a.n) store_pair(y, (size_t)mm * a.n + r0 + 2, 0.f + acc[2], 0.f + acc[3]);
+    }
+    // The next row block's scales (issued before this one's ring refills) have landed once all
+    // but the refills since are in; then the buffer and the code-bias totals are shared.
+    if (item + 1 < nitems) {
+      if (ig - ig0 >= D - 1)
+        wait_vm<(D - 1) * L>();
+      else
+        wait_vm<0>();
+    }
+    barrier_lds();
   }
 }
 

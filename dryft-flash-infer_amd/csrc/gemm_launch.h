@@ -140,12 +140,57 @@ bool launch_persist(const GemmArgs& a, int lds, hipStream_t st, hipError_t* err)
   }
 }
 
+// The ring kernel (gemm_ring_w4_kernel) where it applies: 4-bit weights, at most 16 tokens,
+// one tile per wave (kw = 1), bf16 outputs, the persistent launch's other conditions, at least
+// 4 steps per row block, and LDS for a ring of 8 steps per wave (4 where the activation leaves
+// less room). One workgroup per CU.
+template <class F, int MT, int RW, int WAVES>
+bool launch_ring(const GemmArgs& a, int lds, hipStream_t st, hipError_t* err) {
+  if constexpr (!std::is_same<F, FmtW4>::value || RW != 1 || MT != 1) {
+    return false;
+  } else {
+    if (a.kw != 1 || a.splits != 1 || a.an_counter || a.n % 16 || a.mode != QLX_MODE_BF16 || a.nsteps < 4)
+      return false;
+    const int grid = device_cus();
+    if (grid <= 0 || a.tile_groups < 2 * grid) return false;
+    GemmArgs b = a;
+    b.off_bt = round16(a.off_sc + 2 * ring_scale_words(a.nsteps, a.rt) * 4);
+    b.off_ring = round16(b.off_bt + a.nsteps * 2 * 16 * 4);
+    const int slot = F::LOADS * 1024 * WAVES;  // one step of every wave
+    // Two workgroups per CU (four waves per SIMD, whose issue overlaps) with 3-step rings where
+    // LDS allows, else one with 8 or 4 steps.
+    struct Shape { int wpc, depth; const void* fn; };
+    const Shape shapes[] = {{2, 3, reinterpret_cast<const void*>(&gemm_ring_w4_kernel<WAVES, 3, 2>)},
+                            {1, 8, reinterpret_cast<const void*>(&gemm_ring_w4_kernel<WAVES, 8, 1>)},
+                            {1, 4, reinterpret_cast<const void*>(&gemm_ring_w4_kernel<WAVES, 4, 1>)}};
+    int pick = -1;
+    for (int i = 0; i < 3 && pick < 0; ++i) {
+      const int lds_i = b.off_ring + shapes[i].depth * slot;
+      if (lds_i * shapes[i].wpc <= kLdsLimit && a.tile_groups >= 2 * grid * shapes[i].wpc) pick = i;
+    }
+    if (pick < 0) return false;
+    const int total = b.off_ring + shapes[pick].depth * slot;
+    const void* fn = shapes[pick].fn;
+    static int allowed[3] = {64 * 1024, 64 * 1024, 64 * 1024};
+    int& ok = allowed[pick];
+    if (total > ok) {
+      if ((*err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, total)) != hipSuccess)
+        return true;
+      ok = total;
+    }
+    void* args[] = {&b};
+    *err = hipLaunchKernel(fn, dim3(grid * shapes[pick].wpc), dim3(WAVES * 64), args, (size_t)total, st);
+    return true;
+  }
+}
+
 // AN_OK: this format's entry points include the fused add-norm (qlx_linear_add_norm), which
 // launches the AN instantiation when a.an_counter is set.
 template <class F, int MT, int RW, int WAVES, bool AN_OK>
 hipError_t launch_one(const GemmArgs& a, int lds, hipStream_t st) {
   const int grid = a.tile_groups * a.splits;
   hipError_t e;
+  if (launch_ring<F, MT, RW, WAVES>(a, lds, st, &e)) return e;
   if (launch_persist<F, MT, RW, WAVES>(a, lds, st, &e)) return e;
   if constexpr (AN_OK) {
     if (a.an_counter) {

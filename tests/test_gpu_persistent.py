@@ -1,8 +1,10 @@
-"""The persistent single-call GEMM (gemm_persist_kernel): a projection with at least two row
-blocks per workgroup -- the 151936-row lm_head -- runs as one workgroup per CU (W4A16; two for
-FP8) looping over row blocks, W4A16 with its code-bias totals computed on the first row block
-only. Its outputs must be bit-identical to the one-workgroup-per-row-block kernel on the same
-plan: a slice of whole tiles of the same tile-layout weight (too few row blocks for the
+"""The persistent single-call GEMMs: a projection with at least two row blocks per workgroup --
+the 151936-row lm_head -- runs as persistent workgroups looping over row blocks, W4A16 with its
+code-bias totals computed on the first row block only. W4A16 at one tile per wave takes the
+direct-to-LDS weight ring (gemm_ring_w4_kernel: two workgroups per CU with 3-step rings at 1-4
+tokens, one with 4-step rings at 8 and 16); FP8 the register pipeline (gemm_persist_kernel).
+Their outputs must be bit-identical to the one-workgroup-per-row-block kernel on the same
+plan: a slice of whole tiles of the same tile-layout weight (too few row blocks for a
 persistent launch) gives the same rows bit for bit. SwiGLU outputs of a persistent launch are
 within one bf16 step of the SwiGLU of its own bf16 outputs, and everything is within the
 north star's rel-L2 of the oracle."""
@@ -26,7 +28,7 @@ def tile_slice(t, t0, t1):
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "fp8"])
-@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
 def test_persistent_lm_head_equals_per_block_kernel(fmt, m):
     print(f"persistent lm_head {fmt} m={m}", flush=True)
     n, k = 151936, 2560
