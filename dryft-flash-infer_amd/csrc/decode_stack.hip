@@ -676,6 +676,53 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
   const GemmArgs& a = d.a;
   char* red = lds + d.off_red;
   acc_to_lds<1, 1>(red, acc, team, guard);
+  if constexpr (!PIECES) {
+    if (!(MAXIMA && d.ymax)) {
+      // One output value per thread, (tile, token, row) in thread order so that a row pair is
+      // two neighbouring lanes: its kw partial sums read together (one LDS round trip) and
+      // added in wave order, as tile_value adds them; the even lane takes its neighbour's
+      // value by a DPP move and stores the pair.
+      constexpr int RO = SW ? 8 : 16;  // output rows per tile
+      const int m = a.m, kw = a.kw, per_tile = RO * m, total = a.rt * per_tile;
+      const int nout = SW ? a.half : a.n;
+      const float* rf = reinterpret_cast<const float*>(red);
+      uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+      uint64_t* const ywire = d.ywire;
+      for (int idx = team.tid(); idx < total; idx += team.size()) {
+        const int tl = idx / per_tile, rem = idx - tl * per_tile;
+        const int mm = rem / RO, r = rem - mm * RO;
+        const int tile = it.tg * a.rt + tl;
+        // partial (wave tl * kw + q, row, token mm): rf[((tl * kw + q) * 16 + row) * 16 + mm]
+        const float* base = rf + ((tl * kw) * 16 + r) * 16 + mm;
+        float pg[8], pu[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          pg[q] = q < kw ? base[q * 256] : 0.f;
+          if constexpr (SW) pu[q] = q < kw ? base[q * 256 + 8 * 16] : 0.f;
+        }
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (q < kw) {
+            g += pg[q];
+            if constexpr (SW) u += pu[q];
+          }
+        float o;
+        if constexpr (SW)
+          o = swiglu_bf(F::finish(a, lds, g, tl * 16 + r, mm), F::finish(a, lds, u, tl * 16 + r + 8, mm));
+        else
+          o = F::finish(a, lds, g, tl * 16 + r, mm);
+        const float o1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(o), 0x101, 0xf, 0xf, false));
+        if ((r & 1) == 0 && tile < a.ntiles) {
+          const int oi = (SW ? 8 : 16) * tile + r;
+          const uint32_t pair = bf16_pair(o, o1);
+          *gmem(reinterpret_cast<uint32_t*>(y + (size_t)mm * nout + oi)) = pair;
+          if (ywire) wire_store_pair(ywire + (size_t)mm * (nout >> 1) + (oi >> 1), pair, w.epoch);
+        }
+      }
+      return;
+    }
+  }
   constexpr int NV = SW ? 4 : 2;  // values per output pair: (g0, g1, u0, u1) or (v0, v1)
   constexpr int rows_out = SW ? 8 : 16;
   const int per_tile = (rows_out / 2) * a.m;
