@@ -370,6 +370,7 @@ __device__ __forceinline__ void stage_fp8_maxima(const GemmArgs& a, const XS& xs
 // thread (one row at least, checked on the host); more tokens take more passes.
 constexpr int kNormU = 3;
 __host__ __device__ inline int norm_row_slots(int k) { return ((k >> 3) + 63) & ~63; }
+constexpr int kNormWpr = 8;  // wave sums of one token row read together (rows up to k = 4096)
 
 // Token rows one pass of a norm stage takes.
 __host__ __device__ inline int norm_pass_tokens(int m, int k, int u, int threads) {
@@ -467,24 +468,25 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
   }
   __syncthreads();
   // Each thread adds up the wave sums of its tokens, in slot order (entry e = u * waves + wave
-  // covers slots 64 e .. 64 e + 63, all of one token).
-  constexpr int E = U * 8;
-  const int ne = min(U * nw, (slots + 63) >> 6);
-  double ws[E];
+  // covers slots 64 e .. 64 e + 63, all of one token; token t's are [t * wpr, (t + 1) * wpr)).
+  // Up to kNormWpr of them are read together; longer rows (k > 4096) read the rest one by one.
+  const int ne = min(U * nw, (slots + 63) >> 6), wpr = cpw >> 6;
+  int e0[U], e1[U];
 #pragma unroll
-  for (int e = 0; e < E; ++e) ws[e] = e < ne ? css[e] : 0.0;
-  // entries of token t (relative): [t * wpr, (t + 1) * wpr)
-  const int wpr = cpw >> 6;
-  int e0[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) e0[u] = (tok[u] - t0) * wpr;
+  for (int u = 0; u < U; ++u) {
+    e0[u] = (tok[u] - t0) * wpr;
+    e1[u] = min(e0[u] + wpr, ne);
+  }
   float scale[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    double tot = 0.0;
+    double v[kNormWpr], tot = 0.0;
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      if (e < ne && e >= e0[u] && e < e0[u] + wpr) tot += ws[e];
+    for (int i = 0; i < kNormWpr; ++i) v[i] = e0[u] + i < e1[u] ? css[e0[u] + i] : 0.0;
+#pragma unroll
+    for (int i = 0; i < kNormWpr; ++i)
+      if (e0[u] + i < e1[u]) tot += v[i];
+    for (int e = e0[u] + kNormWpr; e < e1[u]; ++e) tot += css[e];
     scale[u] = 1.0f / sqrtf((float)(tot / (double)a.k) + d.eps);
   }
   // The normed input (kept for the codes) and, for FP8, its largest magnitude per wave.
@@ -536,16 +538,15 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
       if (lane == 63 && u * nthr < slots) wm[u * nw + wave] = m;
     }
     __syncthreads();
-    float wmx[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) wmx[e] = e < ne ? wm[e] : 0.f;
     float* sx = reinterpret_cast<float*>(lds + a.off_sx);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float m = 0.f;
+      float v[kNormWpr], m = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e)
-        if (e < ne && e >= e0[u] && e < e0[u] + wpr) m = fmaxf(m, wmx[e]);
+      for (int i = 0; i < kNormWpr; ++i) v[i] = e0[u] + i < e1[u] ? wm[e0[u] + i] : 0.f;
+#pragma unroll
+      for (int i = 0; i < kNormWpr; ++i) m = fmaxf(m, v[i]);
+      for (int e = e0[u] + kNormWpr; e < e1[u]; ++e) m = fmaxf(m, wm[e]);
       const float ts = fmaxf(m / 448.f, 1e-12f);
       if (!on[u]) continue;
       if (kab[u] == 0) sx[tok[u]] = ts;
