@@ -448,10 +448,17 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
       if (has_delta) {
         const uint4 dv = dx.value(rd[u]);
         const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ds[4] = {dv.x, dv.y, dv.z, dv.w};
-        uint32_t o[4];
+        uint32_t o[4], nan = 0u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          o[i] = bf16_pair(bf2f(xs[i] & 0xffffu) + bf2f(ds[i] & 0xffffu), bf2f(xs[i] >> 16) + bf2f(ds[i] >> 16));
+        for (int i = 0; i < 4; ++i) {
+          o[i] = bf16_pair_hw(bf2f(xs[i] & 0xffffu) + bf2f(ds[i] & 0xffffu), bf2f(xs[i] >> 16) + bf2f(ds[i] >> 16));
+          nan |= bf16_nan_bits(o[i]);
+        }
+        if (nan != 0u) {  // a NaN: the integer rounding's sign | 0x7FC0 form
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            o[i] = bf16_pair(bf2f(xs[i] & 0xffffu) + bf2f(ds[i] & 0xffffu), bf2f(xs[i] >> 16) + bf2f(ds[i] >> 16));
+        }
         r = uint4{o[0], o[1], o[2], o[3]};
       }
       rv[u] = r;
@@ -495,14 +502,26 @@ __device__ __forceinline__ void stage_norm_pass(const StackDesc& d, char* lds, i
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint32_t rs[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w}, ws2[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-    uint32_t o[4];
+    uint32_t o[4], nan = 0u;
     float m = 0.f;
+    // bf16(bf16(r * scale) * w) by the hardware's pair conversion; a wave with a NaN anywhere
+    // redoes its values with the integer rounding (same bits but for a NaN's).
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale[u]) * bf2f(ws2[i] & 0xffffu));
-      const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale[u]) * bf2f(ws2[i] >> 16));
-      o[i] = bf16_pair(y0, y1);
-      m = fmaxf(m, fmaxf(fabsf(y0), fabsf(y1)));
+      const uint32_t t = bf16_pair_hw(bf2f(rs[i] & 0xffffu) * scale[u], bf2f(rs[i] >> 16) * scale[u]);
+      o[i] = bf16_pair_hw(bf2f(t & 0xffffu) * bf2f(ws2[i] & 0xffffu), bf2f(t >> 16) * bf2f(ws2[i] >> 16));
+      nan |= bf16_nan_bits(t) | bf16_nan_bits(o[i]);
+      m = fmaxf(m, fmaxf(fabsf(bf2f(o[i] & 0xffffu)), fabsf(bf2f(o[i] >> 16))));
+    }
+    if (nan != 0u) {
+      m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y0 = round_bf(round_bf(bf2f(rs[i] & 0xffffu) * scale[u]) * bf2f(ws2[i] & 0xffffu));
+        const float y1 = round_bf(round_bf(bf2f(rs[i] >> 16) * scale[u]) * bf2f(ws2[i] >> 16));
+        o[i] = bf16_pair(y0, y1);
+        m = fmaxf(m, fmaxf(fabsf(y0), fabsf(y1)));
+      }
     }
     yv[u] = uint4{o[0], o[1], o[2], o[3]};
     mx[u] = on[u] ? m : 0.f;
