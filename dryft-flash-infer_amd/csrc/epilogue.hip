@@ -111,14 +111,37 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
       for (int i = 0; i < 8; ++i) r[i] = bf2f((xs[i >> 1] >> (16 * (i & 1))) & 0xffffu);
       if (add) {
         const uint32_t ds[4] = {dv[u].x, dv[u].y, dv[u].z, dv[u].w};
+        // bf16 rounding by the hardware's pair conversion (the integer rounding's bits for every
+        // value but a NaN); a chunk meeting a NaN is redone the integer way.
+        uint32_t rp[4], nan = 0u;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float dd = planes ? round_bf(d[u][i]) : bf2f((ds[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-          r[i] = round_bf(r[i] + dd);
+        for (int i = 0; i < 8; i += 2) {
+          float dd0, dd1;
+          if (planes) {
+            const uint32_t dp = bf16_pair_hw(d[u][i], d[u][i + 1]);
+            nan |= bf16_nan_bits(dp);
+            dd0 = bf2f(dp & 0xffffu);
+            dd1 = bf2f(dp >> 16);
+          } else {
+            dd0 = bf2f(ds[i >> 1] & 0xffffu);
+            dd1 = bf2f(ds[i >> 1] >> 16);
+          }
+          rp[i >> 1] = bf16_pair_hw(r[i] + dd0, r[i + 1] + dd1);
+          nan |= bf16_nan_bits(rp[i >> 1]);
         }
-        if (res)
-          *reinterpret_cast<u32x4*>(res + base + 8 * c) =
-              u32x4{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+        if (nan == 0u) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) r[i] = bf2f((rp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float dd = planes ? round_bf(d[u][i]) : bf2f((ds[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+            r[i] = round_bf(r[i] + dd);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rp[i] = pack_bf2(r[2 * i], r[2 * i + 1]);
+        }
+        if (res) *reinterpret_cast<u32x4*>(res + base + 8 * c) = u32x4{rp[0], rp[1], rp[2], rp[3]};
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -166,14 +189,27 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
       if (c >= nc) continue;
       const uint32_t ws[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
       float v[8];
+      uint32_t vp[4], nan = 0u;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[i] = round_bf(round_bf(rbuf[8 * c + i] * scale) * bf2f((ws[i >> 1] >> (16 * (i & 1))) & 0xffffu));
-        rbuf[8 * c + i] = v[i];
+      for (int i = 0; i < 8; i += 2) {  // as above: the pair conversion, the integer way on a NaN
+        const uint32_t t = bf16_pair_hw(rbuf[8 * c + i] * scale, rbuf[8 * c + i + 1] * scale);
+        vp[i >> 1] = bf16_pair_hw(bf2f(t & 0xffffu) * bf2f(ws[i >> 1] & 0xffffu),
+                                  bf2f(t >> 16) * bf2f(ws[i >> 1] >> 16));
+        nan |= bf16_nan_bits(t) | bf16_nan_bits(vp[i >> 1]);
       }
-      if (y)
-        *reinterpret_cast<u32x4*>(y + base + 8 * c) =
-            u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
+      if (nan == 0u) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = bf2f((vp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = round_bf(round_bf(rbuf[8 * c + i] * scale) * bf2f((ws[i >> 1] >> (16 * (i & 1))) & 0xffffu));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vp[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rbuf[8 * c + i] = v[i];
+      if (y) *reinterpret_cast<u32x4*>(y + base + 8 * c) = u32x4{vp[0], vp[1], vp[2], vp[3]};
     }
   } else {
     for (int c = threadIdx.x; c < n; c += 256) {
@@ -183,7 +219,8 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
     }
   }
   if (q8) {
-    // FP8 per-token activation quantize of the normed row (every value is a bf16 value):
+    // FP8 per-token activation quantize of the normed row (every value is a bf16 value, so its
+    // top 16 bits are its bf16 bits, a NaN's the integer rounding's sign | 0x7FC0 form):
     // scale = max(amax / 448, 1e-12), codes e4m3(x / scale).
     __shared__ float pmax[4];
     __syncthreads();
@@ -199,7 +236,7 @@ add_rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
       uint32_t pk[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        pk[i] = (uint32_t)f2bf(rbuf[8 * c8 + 2 * i]) | ((uint32_t)f2bf(rbuf[8 * c8 + 2 * i + 1]) << 16);
+        pk[i] = (__float_as_uint(rbuf[8 * c8 + 2 * i]) >> 16) | (__float_as_uint(rbuf[8 * c8 + 2 * i + 1]) & 0xffff0000u);
       *reinterpret_cast<uint2*>(q8 + base + 8 * c8) = e4m3_chunk(uint4{pk[0], pk[1], pk[2], pk[3]}, sc, yr);
     }
     return;
