@@ -125,13 +125,48 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeArgs ra) {
   unpack8(*gmem(reinterpret_cast<const u32x4*>(gain + 64 + 8 * j)), wh);
 
 
+  // Every rounding below is to bf16, by the hardware's pair conversion (the integer rounding's
+  // bits for every value but a NaN, checked on all 2^32 inputs); a lane meeting a NaN redoes its
+  // values with the integer rounding.
   float yl[8], yh[8];
+  uint32_t ylp[4], yhp[4], nan = 0u;
+  auto lo = [](uint32_t p) { return bf2f(p & 0xffffu); };
+  auto hi = [](uint32_t p) { return bf2f(p >> 16); };
+  auto pr = [&nan](float x0, float x1) {
+    const uint32_t p = bf16_pair_hw(x0, x1);
+    nan |= bf16_nan_bits(p);
+    return p;
+  };
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float a = round_bf(round_bf(xl[i] * scale) * wl[i]);  // n[8 j + i]
-    const float b = round_bf(round_bf(xh[i] * scale) * wh[i]);  // n[64 + 8 j + i]
-    yl[i] = round_bf(round_bf(a * cl[i]) + round_bf(-b * sl[i]));
-    yh[i] = round_bf(round_bf(b * ch[i]) + round_bf(a * sh[i]));
+  for (int i = 0; i < 8; i += 2) {
+    const uint32_t ta = pr(xl[i] * scale, xl[i + 1] * scale), tb = pr(xh[i] * scale, xh[i + 1] * scale);
+    const uint32_t a = pr(lo(ta) * wl[i], hi(ta) * wl[i + 1]);  // n[8 j + i], n[8 j + i + 1]
+    const uint32_t b = pr(lo(tb) * wh[i], hi(tb) * wh[i + 1]);  // n[64 + 8 j + i], ...
+    const uint32_t p1 = pr(lo(a) * cl[i], hi(a) * cl[i + 1]), p2 = pr(-lo(b) * sl[i], -hi(b) * sl[i + 1]);
+    const uint32_t p3 = pr(lo(b) * ch[i], hi(b) * ch[i + 1]), p4 = pr(lo(a) * sh[i], hi(a) * sh[i + 1]);
+    ylp[i >> 1] = pr(lo(p1) + lo(p2), hi(p1) + hi(p2));
+    yhp[i >> 1] = pr(lo(p3) + lo(p4), hi(p3) + hi(p4));
+  }
+  if (nan == 0u) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      yl[i] = bf2f((ylp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+      yh[i] = bf2f((yhp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float a = round_bf(round_bf(xl[i] * scale) * wl[i]);  // n[8 j + i]
+      const float b = round_bf(round_bf(xh[i] * scale) * wh[i]);  // n[64 + 8 j + i]
+      yl[i] = round_bf(round_bf(a * cl[i]) + round_bf(-b * sl[i]));
+      yh[i] = round_bf(round_bf(b * ch[i]) + round_bf(a * sh[i]));
+    }
+    const u32x4 l = pack8(yl), h = pack8(yh);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ylp[i] = l[i];
+      yhp[i] = h[i];
+    }
   }
 
   if (is_q) {
@@ -141,8 +176,13 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeArgs ra) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) yl[i] = yh[i] = __builtin_nanf("");
     }
-    *gmem(reinterpret_cast<u32x4*>(q + 8 * j)) = pack8(yl);
-    *gmem(reinterpret_cast<u32x4*>(q + 64 + 8 * j)) = pack8(yh);
+    if (!in_table) {
+      *gmem(reinterpret_cast<u32x4*>(q + 8 * j)) = pack8(yl);
+      *gmem(reinterpret_cast<u32x4*>(q + 64 + 8 * j)) = pack8(yh);
+    } else {
+      *gmem(reinterpret_cast<u32x4*>(q + 8 * j)) = u32x4{ylp[0], ylp[1], ylp[2], ylp[3]};
+      *gmem(reinterpret_cast<u32x4*>(q + 64 + 8 * j)) = u32x4{yhp[0], yhp[1], yhp[2], yhp[3]};
+    }
     return;
   }
 
@@ -159,8 +199,8 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeArgs ra) {
     const size_t cslot = (hs * p.seq_len + tok) * 128;
     uint16_t* kc = reinterpret_cast<uint16_t*>(p.k_copy) + cslot;
     uint16_t* vc = reinterpret_cast<uint16_t*>(p.v_copy) + cslot;
-    *gmem(reinterpret_cast<u32x4*>(kc + 8 * j)) = pack8(yl);
-    *gmem(reinterpret_cast<u32x4*>(kc + 64 + 8 * j)) = pack8(yh);
+    *gmem(reinterpret_cast<u32x4*>(kc + 8 * j)) = u32x4{ylp[0], ylp[1], ylp[2], ylp[3]};
+    *gmem(reinterpret_cast<u32x4*>(kc + 64 + 8 * j)) = u32x4{yhp[0], yhp[1], yhp[2], yhp[3]};
     *gmem(reinterpret_cast<u32x4*>(vc + 8 * j)) = pack8(vl);
     *gmem(reinterpret_cast<u32x4*>(vc + 64 + 8 * j)) = pack8(vh);
   }
@@ -189,8 +229,8 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeArgs ra) {
   if (!writes) return;
   uint16_t* kc = reinterpret_cast<uint16_t*>(p.k_cache) + slot;
   uint16_t* vc = reinterpret_cast<uint16_t*>(p.v_cache) + slot;
-  *gmem(reinterpret_cast<u32x4*>(kc + 8 * j)) = pack8(yl);
-  *gmem(reinterpret_cast<u32x4*>(kc + 64 + 8 * j)) = pack8(yh);
+  *gmem(reinterpret_cast<u32x4*>(kc + 8 * j)) = u32x4{ylp[0], ylp[1], ylp[2], ylp[3]};
+  *gmem(reinterpret_cast<u32x4*>(kc + 64 + 8 * j)) = u32x4{yhp[0], yhp[1], yhp[2], yhp[3]};
   *gmem(reinterpret_cast<u32x4*>(vc + 8 * j)) = pack8(vl);
   *gmem(reinterpret_cast<u32x4*>(vc + 64 + 8 * j)) = pack8(vh);
 }
