@@ -552,7 +552,7 @@ def measure_projection(fmt, name, m, reps):
     def run():
         for t in ws:
             linear(x, t, swiglu=sw)
-    us = timed_step(run, reps, 2) / len(ws)
+    us = timed_step(run, reps, 5) / len(ws)  # steady state: the first replays of a process run slower
     alg = per + m * k * 2 + m * (n // 2 if sw else n) * 2
     log(f"{fmt} {name} M={m}: {us:.2f} us per call, {alg / us / 1e3:.0f} GB/s ({len(ws)} weights)")
     return {"fmt": fmt, "projection": name, "m": m, "us": round(us, 2), "alg_MB": round(alg / 1e6, 3),
