@@ -326,7 +326,7 @@ def test_skinny_gemm_matches_decode_kernel_and_oracle(fmt, n, k, sw):
         deq = O.dequantize(O.unpack_int4_k32(q.cpu().numpy()), bits16(s), bits=4, scale_dtype="bf16")
     else:
         deq = O.dequantize(q.cpu().numpy(), bits16(s)[:, None], bits=8, scale_dtype="bf16", storage="signed")
-    for m in (9, 17, 33, 64):
+    for m in (9, 16, 17, 33, 64):
         x = acts(m, k, 700 + m).to(DEV)
         ys = linear(x, tiled, swiglu=sw)
         yd = linear(x, tiled, swiglu=sw, skinny=False)
@@ -402,3 +402,4 @@ def test_skinny_token_blocks_bit_identical(m, n, k, sw):
     _lib.call("qlx_linear_skinny", _lib.FMT_W4A16, _lib.ptr(tiled.weight), _lib.ptr(tiled.scale), _lib.ptr(x),
               _lib.ptr(y8), m, n, k, ctypes.byref(plan), _lib.stream(x.device))
     assert torch.equal(ys, y8), (m, n, k)
+
