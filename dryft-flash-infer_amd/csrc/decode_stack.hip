@@ -25,10 +25,11 @@
 //     needs until their epoch is the current run's. A dependency costs one store-to-load
 //     trip instead of a store, its acknowledgement, a counter update and a counter poll.
 //     Every run has a new nonzero epoch, so words left by earlier runs never match. The
-//     epoch lives in the arena's first words: each workgroup reads the last run's epoch at
-//     its start and uses the next one; the workgroup that finishes last (a ticket) stores it.
-//     The launch takes no per-run argument, so a run captures into a HIP graph and every
-//     replay is a new run.
+//     epoch lives in the arena's first words, one per workgroup: each workgroup reads the
+//     last run's at its start, uses the next one and stores it at its end. Every workgroup
+//     runs every run, so all of them hold the same epoch, and none waits at its end for a
+//     shared counter. The launch takes no per-run argument, so a run captures into a HIP graph
+//     and every replay is a new run.
 //   * Every wait is bounded by a per-run deadline on the 100 MHz real-time counter: a wait
 //     past it sets the error flag and moves on (that run's outputs are undefined), so the
 //     kernel always ends. The grid is one workgroup per CU per lane and the planner checks
@@ -42,7 +43,8 @@
 namespace qlx {
 
 constexpr int kMaxPieces = 4;  // pieces of one row block (the reducer has all in flight)
-constexpr long long kArenaCtlBytes = 256;  // arena head: {last run's epoch, finish ticket}
+constexpr int kMaxGrid = 1024;  // workgroups of one launch (one epoch word each)
+constexpr long long kArenaCtlBytes = 4 * kMaxGrid;  // arena head: each workgroup's last run epoch
 
 // One projection of the chain, as the executor reads it (from LDS when the chain's
 // descriptors fit next to the items' LDS: read once per launch instead of missing the
@@ -899,11 +901,6 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
   extern __shared__ __align__(16) char lds[];
   const int per_lane = gridDim.x / lanes;
   const int lane = blockIdx.x / per_lane, p = blockIdx.x - lane * per_lane;
-  // This run's epoch: the next after the last finished run's, skipping low 16 bits of 0 (the
-  // tag of a zeroed arena).
-  uint32_t epoch = __hip_atomic_load(gmem(ctl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-  if ((epoch & 0xffffu) == 0u) epoch += 1u;
-  const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   constexpr bool MAXIMA = std::is_same<F, FmtFP8>::value;  // published row-block maxima
   uint32_t* amax = reinterpret_cast<uint32_t*>(lds + amax_off);  // FP8 staging: per-token maxima
   if (threadIdx.x < 16) amax[threadIdx.x] = 0u;
@@ -915,6 +912,12 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
     for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
     calls = reinterpret_cast<const StackDesc*>(lds + desc_off);
   }
+  // This run's epoch: the next after this workgroup's last run's, skipping low 16 bits of 0
+  // (the tag of a zeroed arena). Read after the descriptors, so that the first weight prefetch
+  // (which needs them, not the epoch) does not wait for this device-scope load.
+  uint32_t epoch = __hip_atomic_load(gmem(ctl + blockIdx.x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  if ((epoch & 0xffffu) == 0u) epoch += 1u;
+  const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   __syncthreads();
   ExecItem cur, nxt;
   uint4 buf[ExecDepth<F, PIECES>::PF][F::LOADS];
@@ -951,15 +954,8 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
     if (have) exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
     __syncthreads();  // LDS is reused by the next item
   }
-  // The last workgroup to finish hands this run's epoch to the next run. Every workgroup read
-  // the previous one at its start, before it took its ticket here.
-  if (threadIdx.x == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(gmem(ctl + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == gridDim.x - 1) {
-      __hip_atomic_store(gmem(ctl + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gmem(ctl), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  // This run's epoch for this workgroup's next run (no wait: nothing here reads it back).
+  if (threadIdx.x == 0) __hip_atomic_store(gmem(ctl + blockIdx.x), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <class F, int WAVES>
@@ -1222,6 +1218,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   std::vector<StackPlan> sp(ncalls);
   int lds = 0, lanes = groups_per_cu, desc_lds = -1, amax_off = 0;
   const int P = cus;  // workgroups per lane
+  QLX_REQUIRE(P >= 1 && (long long)P * lanes <= kMaxGrid, "%d CUs x %d lanes exceed %d workgroups", P, lanes, kMaxGrid);
   const long long desc_bytes = (long long)ncalls * sizeof(StackDesc);
   // Plan for P workgroups, then shrink P to what fits the CUs with that LDS; repeat until
   // plan and grid agree. LDS: [items][64 B of FP8 row maxima][descriptors, if they fit].
@@ -1278,7 +1275,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     return a.rt;
   };
   // Arena: published outputs (and their maxima) and partial sums, 256-byte aligned regions.
-  long long off = kArenaCtlBytes;  // [0, 256): the run epoch and the finish ticket
+  long long off = kArenaCtlBytes;  // [0, 4 kMaxGrid): each workgroup's last run epoch
   std::vector<long long> wire_off(ncalls, -1), part_off(ncalls, -1), max_off(ncalls, -1), rpub_off(ncalls, -1);
   for (int c = 0; c < ncalls; ++c) {
     if (published[c]) {
@@ -1374,7 +1371,8 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
 
 int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch* launch, void* arena, int* error,
                   long long budget_us, void* stream) {
-  QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1,
+  QLX_REQUIRE(launch != nullptr && (launch->waves == 4 || launch->waves == 8) && launch->grid >= 1 &&
+                  launch->grid <= kMaxGrid,
               "bad executor launch configuration");
   QLX_REQUIRE(launch->pieces == 0 || launch->pieces == 1, "launch.pieces must be 0 or 1 (got %d)", launch->pieces);
   const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0, launch->pieces != 0);

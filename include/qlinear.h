@@ -314,15 +314,16 @@ typedef struct qlx_stack_launch {
  * Outputs must not overlap each other or an input read from memory (EINVAL otherwise).
  * Replaces the reference's per-projection launches chained by programmatic dependent launch
  * inside a captured graph (engine/kernels/cuda_fp8.py:47-50, 150-169;
- * engine/kernels/cuda_jit.py:218-262): here the whole chain is one launch. The arena's first
- * 256 bytes hold the run epoch and a finish counter (zero in a fresh arena). */
+ * engine/kernels/cuda_jit.py:218-262): here the whole chain is one launch (at most 1024
+ * workgroups). The arena's first 4096 bytes hold each workgroup's last run epoch (zero in a fresh
+ * arena). */
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
                     void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch);
 
 /* Run the chain: `desc` is the device copy of qlx_stack_build's descriptors, `launch` its
  * launch configuration and `arena` the arena they were built for (256-byte aligned). Each run
- * tags what it publishes with the next epoch after the one the arena holds and stores it there
- * when its last workgroup finishes, so the call has no per-run argument and captures into a
+ * tags what it publishes with the next epoch after the one the arena holds (every workgroup
+ * reads and stores its own copy), so the call has no per-run argument and captures into a
  * hipGraph (every replay is a new run). `error` is one int32 in device memory, zero before the
  * run: once a wait passes `budget_us` microseconds from the run's start, every wait gives up,
  * the first one writing (1 << kind) to it (0: an input from an earlier projection, 1: a
