@@ -283,6 +283,36 @@ class Model:
                 segments[i + 1].run()
         return step
 
+    def executor_one_launch(self, splits=4):
+        """The same decode step as ONE executor launch (m = 1): each layer's attention is a stage
+        of the chain (DecodeStack.add_attention: head norm + RoPE + cache write, split attention
+        and its merge) between qkv and o, so no launch boundary remains inside the step."""
+        from kernels.decode_stack import DecodeStack
+        new = lambda n: torch.empty((self.m, n), dtype=torch.bfloat16, device="cuda")
+        chain = DecodeStack(self.fmt, self.m, waves=EXECUTOR_WAVES)
+        qkv, r0 = new(6144), new(HIDDEN)
+        chain.add_normed(self.w[0]["qkv"].tiles, self.h, qkv, self.norm_in[0], EPS, resid_out=r0)
+        self.one_keep, resid = [qkv, r0], r0
+        for i in range(self.layers):
+            w = self.w[i]
+            att, o, act, down, r1, r2 = new(4096), new(HIDDEN), new(9728), new(HIDDEN), new(HIDDEN), new(HIDDEN)
+            chain.add_attention(qkv, 32, 8, self.q_norm[i], self.k_norm[i], self.cos, self.sin, self.positions,
+                                self.k_cache[i], self.v_cache[i], att, EPS, splits=splits)
+            chain.add(w["o"].tiles, att, o)
+            chain.add_normed(w["gate_up"].tiles, resid, act, self.norm_post[i], EPS, delta=o, resid_out=r1,
+                             swiglu=True)
+            chain.add(w["down"].tiles, act, down)
+            if i + 1 < self.layers:
+                qkv = new(6144)
+                chain.add_normed(self.w[i + 1]["qkv"].tiles, r1, qkv, self.norm_in[i + 1], EPS, delta=down,
+                                 resid_out=r2)
+            else:
+                self.logits1 = new(LM_HEAD[1])
+                chain.add_normed(self.lm_head.tiles, r1, self.logits1, self.norm_out, EPS, delta=down, resid_out=r2)
+            self.one_keep += [att, o, act, down, r1, r2, qkv]
+            resid = r2
+        return chain.build()
+
     def attention_only(self):
         """The step's rope + attention calls alone (the same calls as in the steps above)."""
         from kernels import qkv_norm_rope_to_cache

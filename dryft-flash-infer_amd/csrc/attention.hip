@@ -28,7 +28,7 @@
 // wave's first block can be fetched before the position arrives, and the grid stays fixed for
 // graph capture. A short context uses fewer splits (one block per wave at least); with one,
 // the workgroup writes the output itself.
-#include "common.h"
+#include "attn_common.h"
 #include "../../include/qlinear.h"
 
 #include <algorithm>
@@ -46,124 +46,6 @@ struct AttnArgs {
   float* pacc;         // split partials: [B*H][S][R][128], then maxima and totals [B*H][S][R]
   float scale2;        // head_dim^-0.5 * log2(e)
   int cap, splits, T, G, H, R, heads;
-};
-
-constexpr float kNegInf = -__builtin_inff();
-
-__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Dim slot of MFMA k-step s for lane group g. The order inside a product is free as long as
-// the query and key fragments agree: bf16 keys take dims 32 s + 8 g (each load instruction
-// reads 64 consecutive bytes of 16 keys), INT8 keys 32 g + 8 s (a lane's four steps are 32
-// consecutive bytes, two 16-byte loads).
-template <bool Q8>
-__device__ __forceinline__ int kdim(int s, int g) { return Q8 ? 32 * g + 8 * s : 32 * s + 8 * g; }
-
-// Key of slot j (0..7) of lane group g in a 32-key block: the keys the S^T fragment leaves
-// in that lane (key tile j / 4, row 4 g + j % 4).
-__device__ __forceinline__ int slot_key(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
-
-typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
-
-__device__ __forceinline__ bf16x8 bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
-
-template <bool Q8>
-struct KVBlock;
-
-template <>
-struct KVBlock<false> {
-  u32x4 k[2][4];  // [key tile][k-step]: 8 dims of key 16 kt + n
-  u32x4 v[8];     // [slot]: V[key(slot)][8 n .. 8 n + 7]
-  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int kcap, int n, int g) {
-    const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + hb;
-    const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + hb;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int key = min(kb + 16 * kt + n, kcap - 1);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) k[kt][s] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + kdim<false>(s, g)));
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = min(kb + slot_key(g, j), kcap - 1);
-      v[j] = *gmem(reinterpret_cast<const u32x4*>(V + (size_t)key * 128 + 8 * n));
-    }
-  }
-  __device__ __forceinline__ void zero_from(int kb, int end, int g) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (kb + slot_key(g, j) >= end) v[j] = u32x4{0u, 0u, 0u, 0u};
-  }
-  __device__ __forceinline__ u32x4 kfrag(int kt, int s) const { return k[kt][s]; }
-  // Column c (0..7) of the lane's 8 keys x 8 dims block: 8 keys of dim 8 n + c, slot order.
-  __device__ __forceinline__ u32x4 vfrag(int c) const {
-    uint32_t d[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = reinterpret_cast<const uint32_t*>(&v[2 * q])[c >> 1];
-      const uint32_t hi = reinterpret_cast<const uint32_t*>(&v[2 * q + 1])[c >> 1];
-      d[q] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-    }
-    return u32x4{d[0], d[1], d[2], d[3]};
-  }
-};
-
-// INT8 cache: codes with one fp32 scale per (token, head); each value is dequantised to
-// bf16(code * scale) as it is loaded (attention.py:94-99).
-template <>
-struct KVBlock<true> {
-  u32x4 k[2][2];  // [key tile][half]: dims 32 g .. 32 g + 31 of key 16 kt + n
-  u32x2 v[8];     // [slot]: codes of V[key(slot)][8 n .. 8 n + 7]
-  float ksc[2], vsc[8];
-  __device__ __forceinline__ void load(const AttnArgs& a, size_t hb, int kb, int kcap, int n, int g) {
-    const int8_t* K = reinterpret_cast<const int8_t*>(a.k) + hb;
-    const int8_t* V = reinterpret_cast<const int8_t*>(a.v) + hb;
-    const size_t sb = hb >> 7;  // scale index of key 0 of this head
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int key = min(kb + 16 * kt + n, kcap - 1);
-      k[kt][0] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g));
-      k[kt][1] = *gmem(reinterpret_cast<const u32x4*>(K + (size_t)key * 128 + 32 * g + 16));
-      ksc[kt] = gmem(a.ks)[sb + key];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = min(kb + slot_key(g, j), kcap - 1);
-      v[j] = *gmem(reinterpret_cast<const u32x2*>(V + (size_t)key * 128 + 8 * n));
-      vsc[j] = gmem(a.vs)[sb + key];
-    }
-  }
-  __device__ __forceinline__ void zero_from(int kb, int end, int g) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (kb + slot_key(g, j) >= end) {
-        v[j] = u32x2{0u, 0u};
-        vsc[j] = 0.f;
-      }
-  }
-  static __device__ __forceinline__ float deq(uint32_t w, int b, float sc) {
-    return round_bf((float)(int)(int8_t)(w >> (8 * b)) * sc);
-  }
-  __device__ __forceinline__ u32x4 kfrag(int kt, int s) const {
-    const uint32_t* c = reinterpret_cast<const uint32_t*>(&k[kt][s >> 1]) + 2 * (s & 1);
-    const float sc = ksc[kt];
-    return u32x4{pack_bf(deq(c[0], 0, sc), deq(c[0], 1, sc)), pack_bf(deq(c[0], 2, sc), deq(c[0], 3, sc)),
-                 pack_bf(deq(c[1], 0, sc), deq(c[1], 1, sc)), pack_bf(deq(c[1], 2, sc), deq(c[1], 3, sc))};
-  }
-  __device__ __forceinline__ u32x4 vfrag(int c) const {
-    uint32_t d[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t w0 = reinterpret_cast<const uint32_t*>(&v[2 * q])[c >> 2];
-      const uint32_t w1 = reinterpret_cast<const uint32_t*>(&v[2 * q + 1])[c >> 2];
-      d[q] = pack_bf(deq(w0, c & 3, vsc[2 * q]), deq(w1, c & 3, vsc[2 * q + 1]));
-    }
-    return u32x4{d[0], d[1], d[2], d[3]};
-  }
 };
 
 // RT tiles of 16 query rows (R <= 16 RT). 256 threads; dynamic LDS 4 x R x 128 fp32.
@@ -185,7 +67,8 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   const int j0 = part + a.splits * w;
   constexpr bool PF = RT <= 2;  // prefetch the next block (registers allow it up to 2 row tiles)
   KVBlock<Q8> cur, nxt;
-  if (PF && 32 * j0 < a.cap) cur.load(a, hb, 32 * j0, a.cap, n, g);
+  const KVSrc kv{a.k, a.v, a.ks, a.vs};
+  if (PF && 32 * j0 < a.cap) cur.load(kv, hb, 32 * j0, a.cap, n, g);
 
   // Query fragments (B operand of S^T = K Q^T): row 16 rt + n, dims kdim(s, g). Up to two row
   // tiles live in registers; more are read from LDS each block (the four waves share them),
@@ -223,7 +106,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
   if (part >= se) return;
   const int j1 = part + se * w, jstep1 = 4 * se;
   const int nb = j1 < nblk ? (nblk - j1 + jstep1 - 1) / jstep1 : 0;  // this wave's blocks
-  if (PF && j1 != j0 && nb > 0) cur.load(a, hb, 32 * j1, a.cap, n, g);
+  if (PF && j1 != j0 && nb > 0) cur.load(kv, hb, 32 * j1, a.cap, n, g);
   // Last live key + 1 of row 16 rt + n (padding rows: every live key).
   int lim[RT];
 #pragma unroll
@@ -310,15 +193,15 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
       // (sched_barrier: the scheduler would otherwise sink the prefetch below the first
       // products of the current block, behind a wait for every load in flight)
       for (; i + 2 < nb; i += 2) {
-        nxt.load(a, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
+        nxt.load(kv, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
         __builtin_amdgcn_sched_barrier(0);
         run(cur, j1 + jstep1 * i);
-        cur.load(a, hb, 32 * (j1 + jstep1 * (i + 2)), a.cap, n, g);
+        cur.load(kv, hb, 32 * (j1 + jstep1 * (i + 2)), a.cap, n, g);
         __builtin_amdgcn_sched_barrier(0);
         run(nxt, j1 + jstep1 * (i + 1));
       }
       if (i + 1 < nb) {
-        nxt.load(a, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
+        nxt.load(kv, hb, 32 * (j1 + jstep1 * (i + 1)), a.cap, n, g);
         __builtin_amdgcn_sched_barrier(0);
         run(cur, j1 + jstep1 * i);
         run(nxt, j1 + jstep1 * (i + 1));
@@ -328,7 +211,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
     }
   } else {
     for (int i = 0; i < nb; ++i) {
-      cur.load(a, hb, 32 * (j1 + jstep1 * i), a.cap, n, g);
+      cur.load(kv, hb, 32 * (j1 + jstep1 * i), a.cap, n, g);
       run(cur, j1 + jstep1 * i);
     }
   }

@@ -38,7 +38,9 @@
 //     than hang.
 #include <vector>
 
+#include "attn_common.h"
 #include "exec_common.h"
+#include "rope_common.h"
 
 namespace qlx {
 
@@ -86,6 +88,9 @@ struct alignas(16) StackDesc {
   void* nout;
   uint64_t* rpub;
   float eps;
+  // 0: a projection. 1: the splits of an attention stage, 2: their merge (see exec_attention;
+  // GemmArgs fields hold that stage's parameters there).
+  int kind;
 };
 
 constexpr int kMaxLine = 32;  // maxima words per row block: one 128-byte line
@@ -840,6 +845,316 @@ __device__ __forceinline__ void exec_finish(const StackDesc& d, char* lds, const
   }
 }
 
+// ---- attention stage ---------------------------------------------------------------------
+//
+// One token (m = 1, batch 1), head_dim 128, bf16 caches, G = n_q / n_kv = 4 query heads per KV
+// head. The stage's parameters sit in the descriptor's GemmArgs: w, ws = cos, sin tables;
+// resid, norm_w = q and k norm gains; res_out, normed = k and v caches; tickets = the position
+// (int32); n = capacity; k = table rows; half = n_q; group = n_kv; splits = items per KV head;
+// eps = the RMSNorm epsilon; the descriptor's eps = head_dim^-0.5 * log2(e). xwire = the
+// published qkv row; part = the splits' partials, kAttnWords 64-bit words per (KV head, split,
+// query row): the accumulator's 128 values, the maximum, the total.
+constexpr int kAttnWords = 130;
+constexpr int kAttnG = 4;  // query heads per KV head (query rows of an item)
+
+// LDS of an attention item: the KV head's q/k/v values [6][128] bf16 (2 KB), then the waves'
+// accumulators [waves][4][128] and their maxima and totals [waves][4] (fp32).
+__host__ __device__ inline int attn_lds_bytes(int waves) { return 2048 + waves * kAttnG * 130 * 4 + 2 * waves * kAttnG * 4; }
+
+// Splits item (KV head kvh, split part): poll the KV head's q, k, v words; head norm + RoPE of
+// the 4 query heads and the key (rope_norm_rotate: the arithmetic of qlx_qkv_norm_rope); the item
+// that reads the key's block writes k and v into the caches at the position; then S^T = K Q^T,
+// the online softmax and P V over the item's blocks (block j = part + S (wave + waves i)), with
+// the arithmetic of attn_kernel (the new key's values taken from LDS where its block was read
+// from memory before they were written); the waves merged through LDS; the item's partials
+// published.
+template <int WAVES>
+__device__ __forceinline__ void exec_attention(const StackDesc& d, char* lds, int item, const Waits& w) {
+  const GemmArgs& a = d.a;
+  const int S = a.splits, NQ = a.half, H = a.group, cap = a.n;
+  const int kvh = item / S, part = item - kvh * S;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  uint16_t* hs = reinterpret_cast<uint16_t*>(lds);  // [6][128]: q heads 0..3, k, v of the KV head
+  float* wacc = reinterpret_cast<float*>(lds + 2048);
+  float* wm = wacc + WAVES * kAttnG * 128;
+  float* wl = wm + WAVES * kAttnG;
+  // Loads in the order they are needed (memory operations complete in order): the position,
+  // the KV head's words (6 heads x 16 chunks of 8 values, one chunk per thread), this wave's
+  // first block (its index does not depend on the position), then the rotation inputs.
+  const int pos0 = *gmem(reinterpret_cast<const int*>(a.tickets));
+  const XWire xs(d.xwire, d.xpitch, 1, w);
+  XWire::Raw r;
+  const int hsl = tid >> 4, c8 = tid & 15;
+  const bool poll = tid < 96;
+  const int col = (hsl < 4 ? (kvh * kAttnG + hsl) * 128 : (NQ + (hsl == 4 ? 0 : H) + kvh) * 128) + 8 * c8;
+  if (poll) xs.fetch(a, 0, col, r);
+  const int j1 = part + S * wv, jstep = S * WAVES;
+  const size_t hb = (size_t)kvh * cap * 128;
+  const KVSrc kv{a.res_out, a.normed, nullptr, nullptr};
+  KVBlock<false> cur;
+  if (32 * j1 < cap) cur.load(kv, hb, 32 * j1, cap, n, g);
+  const int pos = __builtin_amdgcn_readfirstlane(pos0);
+  const int end = min(pos + 1, cap);  // keys at or past end are live for no row
+  const int nblk = end > 0 ? (end + 31) >> 5 : 0;
+  const int nb = j1 < nblk ? (nblk - j1 + jstep - 1) / jstep : 0;
+  // Rotation inputs of wave 0's lanes 8 h + j (h = 0..3: query heads, 4: the key).
+  const bool in_table = pos >= 0 && pos < a.k;
+  const int hr = min(lane >> 3, 4), jr = lane & 7;
+  float cl[8], ch[8], sl[8], sh[8], gl[8], gh[8];
+  if (wv == 0) {
+    const size_t tp = (size_t)(in_table ? pos : 0) * 128;
+    const uint16_t* cs = reinterpret_cast<const uint16_t*>(a.w) + tp;
+    const uint16_t* sn = reinterpret_cast<const uint16_t*>(a.ws) + tp;
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(cs + 8 * jr)), cl);
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(cs + 64 + 8 * jr)), ch);
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(sn + 8 * jr)), sl);
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(sn + 64 + 8 * jr)), sh);
+    const uint16_t* gain = reinterpret_cast<const uint16_t*>(hr < 4 ? a.resid : a.norm_w);
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(gain + 8 * jr)), gl);
+    unpack8(*gmem(reinterpret_cast<const u32x4*>(gain + 64 + 8 * jr)), gh);
+  }
+  if (poll) {
+    while (!xs.ready(r) && !xs.expired()) {
+      __builtin_amdgcn_s_sleep(1);
+      xs.refetch(a, 0, col, r);
+    }
+    const uint4 v = xs.value(r);
+    *reinterpret_cast<u32x4*>(hs + hsl * 128 + 8 * c8) = u32x4{v.x, v.y, v.z, v.w};
+  }
+  __syncthreads();
+  // The item holding the key's block (when the key is written at all) writes k and v.
+  const bool writes = in_table && pos < cap;
+  const bool owner = writes && ((pos >> 5) % S) == part;
+  if (wv == 0) {
+    float xl[8], xh[8], yl[8], yh[8];
+    uint32_t ylp[4], yhp[4];
+    unpack8(*reinterpret_cast<const u32x4*>(hs + hr * 128 + 8 * jr), xl);
+    unpack8(*reinterpret_cast<const u32x4*>(hs + hr * 128 + 64 + 8 * jr), xh);
+    rope_norm_rotate(xl, xh, gl, gh, cl, ch, sl, sh, a.eps, yl, yh, ylp, yhp);
+    if (lane < 40) {
+      u32x4 lo = u32x4{ylp[0], ylp[1], ylp[2], ylp[3]}, hi = u32x4{yhp[0], yhp[1], yhp[2], yhp[3]};
+      if (!in_table) {  // outside the cos/sin table: the query reads as NaN
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yl[i] = yh[i] = __builtin_nanf("");
+        lo = pack8(yl);
+        hi = pack8(yh);
+      }
+      if (hr < 4 || writes) {  // (a key that is not written leaves the cache's values in place)
+        *reinterpret_cast<u32x4*>(hs + hr * 128 + 8 * jr) = lo;
+        *reinterpret_cast<u32x4*>(hs + hr * 128 + 64 + 8 * jr) = hi;
+      }
+    } else if (lane < 56) {  // the value row, as the cache stores it (bf16 of its bf16 values)
+      const int c = lane - 40;
+      float f[8];
+      unpack8(*reinterpret_cast<const u32x4*>(hs + 5 * 128 + 8 * c), f);
+      *reinterpret_cast<u32x4*>(hs + 5 * 128 + 8 * c) = pack8(f);
+    }
+  }
+  __syncthreads();
+  if (owner && tid < 32) {  // k, then v: 16 chunks each
+    const int which = tid >> 4, c = tid & 15;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(which ? a.normed : a.res_out) + hb + (size_t)pos * 128 + 8 * c;
+    *gmem(reinterpret_cast<u32x4*>(dst)) = *reinterpret_cast<const u32x4*>(hs + (4 + which) * 128 + 8 * c);
+  }
+  // Query fragments: row n (query head G kvh + n for n < 4), dims kdim(s, g).
+  u32x4 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    qf[s] = n < kAttnG ? *reinterpret_cast<const u32x4*>(hs + n * 128 + kdim<false>(s, g)) : u32x4{0u, 0u, 0u, 0u};
+  const int lim = end;  // one token: every query row sees keys 0 .. pos
+  float m = kNegInf, l = 0.f;
+  f32x4 acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The block holding the key read the cache before the key was written: its values come from
+  // LDS (the ones just written to the cache).
+  auto patch = [&](KVBlock<false>& b, int kb) __attribute__((always_inline)) {
+    if (!writes || pos < kb || pos >= kb + 32) return;
+    const int o = pos - kb;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+      if (o == 16 * kt + n) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b.k[kt][s] = *reinterpret_cast<const u32x4*>(hs + 4 * 128 + kdim<false>(s, g));
+      }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (slot_key(g, j) == o) b.v[j] = *reinterpret_cast<const u32x4*>(hs + 5 * 128 + 8 * n);
+  };
+  auto compute = [&](const KVBlock<false>& b, int kb) __attribute__((always_inline)) {
+    f32x4 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf8(b.kfrag(kt, s)), bf8(qf[s]), st[kt], 0, 0, 0);
+    }
+    float sc[8], bm = kNegInf;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + 16 * kt + 4 * g + i;
+        sc[4 * kt + i] = key < lim ? st[kt][i] * d.eps : kNegInf;
+        bm = fmaxf(bm, sc[4 * kt + i]);
+      }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float mu = mn == kNegInf ? 0.f : mn;
+    const float carry = ex2(m - mu);
+    m = mn;
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = ex2(sc[j] - mu);
+      ps += p[j];
+    }
+    l = l * carry + ps;
+    const u32x4 pf = u32x4{pack_bf(p[0], p[1]), pack_bf(p[2], p[3]), pack_bf(p[4], p[5]), pack_bf(p[6], p[7])};
+    float cr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cr[i] = __shfl(carry, 4 * g + i, 64);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      f32x4 t = acc[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] *= cr[i];
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf8(pf), bf8(b.vfrag(c)), t, 0, 0, 0);
+    }
+  };
+  auto run = [&](KVBlock<false>& b, int j) __attribute__((always_inline)) {
+    const int kb = 32 * j;
+    patch(b, kb);
+    if (kb + 32 > end) b.zero_from(kb, end, g);
+    compute(b, kb);
+  };
+  // One block in registers at a time (the executor's registers are its weight pipeline's): at
+  // decode lengths a wave has one or two blocks, the first fetched at the item's start.
+  for (int i = 0; i < nb; ++i) {
+    if (i > 0) cur.load(kv, hb, 32 * (j1 + jstep * i), cap, n, g);
+    run(cur, j1 + jstep * i);
+  }
+  // Merge the waves (maxima and totals, then each accumulator rescaled to the item's maximum,
+  // summed over waves in order) and publish the item's partial of each query row.
+  {
+    float lt = l + __shfl_xor(l, 16, 64);
+    lt = lt + __shfl_xor(lt, 32, 64);
+    if (g == 0 && n < kAttnG) {
+      wm[wv * kAttnG + n] = m;
+      wl[wv * kAttnG + n] = lt;
+    }
+  }
+  __syncthreads();
+  if (g == 0) {  // rows 4 g + i = i: lanes 0..15 hold rows 0..3 of dims 8 n + c
+#pragma unroll
+    for (int i = 0; i < kAttnG; ++i) {
+      float M = kNegInf;
+#pragma unroll
+      for (int q = 0; q < WAVES; ++q) M = fmaxf(M, wm[q * kAttnG + i]);
+      const float f = wm[wv * kAttnG + i] == kNegInf ? 0.f : ex2(wm[wv * kAttnG + i] - M);
+      float* dst = wacc + ((size_t)wv * kAttnG + i) * 128 + 8 * n;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dst[c] = acc[c][i] * f;
+    }
+  }
+  __syncthreads();
+  uint64_t* out = d.part + ((size_t)kvh * S + part) * kAttnG * kAttnWords;
+  for (int idx = tid; idx < kAttnG * kAttnWords; idx += WAVES * 64) {
+    const int row = idx / kAttnWords, e = idx - row * kAttnWords;
+    float M = kNegInf;
+#pragma unroll
+    for (int q = 0; q < WAVES; ++q) M = fmaxf(M, wm[q * kAttnG + row]);
+    float v;
+    if (e < 128) {
+      v = 0.f;
+#pragma unroll
+      for (int q = 0; q < WAVES; ++q) v += wacc[((size_t)q * kAttnG + row) * 128 + e];
+    } else if (e == 128) {
+      v = M;
+    } else {
+      v = 0.f;
+#pragma unroll
+      for (int q = 0; q < WAVES; ++q) {
+        const float mq = wm[q * kAttnG + row];
+        v += mq == kNegInf ? 0.f : wl[q * kAttnG + row] * ex2(mq - M);
+      }
+    }
+    ll_store(out + idx, __float_as_uint(v), w.epoch);
+  }
+}
+
+// Merge item: query row qr (query head qr of the token, KV head qr / 4): every split's partial
+// polled, then combined as attn_merge_kernel does -- weights exp(max_s - max), weighted
+// accumulators over weighted totals, splits in order -- and the row written to y and, for later
+// projections, published.
+template <int WAVES>
+__device__ __forceinline__ void exec_merge(const StackDesc& d, int qr, const Waits& w) {
+  const GemmArgs& a = d.a;
+  const int S = a.splits, kvh = qr / kAttnG, row = qr - kvh * kAttnG;
+  const int t = threadIdx.x;
+  if (t >= 128) return;
+  const uint64_t* base = d.part + ((size_t)kvh * S * kAttnG + row) * kAttnWords;
+  constexpr int kMaxS = 4;  // splits polled together
+  float M = kNegInf, L = 0.f, A = 0.f;
+  for (int s0 = 0; s0 < S; s0 += kMaxS) {
+    uint64_t av[kMaxS], mv[kMaxS], lv[kMaxS];
+#pragma unroll
+    for (int j = 0; j < kMaxS; ++j) {
+      if (s0 + j >= S) continue;
+      const uint64_t* p = base + (size_t)(s0 + j) * kAttnG * kAttnWords;
+      av[j] = ll_load(p + t);
+      mv[j] = ll_load(p + 128);
+      lv[j] = ll_load(p + 129);
+    }
+    auto ok = [&](uint64_t x) { return (uint32_t)(x >> 32) == w.epoch; };
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int j = 0; j < kMaxS; ++j)
+        if (s0 + j < S && !(ok(av[j]) && ok(mv[j]) && ok(lv[j]))) all = false;
+      if (all || ll_expired(w, kWaitInput)) break;
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int j = 0; j < kMaxS; ++j) {
+        if (s0 + j >= S) continue;
+        const uint64_t* p = base + (size_t)(s0 + j) * kAttnG * kAttnWords;
+        if (!ok(av[j])) av[j] = ll_load(p + t);
+        if (!ok(mv[j])) mv[j] = ll_load(p + 128);
+        if (!ok(lv[j])) lv[j] = ll_load(p + 129);
+      }
+    }
+    float Mb = M;
+#pragma unroll
+    for (int j = 0; j < kMaxS; ++j)
+      if (s0 + j < S) Mb = fmaxf(Mb, __uint_as_float((uint32_t)mv[j]));
+    const float Mu = Mb == kNegInf ? 0.f : Mb;
+    const float c = M == kNegInf ? 0.f : ex2(M - Mu);
+    A *= c;
+    L *= c;
+#pragma unroll
+    for (int j = 0; j < kMaxS; ++j) {
+      const float mj = __uint_as_float((uint32_t)mv[j]);
+      if (s0 + j >= S || mj == kNegInf) continue;
+      const float f = ex2(mj - Mu);
+      A += f * __uint_as_float((uint32_t)av[j]);
+      L += f * __uint_as_float((uint32_t)lv[j]);
+    }
+    M = Mb;
+  }
+  const float o = A / L;
+  const float o1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(o), 0x101, 0xf, 0xf, false));
+  if ((t & 1) == 0) {
+    const int oi = qr * 128 + t;
+    const uint32_t pair = pack_bf(o, o1);
+    *gmem(reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.y) + oi)) = pair;
+    if (d.ywire) wire_store_pair(d.ywire + (oi >> 1), pair, w.epoch);
+  }
+}
+
 // ---- the chain ---------------------------------------------------------------------------
 
 // The work item after (c, g) for workgroup p of its lane: (c, g + 1) inside its share, else
@@ -894,7 +1209,9 @@ __device__ __forceinline__ NextItem find_next(const StackDesc* calls, int ncalls
   return n;
 }
 
-template <class F, int WAVES, bool DLDS, bool PIECES>
+// ATT: the chain has attention stages (its own instance, so that chains without keep the
+// projection path's registers and code unchanged).
+template <class F, int WAVES, bool DLDS, bool PIECES, bool ATT = false>
 __global__ void __launch_bounds__(WAVES * 64)
 stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, int* err, long long budget_ticks,
              int desc_off, int lanes, int amax_off) {
@@ -925,11 +1242,40 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
   int nc = -1, ng = 0;
   int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
   bool have = next_work(calls, ncalls, lanes, lane, p, nc, ng);
-  if (have) prefetch_work<F, WAVES, PIECES>(calls[nc], p, ng, nxt, buf);
+  if (have) {
+    if (!ATT || calls[nc].kind == 0)
+      prefetch_work<F, WAVES, PIECES>(calls[nc], p, ng, nxt, buf);
+    else
+      nxt.tg = ng;
+  }
   while (have) {
     const int c = nc;
     const StackDesc& d = calls[c];
     cur = nxt;
+    if (ATT && d.kind != 0) {  // an attention stage's item: its splits, or their merge
+      // No weights are in flight for it: the registers of the weight pipeline are free.
+#pragma unroll
+      for (int q = 0; q < ExecDepth<F, PIECES>::PF; ++q)
+#pragma unroll
+        for (int j = 0; j < F::LOADS; ++j) buf[q][j] = uint4{0u, 0u, 0u, 0u};
+      if (d.kind == 1)
+        exec_attention<WAVES>(d, lds, cur.tg, w);
+      else
+        exec_merge<WAVES>(d, cur.tg, w);
+      staged_c = -1;
+      const NextItem after = find_next(calls, ncalls, lanes, lane, p, nc, ng);
+      have = after.have;
+      nc = after.c;
+      ng = after.g;
+      if (have) {
+        if (calls[nc].kind == 0)
+          exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+        else
+          nxt.tg = ng;
+      }
+      __syncthreads();  // LDS is reused by the next item
+      continue;
+    }
     const bool reuse = staged_c == c && staged_step0 == cur.step0 && staged_nst == cur.nst;
     if (d.xwire && !d.nw)
       exec_main<F, WAVES, PIECES>(d.a, XWire(d.xwire, d.xpitch, d.a.m, w), lds, cur, reuse, buf, acc, amax,
@@ -951,7 +1297,12 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
     have = after.have;
     nc = after.c;
     ng = after.g;
-    if (have) exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+    if (have) {
+      if (!ATT || calls[nc].kind == 0)
+        exec_prefetch<F, WAVES, PIECES>(calls[nc].a, ng, after.step0, after.nst, after.piece, after.np, nxt, buf);
+      else
+        nxt.tg = ng;
+    }
     __syncthreads();  // LDS is reused by the next item
   }
   // This run's epoch for this workgroup's next run (no wait: nothing here reads it back).
@@ -959,7 +1310,11 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
 }
 
 template <class F, int WAVES>
-const void* stack_fn2(bool dlds, bool pieces) {
+const void* stack_fn2(bool dlds, bool pieces, bool att) {
+  if (att)  // attention stages: chains without K pieces (one token)
+    return pieces ? nullptr
+                  : dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, true, false, true>)
+                         : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, false, false, true>);
   if (pieces)
     return dlds ? reinterpret_cast<const void*>(&stack_kernel<F, WAVES, true, true>)
                 : reinterpret_cast<const void*>(&stack_kernel<F, WAVES, false, true>);
@@ -968,18 +1323,18 @@ const void* stack_fn2(bool dlds, bool pieces) {
 }
 
 template <class F>
-const void* stack_fn(int waves, bool dlds, bool pieces) {
-  return waves == 8 ? stack_fn2<F, 8>(dlds, pieces) : stack_fn2<F, 4>(dlds, pieces);
+const void* stack_fn(int waves, bool dlds, bool pieces, bool att) {
+  return waves == 8 ? stack_fn2<F, 8>(dlds, pieces, att) : stack_fn2<F, 4>(dlds, pieces, att);
 }
 
 // The kernel for a launch of `waves` (4 or 8) waves per workgroup: `pieces` when some row block
-// of the chain is cut into K pieces.
-const void* stack_fn_for(int fmt, int waves, bool dlds, bool pieces) {
+// of the chain is cut into K pieces, `att` when the chain has attention stages.
+const void* stack_fn_for(int fmt, int waves, bool dlds, bool pieces, bool att = false) {
   if (waves != 4 && waves != 8) return nullptr;
   switch (fmt) {
-    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, dlds, pieces);
-    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, dlds, pieces);
-    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, dlds, pieces);
+    case QLX_FMT_W8A16: return stack_fn<FmtW8>(waves, dlds, pieces, att);
+    case QLX_FMT_W4A16: return stack_fn<FmtW4>(waves, dlds, pieces, att);
+    case QLX_FMT_FP8: return stack_fn<FmtFP8>(waves, dlds, pieces, att);
     default: return nullptr;
   }
 }
@@ -1108,13 +1463,20 @@ int qlx_stack_desc_size(void) { return (int)sizeof(StackDesc); }
 
 int qlx_stack_build(int fmt, int m, const qlx_stack_call* calls, int ncalls, int waves, int groups_per_cu,
                     void* desc, qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch) {
-  return qlx_stack_build_normed(fmt, m, calls, ncalls, nullptr, waves, groups_per_cu, desc, plans, arena,
-                                arena_bytes, launch);
+  return qlx_stack_build_step(fmt, m, calls, ncalls, nullptr, nullptr, waves, groups_per_cu, desc, plans, arena,
+                              arena_bytes, launch);
 }
 
 int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
                            int waves, int groups_per_cu, void* desc, qlx_plan* plans, void* arena,
                            long long* arena_bytes, qlx_stack_launch* launch) {
+  return qlx_stack_build_step(fmt, m, calls, ncalls, norms, nullptr, waves, groups_per_cu, desc, plans, arena,
+                              arena_bytes, launch);
+}
+
+int qlx_stack_build_step(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                         const qlx_stack_attention* attns, int waves, int groups_per_cu, void* desc,
+                         qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch) {
   QLX_REQUIRE(stack_fn_for(fmt, 8, false, false) != nullptr,
               "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(waves == 4 || waves == 8, "waves must be 4 or 8 (got %d)", waves);
@@ -1123,6 +1485,9 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   QLX_REQUIRE(groups_per_cu >= 1 && groups_per_cu <= 4, "groups_per_cu must be 1..4");
   const FmtInfo fi = stack_info(fmt);
   auto normed = [&](int c) { return norms != nullptr && norms[c].norm_w != nullptr; };
+  auto kind = [&](int c) { return attns != nullptr ? attns[c].kind : 0; };
+  // Work items of an attention stage's entry: (KV head, split), or query rows for the merge.
+  auto attn_items = [&](int c) { return kind(c) == 1 ? attns[c].n_kv * attns[c].splits : attns[c].n_q; };
   // Shapes, and which earlier projection (if any) produces each activation. Outputs may not
   // overlap each other or an activation read from memory: the chain has no ordering between
   // projections other than these data dependencies.
@@ -1130,6 +1495,35 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   int css_doubles = 0;  // LDS of the widest norm stage's per-chunk sums
   for (int c = 0; c < ncalls; ++c) {
     const qlx_stack_call& q = calls[c];
+    if (kind(c) != 0) {
+      const qlx_stack_attention& at = attns[c];
+      QLX_REQUIRE(kind(c) == 1 || kind(c) == 2, "entry %d: attention kind %d", c, kind(c));
+      QLX_REQUIRE(m == 1, "entry %d: an attention stage takes one token (m = 1, got %d)", c, m);
+      QLX_REQUIRE(at.n_kv >= 1 && at.n_q == kAttnG * at.n_kv, "entry %d: n_q must be %d x n_kv", c, kAttnG);
+      QLX_REQUIRE(at.splits >= 1 && at.splits <= 64, "entry %d: splits must be 1..64", c);
+      QLX_REQUIRE(at.capacity >= 1 && at.table_rows >= 1 && (long long)at.n_kv * at.capacity * 128 < (1ll << 40),
+                  "entry %d: bad capacity or table rows", c);
+      QLX_REQUIRE(at.q_norm_w && at.k_norm_w && at.cos && at.sin && at.positions && at.k_cache && at.v_cache,
+                  "entry %d: NULL attention pointer", c);
+      QLX_REQUIRE(q.n == at.n_q * 128 && q.mode == QLX_MODE_BF16, "entry %d: n must be n_q x 128, mode bf16", c);
+      if (kind(c) == 1) {
+        QLX_REQUIRE(q.x != nullptr && q.y == nullptr && q.k == (at.n_q + 2 * at.n_kv) * 128,
+                    "entry %d: the splits read the qkv row (x, k = (n_q + 2 n_kv) x 128) and write no y", c);
+        QLX_REQUIRE(c + 1 < ncalls && kind(c + 1) == 2, "entry %d: the splits must be followed by their merge", c);
+        const qlx_stack_attention& mg = attns[c + 1];
+        QLX_REQUIRE(mg.n_q == at.n_q && mg.n_kv == at.n_kv && mg.splits == at.splits && mg.capacity == at.capacity &&
+                        mg.table_rows == at.table_rows && mg.q_norm_w == at.q_norm_w && mg.k_norm_w == at.k_norm_w &&
+                        mg.cos == at.cos && mg.sin == at.sin && mg.positions == at.positions &&
+                        mg.k_cache == at.k_cache && mg.v_cache == at.v_cache && mg.eps == at.eps &&
+                        mg.scale == at.scale,
+                    "entry %d: the merge's attention fields differ from its splits'", c + 1);
+      } else {
+        QLX_REQUIRE(c >= 1 && kind(c - 1) == 1, "entry %d: a merge must follow its splits", c);
+        QLX_REQUIRE(q.x == nullptr && q.y != nullptr && q.k == 0, "entry %d: the merge writes y and reads no x", c);
+      }
+      QLX_REQUIRE(!normed(c), "entry %d: an attention stage has no norm stage", c);
+      continue;
+    }
     QLX_REQUIRE(q.kw == 0 || q.kw == 1 || q.kw == 2 || q.kw == 4 || q.kw == 8,
                 "projection %d: kw must be 0 (planner) or 1, 2, 4, 8", c);
     QLX_REQUIRE(q.n >= 16 && q.n % 16 == 0 && q.k > 0 && q.k % fi.kstep == 0,
@@ -1145,7 +1539,9 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
       css_doubles = std::max(css_doubles, norm_lds_doubles(8));
     }
   }
-  auto nout = [&](int c) { return calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n; };
+  auto nout = [&](int c) {
+    return kind(c) == 1 ? 0 : (calls[c].mode == QLX_MODE_SWIGLU ? calls[c].n / 2 : calls[c].n);
+  };
   // memory a projection or a norm stage writes
   auto written = [&](const void* p, long long bytes) {
     for (int j = 0; j < ncalls; ++j) {
@@ -1198,9 +1594,10 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
                   "projection %d: resid_out overlaps the residual", c);
       continue;
     }
+    if (kind(c) == 2) continue;  // reads its splits' partials
     const long long xbytes = 2LL * m * calls[c].k;
     for (int j = 0; j < ncalls; ++j) {
-      if (calls[c].x == calls[j].y && j < c && calls[c].k <= nout(j)) {
+      if (kind(j) != 1 && calls[c].x == calls[j].y && j < c && calls[c].k <= nout(j)) {
         src[c] = j;
         published[j] = 1;
         break;
@@ -1210,6 +1607,8 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
       QLX_REQUIRE(!written(calls[c].x, xbytes),
                   "projection %d reads memory the chain writes (only the whole output of an earlier projection "
                   "can be an input)", c);
+    QLX_REQUIRE(kind(c) != 1 || (src[c] >= 0 && calls[c].k == nout(src[c])),
+                "entry %d: the splits read the whole output of an earlier projection", c);
   }
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -1217,6 +1616,8 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   if (e != hipSuccess) return hip_status(e, "stack_build");
   std::vector<StackPlan> sp(ncalls);
   int lds = 0, lanes = groups_per_cu, desc_lds = -1, amax_off = 0;
+  bool att = false;  // attention stages: the kernel instance with their items
+  for (int c = 0; c < ncalls; ++c) att |= kind(c) != 0;
   const int P = cus;  // workgroups per lane
   QLX_REQUIRE(P >= 1 && (long long)P * lanes <= kMaxGrid, "%d CUs x %d lanes exceed %d workgroups", P, lanes, kMaxGrid);
   const long long desc_bytes = (long long)ncalls * sizeof(StackDesc);
@@ -1228,6 +1629,20 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     int items_lds = 0;
     for (int c = 0; c < ncalls; ++c) {
       const qlx_stack_call& q = calls[c];
+      if (kind(c) != 0) {  // attention items: whole items on as many workgroups
+        sp[c] = StackPlan{};
+        sp[c].plan.waves = waves;
+        sp[c].plan.kw = 1;
+        sp[c].plan.rw = 1;
+        sp[c].plan.splits = 1;
+        sp[c].units = attn_items(c);
+        sp[c].pe = std::min(P, sp[c].units);
+        sp[c].gran = 1;
+        sp[c].sps = 1;
+        sp[c].max_np = 1;
+        if (kind(c) == 1) items_lds = std::max(items_lds, attn_lds_bytes(waves));
+        continue;
+      }
       // With published token maxima an FP8 item reads only its slice of a published input, 4
       // bytes per value and token, after the input arrives (the weights were prefetched while
       // it was awaited): the planner charges those bytes 4x a weight byte (measured on the
@@ -1247,7 +1662,8 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     lds = desc_lds >= 0 ? (int)(items_end + desc_bytes) : items_end;
     pieces = false;
     for (int c = 0; c < ncalls; ++c) pieces |= sp[c].max_np > 1;
-    const void* fn = stack_fn_for(fmt, waves, desc_lds >= 0, pieces);
+    QLX_REQUIRE(!(att && pieces), "a chain with attention stages cannot cut row blocks into K pieces");
+    const void* fn = stack_fn_for(fmt, waves, desc_lds >= 0, pieces, att);
     if (lds > 64 * 1024) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       if (e != hipSuccess) return hip_status(e, "stack_build");
@@ -1287,6 +1703,10 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
         off += (4LL * m * max_pitch(c) + 255) & ~255LL;
       }
     }
+    if (kind(c) == 1) {  // the splits' partials: [n_kv][splits][4 rows][kAttnWords] words
+      part_off[c] = off;
+      off += (8LL * attns[c].n_kv * attns[c].splits * kAttnG * kAttnWords + 255) & ~255LL;
+    }
     if (sp[c].max_np > 1) {
       part_off[c] = off;
       off += ((8LL * (sp[c].max_np - 1) * m * calls[c].n) + 255) & ~255LL;
@@ -1302,6 +1722,47 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
   char* base = static_cast<char*>(arena);
   for (int c = 0; c < ncalls; ++c) {
     const qlx_stack_call& q = calls[c];
+    if (kind(c) != 0) {
+      const qlx_stack_attention& at = attns[c];
+      StackDesc d = {};
+      d.kind = kind(c);
+      d.a.w = at.cos;
+      d.a.ws = at.sin;
+      d.a.resid = at.q_norm_w;
+      d.a.norm_w = at.k_norm_w;
+      d.a.res_out = at.k_cache;
+      d.a.normed = at.v_cache;
+      d.a.tickets = const_cast<int*>(at.positions);
+      d.a.y = q.y;
+      d.a.m = 1;
+      d.a.n = at.capacity;
+      d.a.k = at.table_rows;
+      d.a.half = at.n_q;
+      d.a.group = at.n_kv;
+      d.a.splits = at.splits;
+      d.a.eps = at.eps;
+      d.a.nsteps = 1;
+      d.a.tile_groups = sp[c].units;
+      d.eps = at.scale * 1.4426950408889634f;  // scores pre-multiplied by log2(e): base-2 exponentials
+      if (base) {
+        d.part = reinterpret_cast<uint64_t*>(base + part_off[kind(c) == 1 ? c : c - 1]);
+        if (kind(c) == 1) {
+          d.xwire = reinterpret_cast<uint64_t*>(base + wire_off[src[c]]);
+          d.xpitch = nout(src[c]);
+        } else {
+          d.ywire = wire_off[c] >= 0 ? reinterpret_cast<uint64_t*>(base + wire_off[c]) : nullptr;
+        }
+      }
+      d.units = sp[c].units;
+      d.nwg = P;
+      d.rot = rot;
+      rot = (rot + sp[c].pe) % P;
+      d.pe = sp[c].pe;
+      d.gran = 1;
+      if (out) out[c] = d;
+      if (plans) plans[c] = sp[c].plan;
+      continue;
+    }
     StackDesc d = {};
     d.a.w = q.w;
     d.a.ws = q.w_scale;
@@ -1365,6 +1826,7 @@ int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncal
     launch->desc_lds = desc_lds;
     launch->amax_off = amax_off;
     launch->pieces = pieces ? 1 : 0;
+    launch->attention = att ? 1 : 0;
   }
   return QLX_OK;
 }
@@ -1375,7 +1837,8 @@ int qlx_stack_run(int fmt, const void* desc, int ncalls, const qlx_stack_launch*
                   launch->grid <= kMaxGrid,
               "bad executor launch configuration");
   QLX_REQUIRE(launch->pieces == 0 || launch->pieces == 1, "launch.pieces must be 0 or 1 (got %d)", launch->pieces);
-  const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0, launch->pieces != 0);
+  QLX_REQUIRE(launch->attention == 0 || launch->attention == 1, "launch.attention must be 0 or 1");
+  const void* fn = stack_fn_for(fmt, launch->waves, launch->desc_lds >= 0, launch->pieces != 0, launch->attention != 0);
   QLX_REQUIRE(fn != nullptr, "the decode executor serves W8A16, W4A16 and FP8 W8A8 (format %d)", fmt);
   QLX_REQUIRE(desc && arena && error && ncalls >= 1, "bad executor arguments");
   QLX_REQUIRE(reinterpret_cast<uintptr_t>(arena) % 256 == 0, "the arena must be 256-byte aligned");

@@ -2,45 +2,21 @@
 // (engine/kernels/rope.py:24-60 `_norm_rope`, :63-92 q/kv kernels, :125-166 the fused Q/K/V
 // kernel, :169-218 the split-K planes variant, :96-122 the INT8 cache writes).
 //
-// Eight lanes per 128-value head. Lane j holds dims 8 j .. 8 j + 7 and their rotate_half
-// partners 64 + 8 j .. 64 + 8 j + 7 (two 16-byte loads), so the rotation never leaves the lane
-// and only the head's sum of squares crosses lanes (3 shuffles). A workgroup of 256 threads
-// covers 32 heads of one row: Q heads, then K heads (whose lanes also move the V head).
-//
-// Roundings are the reference's (engine/kernels/reference.py:31-46):
-//   scale = 1 / sqrt(mean(x^2) + eps)          (fp32; the sum of squares exact in fp64)
-//   n     = bf16(bf16(x * scale) * w)
-//   y     = bf16(bf16(n * cos) + bf16(rotate_half(n) * sin)),  rotate_half(n) = (-n[64:], n[:64])
+// Eight lanes per 128-value head (rope_common.h: the lane layout and the roundings, those of
+// engine/kernels/reference.py:31-46). A workgroup of 256 threads covers 32 heads of one row:
+// Q heads, then K heads (whose lanes also move the V head).
 // From planes, x = bf16(sum of the fp32 planes in slice order) (rope.py:169-176).
 // INT8 cache: per (token, head) scale max(amax |y|, 1e-12) / 127, codes
 // clamp(floor(y / scale + 0.5), -127, 127) (rope.py:108-118).
-#include "common.h"
+#include "rope_common.h"
 #include "../../include/qlinear.h"
 
 namespace qlx {
-
-typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 
 struct RopeArgs {
   qlx_rope_args p;
   int heads;  // n_q + n_kv
 };
-
-__device__ __forceinline__ void unpack8(u32x4 v, float* f) {
-  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf2f(d[i] & 0xffffu);
-    f[2 * i + 1] = bf2f(d[i] >> 16);
-  }
-}
-
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  uint32_t d[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) d[i] = (uint32_t)f2bf(f[2 * i]) | ((uint32_t)f2bf(f[2 * i + 1]) << 16);
-  return u32x4{d[0], d[1], d[2], d[3]};
-}
 
 // 8 values of row `row` at column `col`: bf16 from qkv, or bf16(sum of the planes).
 __device__ __forceinline__ void load8(const qlx_rope_args& p, int row, long long col, float* f) {
@@ -111,63 +87,13 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeArgs ra) {
   float xl[8], xh[8];
   load8(p, row, col + 8 * j, xl);
   load8(p, row, col + 64 + 8 * j, xh);
-  double ss = 0.0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss += (double)xl[i] * (double)xl[i] + (double)xh[i] * (double)xh[i];
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
-  const float scale = 1.0f / sqrtf((float)(ss / 128.0) + p.eps);
-
   const uint16_t* gain = reinterpret_cast<const uint16_t*>(is_q ? p.q_norm_w : p.k_norm_w);
   float wl[8], wh[8];
   unpack8(*gmem(reinterpret_cast<const u32x4*>(gain + 8 * j)), wl);
   unpack8(*gmem(reinterpret_cast<const u32x4*>(gain + 64 + 8 * j)), wh);
-
-
-  // Every rounding below is to bf16, by the hardware's pair conversion (the integer rounding's
-  // bits for every value but a NaN, checked on all 2^32 inputs); a lane meeting a NaN redoes its
-  // values with the integer rounding.
   float yl[8], yh[8];
-  uint32_t ylp[4], yhp[4], nan = 0u;
-  auto lo = [](uint32_t p) { return bf2f(p & 0xffffu); };
-  auto hi = [](uint32_t p) { return bf2f(p >> 16); };
-  auto pr = [&nan](float x0, float x1) {
-    const uint32_t p = bf16_pair_hw(x0, x1);
-    nan |= bf16_nan_bits(p);
-    return p;
-  };
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    const uint32_t ta = pr(xl[i] * scale, xl[i + 1] * scale), tb = pr(xh[i] * scale, xh[i + 1] * scale);
-    const uint32_t a = pr(lo(ta) * wl[i], hi(ta) * wl[i + 1]);  // n[8 j + i], n[8 j + i + 1]
-    const uint32_t b = pr(lo(tb) * wh[i], hi(tb) * wh[i + 1]);  // n[64 + 8 j + i], ...
-    const uint32_t p1 = pr(lo(a) * cl[i], hi(a) * cl[i + 1]), p2 = pr(-lo(b) * sl[i], -hi(b) * sl[i + 1]);
-    const uint32_t p3 = pr(lo(b) * ch[i], hi(b) * ch[i + 1]), p4 = pr(lo(a) * sh[i], hi(a) * sh[i + 1]);
-    ylp[i >> 1] = pr(lo(p1) + lo(p2), hi(p1) + hi(p2));
-    yhp[i >> 1] = pr(lo(p3) + lo(p4), hi(p3) + hi(p4));
-  }
-  if (nan == 0u) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      yl[i] = bf2f((ylp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-      yh[i] = bf2f((yhp[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float a = round_bf(round_bf(xl[i] * scale) * wl[i]);  // n[8 j + i]
-      const float b = round_bf(round_bf(xh[i] * scale) * wh[i]);  // n[64 + 8 j + i]
-      yl[i] = round_bf(round_bf(a * cl[i]) + round_bf(-b * sl[i]));
-      yh[i] = round_bf(round_bf(b * ch[i]) + round_bf(a * sh[i]));
-    }
-    const u32x4 l = pack8(yl), h = pack8(yh);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ylp[i] = l[i];
-      yhp[i] = h[i];
-    }
-  }
+  uint32_t ylp[4], yhp[4];
+  rope_norm_rotate(xl, xh, wl, wh, cl, ch, sl, sh, p.eps, yl, yh, ylp, yhp);
 
   if (is_q) {
     if (!active) return;

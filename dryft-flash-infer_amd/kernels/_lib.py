@@ -42,15 +42,28 @@ class StackCall(ctypes.Structure):
 
 class StackLaunch(ctypes.Structure):
     """``qlx_stack_launch``: grid, LDS bytes, waves, descriptor LDS offset, lanes, the LDS offset
-    of the FP8 row maxima, and whether row blocks are cut into K pieces."""
+    of the FP8 row maxima, whether row blocks are cut into K pieces, and whether the chain has
+    attention stages."""
 
-    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "amax_off", "pieces")]
+    _fields_ = [(f, ctypes.c_int) for f in ("grid", "lds_bytes", "waves", "desc_lds", "lanes", "amax_off", "pieces",
+                                            "attention")]
 
 
 class NormInput(ctypes.Structure):
     _fields_ = [("resid", ctypes.c_void_p), ("delta", ctypes.c_void_p), ("norm_w", ctypes.c_void_p),
                 ("resid_out", ctypes.c_void_p), ("normed_out", ctypes.c_void_p), ("eps", ctypes.c_float),
                 ("pad", ctypes.c_int)]
+
+
+class StackAttention(ctypes.Structure):
+    """``qlx_stack_attention``: what entry c of an executor chain is -- kind 0 a projection, 1
+    an attention stage's splits, 2 their merge -- and the attention stage's parameters."""
+
+    _fields_ = [("kind", ctypes.c_int), ("n_q", ctypes.c_int), ("n_kv", ctypes.c_int), ("splits", ctypes.c_int),
+                ("capacity", ctypes.c_int), ("table_rows", ctypes.c_int), ("q_norm_w", ctypes.c_void_p),
+                ("k_norm_w", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+                ("positions", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+                ("eps", ctypes.c_float), ("scale", ctypes.c_float)]
 
 
 class RopeArgs(ctypes.Structure):
@@ -111,6 +124,9 @@ SIGNATURES = {
                          ctypes.POINTER(StackLaunch)], _I),
     "qlx_stack_build_normed": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput), _I, _I, _P,
                                 _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)], _I),
+    "qlx_stack_build_step": ([_I, _I, ctypes.POINTER(StackCall), _I, ctypes.POINTER(NormInput),
+                              ctypes.POINTER(StackAttention), _I, _I, _P, _PLAN, _P, _PLL, ctypes.POINTER(StackLaunch)],
+                             _I),
     "qlx_stack_run": ([_I, _P, _I, ctypes.POINTER(StackLaunch), _P, _P, _LL, _P], _I),
     "qlx_stream_read": ([_P, _LL, _P, _I, _P], _I),
     "qlx_qkv_norm_rope": ([ctypes.POINTER(RopeArgs), _P], _I),

@@ -45,7 +45,7 @@ class DecodeStack:
             raise ValueError(f"the decode executor serves m = 1..16 (got {m})")
         self.fmt, self.m, self.waves, self.groups_per_cu = fmt, m, waves, groups_per_cu
         self.calls, self._keep = [], []
-        self.norms = []
+        self.norms, self.attns = [], []
         self.desc = None
 
     def add(self, weight, x, y, swiglu=False, kw=0):
@@ -57,7 +57,7 @@ class DecodeStack:
         if x.device.type != "cuda":
             raise ValueError("quantized linear ops need tensors on a ROCm GPU (no CPU path)")
         if not x.is_contiguous():  # only the first columns of an earlier output, rows n_out apart
-            earlier = [t for t in self._keep[2::3] if t.data_ptr() == x.data_ptr()]
+            earlier = [t for t in self._keep[2::3] if t is not None and t.data_ptr() == x.data_ptr()]
             if not earlier or x.stride() != (earlier[0].shape[1], 1):
                 raise ValueError("a strided input must be the first columns of an earlier output of the chain")
         out_n = weight.rows // 2 if swiglu else weight.rows
@@ -70,7 +70,55 @@ class DecodeStack:
                                          y.data_ptr(), weight.rows, weight.k,
                                          _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, int(kw)))
         self.norms.append(_lib.NormInput())
+        self.attns.append(_lib.StackAttention())
         self._keep += [weight, x, y]
+        self.desc = None
+        return self
+
+    def add_attention(self, qkv, n_q, n_kv, q_norm_w, k_norm_w, cos, sin, positions, k_cache, v_cache, out, eps,
+                      splits=4, scale=None):
+        """Append an attention stage for one token (m = 1, batch 1): the per-head RMSNorm + RoPE
+        of ``qkv`` (the output tensor of an earlier projection: n_q query heads, n_kv key heads,
+        n_kv value heads of 128 values) as ``qkv_norm_rope_to_cache`` does (rope.py:125-166), the
+        key and value written into the bf16 caches ``[1, n_kv, capacity, 128]`` at the token's
+        position ``positions[0]`` (an int32 device tensor), and grouped-query attention over keys
+        0 .. position as ``DecodeAttention`` computes it (attention.py:37-178), into ``out``
+        (bf16 ``[1, n_q * 128]``, which later projections may read, e.g. o). ``splits`` items per KV
+        head share the keys; their partials are merged in the same launch."""
+        if self.m != 1:
+            raise ValueError("an attention stage takes one token (m = 1)")
+        if n_q != 4 * n_kv:
+            raise ValueError("the attention stage serves 4 query heads per KV head")
+        width = (n_q + 2 * n_kv) * 128
+        earlier = [t for t in self._keep[2::3] if t is not None and t.data_ptr() == qkv.data_ptr()]
+        if not earlier or tuple(qkv.shape) != (1, width) or qkv.dtype != torch.bfloat16:
+            raise ValueError(f"qkv must be the bf16 [1, {width}] output tensor of an earlier projection")
+        cap = k_cache.shape[2]
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (1, n_kv, cap, 128) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous bf16 [1, {n_kv}, capacity, 128] tensor")
+        for name, t in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (128,):
+                raise ValueError(f"{name} must be bf16 [128]")
+        if cos.dtype != torch.bfloat16 or cos.dim() != 2 or cos.shape[1] != 128 or sin.shape != cos.shape:
+            raise ValueError("cos and sin must be bf16 [table_rows, 128]")
+        if positions.dtype != torch.int32 or positions.numel() < 1:
+            raise ValueError("positions must be an int32 device tensor holding the token's position")
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (1, n_q * 128) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous bf16 [1, {n_q * 128}] tensor")
+        if not 1 <= splits <= 64:
+            raise ValueError("splits must be 1..64")
+        _lib.require_device(qkv, q_norm_w, k_norm_w, cos, sin, positions, k_cache, v_cache, out)
+        scale = 128 ** -0.5 if scale is None else scale
+        for kind, x, y, k in ((1, qkv.data_ptr(), None, width), (2, None, out.data_ptr(), 0)):
+            self.calls.append(_lib.StackCall(None, None, x, y, n_q * 128, k, _lib.MODE_BF16, 0))
+            self.norms.append(_lib.NormInput())
+            self.attns.append(_lib.StackAttention(kind, n_q, n_kv, int(splits), cap, cos.shape[0], q_norm_w.data_ptr(),
+                                                  k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                                  positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                                  float(eps), float(scale)))
+        self._keep += [None, qkv, None, None, None, out]
+        self._extra = getattr(self, "_extra", []) + [q_norm_w, k_norm_w, cos, sin, positions, k_cache, v_cache]
         self.desc = None
         return self
 
@@ -107,6 +155,7 @@ class DecodeStack:
                                          weight.rows, weight.k, _lib.MODE_SWIGLU if swiglu else _lib.MODE_BF16, 0))
         self.norms.append(_lib.NormInput(ptr(resid), ptr(delta), ptr(norm_w), ptr(resid_out), ptr(normed_out),
                                          float(eps), 0))
+        self.attns.append(_lib.StackAttention())
         self._keep += [weight, resid, y]
         self._extra = getattr(self, "_extra", []) + tensors
         self.desc = None
@@ -116,23 +165,24 @@ class DecodeStack:
         """Plan the chain and upload its descriptors (call after the last ``add``)."""
         if not self.calls:
             raise ValueError("empty chain")
-        device = self._keep[0].weight.device
+        device = next(w for w in self._keep[0::3] if w is not None).weight.device
         lib = _lib.lib()
         arr = (_lib.StackCall * len(self.calls))(*self.calls)
         norms = (_lib.NormInput * len(self.norms))(*self.norms)
+        attns = (_lib.StackAttention * len(self.attns))(*self.attns)
         fmt = _FMTS[self.fmt]
         arena_bytes, launch = ctypes.c_longlong(0), _lib.StackLaunch()
         with torch.cuda.device(device):
             opts = (self.waves, self.groups_per_cu)
-            _lib.check(lib.qlx_stack_build_normed(fmt, self.m, arr, len(self.calls), norms, *opts, None, None, None,
-                                                  arena_bytes, launch), "qlx_stack_build_normed")
+            _lib.check(lib.qlx_stack_build_step(fmt, self.m, arr, len(self.calls), norms, attns, *opts, None, None,
+                                                None, arena_bytes, launch), "qlx_stack_build_step")
             self.arena = torch.zeros(max(arena_bytes.value, 256), dtype=torch.uint8, device=device)
             self.error = torch.zeros(1, dtype=torch.int32, device=device)
             host = torch.empty(lib.qlx_stack_desc_size() * len(self.calls), dtype=torch.uint8)
             plans = (_lib.Plan * len(self.calls))()
-            _lib.check(lib.qlx_stack_build_normed(fmt, self.m, arr, len(self.calls), norms, *opts,
-                                                  ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.arena),
-                                                  arena_bytes, launch), "qlx_stack_build_normed")
+            _lib.check(lib.qlx_stack_build_step(fmt, self.m, arr, len(self.calls), norms, attns, *opts,
+                                                ctypes.c_void_p(host.data_ptr()), plans, _lib.ptr(self.arena),
+                                                arena_bytes, launch), "qlx_stack_build_step")
             self.desc = host.to(device)
         #: (waves, kw, rw, most K pieces of one row block) per projection
         self.configs = [(p.waves, p.kw, p.rw, p.splits) for p in plans]
@@ -169,4 +219,4 @@ class DecodeStack:
         self.error.zero_()
 
     def bytes_moved(self):
-        return sum(w.bytes_moved() for w in self._keep[0::3])
+        return sum(w.bytes_moved() for w in self._keep[0::3] if w is not None)

@@ -301,6 +301,7 @@ typedef struct qlx_stack_launch {
   int amax_off;    /* LDS byte offset of the per-token FP8 maxima (64 bytes) */
   int pieces;      /* 1 when a row block of the chain is cut into K pieces (the kernel with their
                       reduction, whose registers otherwise go to deeper weight prefetch), else 0 */
+  int attention;   /* 1 when the chain has attention stages (qlx_stack_build_step), else 0 */
 } qlx_stack_launch;
 
 /* Plan a chain of `ncalls` projections of one format (W8A16, W4A16 or FP8 W8A8; m = 1..16)
@@ -364,6 +365,44 @@ typedef struct qlx_norm_input {
 int qlx_stack_build_normed(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
                            int waves, int groups_per_cu, void* desc, qlx_plan* plans, void* arena,
                            long long* arena_bytes, qlx_stack_launch* launch);
+
+/* An attention stage inside the executor's chain (one token: m = 1, batch 1; head_dim 128;
+ * bf16 caches [1][n_kv][capacity][128]): per KV head, the per-head RMSNorm + RoPE of its query
+ * heads and of the key, with the arithmetic of qlx_qkv_norm_rope (engine/kernels/rope.py:125-166),
+ * the key and value written into the caches at the token's position p = positions[0], and
+ * grouped-query attention over keys 0 .. p with the arithmetic of qlx_decode_attention
+ * (engine/kernels/attention.py:37-178). It takes two consecutive chain entries:
+ *   kind 1 (splits): calls[c].x = the whole output of an earlier projection (the fused qkv
+ *     row: n_q query heads, then n_kv key heads, then n_kv value heads), calls[c].y = NULL,
+ *     n = n_q * 128, k = (n_q + 2 * n_kv) * 128, w and w_scale NULL. `splits` work items per KV
+ *     head, item s taking the 32-key blocks s, s + splits, ...; each publishes fp32 partials
+ *     (maximum, total and accumulator per query row) inside the launch;
+ *   kind 2 (merge): the entry right after, with the same attention fields; calls[c].x = NULL,
+ *     calls[c].y = the attention output, bf16 [1][n_q * 128] (later projections may read it),
+ *     n = n_q * 128, k = 0. One work item per query row combines the splits in order.
+ * kind 0: calls[c] is a projection (as in qlx_stack_build_normed). The token is in the cos/sin
+ * table when p < table_rows (else its query reads as NaN and nothing is written), and its key
+ * and value are written when also p < capacity. Replaces the reference's head norm + RoPE
+ * kernel and its split and merge attention kernels between the qkv and o projections of a
+ * decode step (engine/engine.py:926-949). */
+typedef struct qlx_stack_attention {
+  int kind, n_q, n_kv, splits;
+  int capacity, table_rows;
+  const void* q_norm_w;  /* bf16 [128] */
+  const void* k_norm_w;  /* bf16 [128] */
+  const void* cos;       /* bf16 [table_rows][128] */
+  const void* sin;
+  const int* positions;  /* int32 device value: the token's position */
+  void* k_cache;
+  void* v_cache;
+  float eps, scale;      /* RMSNorm epsilon; attention scale (head_dim^-0.5) */
+} qlx_stack_attention;
+
+/* qlx_stack_build_normed with attention stages: attns[c].kind selects what entry c is (attns
+ * may be NULL: every entry a projection). */
+int qlx_stack_build_step(int fmt, int m, const qlx_stack_call* calls, int ncalls, const qlx_norm_input* norms,
+                         const qlx_stack_attention* attns, int waves, int groups_per_cu, void* desc,
+                         qlx_plan* plans, void* arena, long long* arena_bytes, qlx_stack_launch* launch);
 
 /* ---- QKV consumer and decode attention ----------------------------------------------- */
 
