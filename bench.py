@@ -14,7 +14,8 @@ Two product paths run the linear stack: the single-call linears and norm kernels
 once in a HIP graph, and the decode-step executor (the whole chain, its residual + RMSNorm
 stages included, in one launch). ``decode_step`` times the real step with head norm + RoPE +
 KV-cache write and decode attention as well: the reference's own call sequence on the
-library (what Engine.generate runs), and executor launches split where attention sits.
+library (what Engine.generate runs), executor launches split where attention sits, and (one
+token) the whole step as one executor launch with attention stages inside the chain.
 
 Prints one JSON line (the driver's contract). ``value`` is microseconds per step for
 the default workload, FP8 e4m3 W8A8 at M=1.
@@ -546,6 +547,20 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
                 raise RuntimeError("decode step executor: a wait gave up")
             del step
             model.segments = None
+        if m == 1:
+            # the whole step in one executor launch, attention stages inside (the split count
+            # per KV head raced like the engine races its attention configs)
+            best = None
+            for splits in (4, 8):
+                chain = model.executor_one_launch(splits)
+                us = timed_step(chain.run, steps, warmup)
+                if chain.failed():
+                    raise RuntimeError("one-launch decode step: a wait gave up")
+                if best is None or us < best[0]:
+                    best = (us, splits)
+                del chain
+            ds["executor_one_launch_us"] = round(best[0], 2)
+            ds["executor_one_launch_splits"] = best[1]
         ds["rope_and_attention_alone_us"] = round(timed_step(model.attention_only(), steps, warmup), 2)
         ds["context_keys"] = CTX + 1
         out["decode_step"] = ds

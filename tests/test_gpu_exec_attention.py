@@ -140,3 +140,44 @@ def test_attention_stage_contract_errors():
         chain.add_attention(torch.empty(1, 6144, dtype=torch.bfloat16, device=DEV), N_Q, N_KV, t["qn"], t["kn"],
                             t["cos"], t["sin"], positions, t["kc"], t["vc"],
                             torch.empty(1, 4096, dtype=torch.bfloat16, device=DEV), EPS)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "w4a16"])
+def test_one_launch_decode_step_matches_split_launches(fmt):
+    """bench.Model's one-launch decode step (executor_one_launch: attention stages inside the
+    chain) against the same step on executor launches split at attention with the rope and
+    attention kernels between them (executor_step), four layers: the logits within relative L2
+    1e-2 and the caches' new rows within 2^-6 of each value plus 2^-8 of the row's largest (the
+    attention outputs differ in their last bits, so later layers' inputs do too); every cache row
+    but the position's untouched."""
+    import bench
+    print(f"one-launch decode step {fmt}", flush=True)
+    model = bench.Model(fmt, 1, layers=4, attention=True)
+    pos = int(model.positions.item())
+    k0 = [k.clone() for k in model.k_cache]
+    v0 = [v.clone() for v in model.v_cache]
+    step = model.executor_step()
+    step()
+    torch.cuda.synchronize()
+    assert not any(seg.failed() for seg in model.segments)
+    want = model.logits.float().clone()
+    kw = [k.clone() for k in model.k_cache]
+    vw = [v.clone() for v in model.v_cache]
+    for i in range(model.layers):
+        model.k_cache[i].copy_(k0[i])
+        model.v_cache[i].copy_(v0[i])
+    chain = model.executor_one_launch(4)
+    chain.run()
+    torch.cuda.synchronize()
+    assert not chain.failed(), chain.failed_waits()
+    got = model.logits1.float()
+    rel = ((got - want).norm() / want.norm()).item()
+    assert rel <= 1e-2, (fmt, rel)
+    for i in range(model.layers):
+        for new, ref, old in ((model.k_cache[i], kw[i], k0[i]), (model.v_cache[i], vw[i], v0[i])):
+            mask = torch.ones(new.shape[2], dtype=torch.bool, device=DEV)
+            mask[pos] = False
+            assert torch.equal(new[:, :, mask], old[:, :, mask]), (fmt, i, "rows other than the position changed")
+            a, b = new[:, :, pos].float(), ref[:, :, pos].float()
+            tol = 2.0 ** -6 * b.abs() + 2.0 ** -8 * b.abs().amax()
+            assert ((a - b).abs() > tol).sum().item() == 0, (fmt, i, (a - b).abs().max().item())
