@@ -150,22 +150,25 @@ __host__ __device__ inline void share_item(int p, int g, int U, int pe, int gran
 // 1400 at 6 / 7 / 8; W4A16 1224 / 1242 at 4 / 5. FP8 with the piece reduction (chains of
 // more than 4 tokens) at 6 steps spilled 5 registers; at 4 it spills none (M = 8 / 16 chains
 // 2411-2416 / 3541-3548 us at 6, 2386-2393 / 3518-3522 at 4 or 5); W4A16's at 4 spilled 14-20,
-// at 3 none (M = 8 chain 1541-1543 us at 4, 1478 at 3, 1484-1485 at 2).
-template <class F, bool PIECES>
+// at 3 none (M = 8 chain 1541-1543 us at 4, 1478 at 3, 1484-1485 at 2). The instance with
+// attention stages (ATT) holds the attention path's registers too; the 36-layer one-launch
+// step (8 / 4 splits) at 7 / 8 / 9 / 10 steps: FP8 1657 / 1612 / 1595 / 1627 us; W8A16 at
+// 4 / 5 / 6 / 7: 1627 / 1651 / 1683 / 1723 (4 splits); W4A16 at 3 / 4 / 5: 1364 / 1369 / 1505.
+template <class F, bool PIECES, bool ATT = false>
 struct ExecDepth {
-  static constexpr int PF = 6;
+  static constexpr int PF = ATT ? 4 : 6;
 };
-template <>
-struct ExecDepth<FmtFP8, false> {
-  static constexpr int PF = 10;
+template <bool ATT>
+struct ExecDepth<FmtFP8, false, ATT> {
+  static constexpr int PF = ATT ? 9 : 10;
 };
-template <>
-struct ExecDepth<FmtFP8, true> {
+template <bool ATT>
+struct ExecDepth<FmtFP8, true, ATT> {
   static constexpr int PF = 4;
 };
-template <bool PIECES>
-struct ExecDepth<FmtW4, PIECES> {
-  static constexpr int PF = PIECES ? 3 : 4;
+template <bool PIECES, bool ATT>
+struct ExecDepth<FmtW4, PIECES, ATT> {
+  static constexpr int PF = PIECES || ATT ? 3 : 4;
 };
 
 // Group scales a workgroup's threads hold for one item (formats with per-group scales): up
@@ -180,11 +183,11 @@ struct ExecItem {
   uint32_t scw[kScaleRegs];  // group scale pairs (bf16 bits), slot q = tid + u * threads
 };
 
-// Issue the wave's first ExecDepth<F, PIECES>::PF weight steps (and the per-row scale) of a work
+// Issue the wave's first PF weight steps (and the per-row scale) of a work
 // item. A wave without steps in the item (my == 0) loads nothing.
-template <class F, int WAVES, bool PIECES>
+template <class F, int WAVES, bool PIECES, int PF>
 __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int step0, int nst, int s, int np,
-                                              ExecItem& it, uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS]) {
+                                              ExecItem& it, uint4 (&buf)[PF][F::LOADS]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   it.tg = tg;
   it.s = s;
@@ -223,7 +226,7 @@ __device__ __forceinline__ void exec_prefetch(const GemmArgs& a, int tg, int ste
     }
   }
 #pragma unroll
-  for (int p = 0; p < ExecDepth<F, PIECES>::PF; ++p)
+  for (int p = 0; p < PF; ++p)
     if (p < it.my) load_chunk<F>(buf[p], a, it.wrow, step0 + it.kwi + p * a.kw, lane);
 }
 
@@ -599,12 +602,11 @@ __device__ __forceinline__ void stage_norm(const StackDesc& d, char* lds, int st
 // `reuse`, the activation slice (and its bias sums) staged for the previous item -- same
 // projection, same steps -- is still in place. `amax` is the zeroed FP8 scratch of the token
 // maxima (and, behind its 64 bytes, a norm stage's sums).
-template <class F, int WAVES, bool PIECES, class XS>
+template <class F, int WAVES, bool PIECES, class XS, int PF>
 __device__ __forceinline__ void exec_main(const GemmArgs& a, const XS& xs, char* lds, const ExecItem& it, bool reuse,
-                                          uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS], f32x4 (&acc)[1][1],
+                                          uint4 (&buf)[PF][F::LOADS], f32x4 (&acc)[1][1],
                                           uint32_t* amax, const MaxIn& mi = {}, const StackDesc* nd = nullptr,
                                           const Waits* nw = nullptr) {
-  constexpr int PF = ExecDepth<F, PIECES>::PF;
   constexpr bool FP8 = std::is_same<F, FmtFP8>::value;
   const int lane = threadIdx.x & 63;
   const int step0 = it.step0, nst = it.nst, kwi = it.kwi, my = it.my;
@@ -1181,9 +1183,9 @@ __device__ __forceinline__ bool next_work(const StackDesc* calls, int ncalls, in
   return false;
 }
 
-template <class F, int WAVES, bool PIECES>
+template <class F, int WAVES, bool PIECES, int PF>
 __device__ __forceinline__ void prefetch_work(const StackDesc& d, int p, int g, ExecItem& it,
-                                              uint4 (&buf)[ExecDepth<F, PIECES>::PF][F::LOADS]) {
+                                              uint4 (&buf)[PF][F::LOADS]) {
   int step0, nst, piece, np;
   share_item(share_slot(d, p), g, d.units, d.pe, d.gran, d.a.nsteps, &step0, &nst, &piece, &np);
   exec_prefetch<F, WAVES, PIECES>(d.a, g, step0, nst, piece, np, it, buf);
@@ -1237,7 +1239,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
   const Waits w{epoch, __builtin_amdgcn_s_memrealtime() + (unsigned long long)budget_ticks, err};
   __syncthreads();
   ExecItem cur, nxt;
-  uint4 buf[ExecDepth<F, PIECES>::PF][F::LOADS];
+  uint4 buf[ExecDepth<F, PIECES, ATT>::PF][F::LOADS];
   f32x4 acc[1][1];
   int nc = -1, ng = 0;
   int staged_c = -1, staged_step0 = -1, staged_nst = -1;  // activation slice now in LDS
@@ -1255,7 +1257,7 @@ stack_kernel(const StackDesc* __restrict__ gcalls, int ncalls, uint32_t* ctl, in
     if (ATT && d.kind != 0) {  // an attention stage's item: its splits, or their merge
       // No weights are in flight for it: the registers of the weight pipeline are free.
 #pragma unroll
-      for (int q = 0; q < ExecDepth<F, PIECES>::PF; ++q)
+      for (int q = 0; q < ExecDepth<F, PIECES, ATT>::PF; ++q)
 #pragma unroll
         for (int j = 0; j < F::LOADS; ++j) buf[q][j] = uint4{0u, 0u, 0u, 0u};
       if (d.kind == 1)
