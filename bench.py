@@ -576,6 +576,32 @@ def measure_stack(fmt, m, steps, warmup, breakdown=True, decode_step=True):
     return model, out
 
 
+def measure_one_launch(fmt, steps, warmup):
+    """The real decode step (m = 1, 513 keys) as one executor launch with its attention stages,
+    for a kernel-trace profile of that launch: the split count raced over 4 and 8 as in
+    measure_stack, then the winner timed again. No other path runs, so the profile's
+    attention-instance launches are this step's."""
+    model = Model(fmt, 1, attention=True)
+    best = None
+    for splits in (4, 8):
+        chain = model.executor_one_launch(splits)
+        us = timed_step(chain.run, steps, warmup)
+        if chain.failed():
+            raise RuntimeError("one-launch decode step: a wait gave up")
+        if best is None or us < best[0]:
+            best = (us, splits)
+        del chain
+    chain = model.executor_one_launch(best[1])
+    us = timed_step(chain.run, steps, warmup)
+    out = {"workload": fmt, "us": round(us, 2), "splits": best[1], "raced_us": round(best[0], 2),
+           "context_keys": CTX + 1,
+           "launch": {"grid": chain.grid, "lds": chain.lds, "waves": chain.waves, "desc_lds": chain.launch.desc_lds >= 0,
+                      "attention": bool(chain.launch.attention)}}
+    del chain, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_projection(fmt, name, m, reps):
     """Single calls of one Qwen3-4B projection in one format at batch m, over enough distinct
     weights to cover >= 1 GiB (so the Infinity Cache serves none of them), replayed as one HIP
@@ -842,6 +868,9 @@ def main():
     ap.add_argument("--only-projection", choices=[n for n, _, _ in PROJ] + [LM_HEAD[0]],
                     help="only single calls of one projection (--workload, --m) over >= 1 GiB of distinct "
                          "weights: one JSON line, for counter profiles (not the driver's line)")
+    ap.add_argument("--only-decode-step", action="store_true",
+                    help="only the one-launch decode step (--workload, m = 1, attention stages inside): one "
+                         "JSON line, for kernel-trace profiles of that launch (not the driver's line)")
     ap.add_argument("--only-reference-formats", action="store_true",
                     help="only the reference formats' cuda_fp8.matmul figures: one JSON line (not the driver's line)")
     args = ap.parse_args()
@@ -861,6 +890,10 @@ def main():
     if args.only_projection:
         print(json.dumps({"single_calls": measure_projection(args.workload, args.only_projection, args.m,
                                                              max(3, args.steps))}), flush=True)
+        return
+    if args.only_decode_step:
+        print(json.dumps({"decode_step_one_launch": measure_one_launch(args.workload, args.steps, args.warmup)}),
+              flush=True)
         return
     if args.only_reference_formats:
         print(json.dumps({"reference_formats_cuda_fp8_matmul": measure_reference_formats(max(3, args.steps // 2))}),
