@@ -1575,6 +1575,11 @@ __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ void dma16(const void* src, char* dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 2);
 }
+// 16 bytes per lane at buffer offset voff + soff into LDS at dst + 16 lane (the same non-temporal
+// policy as dma16): the vector offset can stay fixed while the scalar one advances.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int soff, char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, (int)voff, soff, 0, 2);
+}
 __device__ __forceinline__ void dma4(const void* src, char* dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
 }
@@ -1665,19 +1670,40 @@ __global__ void __launch_bounds__(WAVES * 64, WPC * WAVES / 4) gemm_ring_w4_kern
       dma4(ws + (size_t)row * (a.k >> 8) + st, dst + t * 256);
     }
   };
-  auto wrow_of = [&](int item) {
+  auto tile_of = [&](int item) {  // the wave's tile of row block `item` (past the end: dropped)
     const int tile = ((int)blockIdx.x + item * G) * a.rt + wave;
-    return weight_row(a, tile < a.ntiles ? tile : a.ntiles - 1, lane & 15);  // past the end: dropped
+    return __builtin_amdgcn_readfirstlane(tile < a.ntiles ? tile : a.ntiles - 1);
   };
-  int ig = 0, ii = 0, is = 0, iw = wrow_of(0);  // next step to issue: row block ii, step is
+  auto wrow_of = [&](int item) { return weight_row(a, tile_of(item), lane & 15); };
+  // Tile-layout weights (the launch takes whole tiles and bf16 outputs): step s of a tile is the
+  // 2 KB block (tile * k / 256 + s) * 2048, lane l's 16 bytes of half j at j * 1024 + 16 l --
+  // read through a buffer resource with that block's offset as the scalar offset and the lane's
+  // as a fixed vector offset, so issuing a step costs no vector instruction. Row-major weights
+  // (or tiles past 4 GB) go through chunk_ptr.
+  const int spr = a.k >> 8;
+  const uint32_t lane_off = (uint32_t)lane * 16u;
+  const unsigned long long wbytes = (unsigned long long)a.ntiles * spr * 2048ull;
+  const bool by_buffer = a.tiled && wbytes < (1ull << 31);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.w), (short)0, by_buffer ? (int)wbytes : 0, 0x00020000);
+  int ig = 0, ii = 0, is = 0, it = tile_of(0), iw = wrow_of(0);  // next step to issue: row block ii, step is
   auto issue = [&]() {
     char* slot = ring + (ig % D) * SLOT;
+    if (by_buffer) {
+      const int soff = (it * spr + is) * 2048;
 #pragma unroll
-    for (int j = 0; j < L; ++j) dma16(F::chunk_ptr(a, iw, is, lane, j), slot + j * 1024);
+      for (int j = 0; j < L; ++j) dma16_buf(wr, lane_off + j * 1024u, soff, slot + j * 1024);
+    } else {
+#pragma unroll
+      for (int j = 0; j < L; ++j) dma16(F::chunk_ptr(a, iw, is, lane, j), slot + j * 1024);
+    }
     ++ig;
     if (++is == ns) {
       is = 0;
-      if (++ii < nitems) iw = wrow_of(ii);
+      if (++ii < nitems) {
+        it = tile_of(ii);
+        iw = wrow_of(ii);
+      }
     }
   };
   // Prologue: row block 0's scales, the activation (its LDS writes wait for nothing else in

@@ -71,3 +71,19 @@ def test_persistent_swiglu_w4():
     got = act.float().cpu()
     tol = 2.0 ** -7 * want.abs() + 1e-6
     assert bool(((got - want).abs() <= tol).all())
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_ring_row_major_equals_tiled(m):
+    """The ring kernel reads tile-layout weights through a buffer resource (a scalar offset per
+    2 KB step) and row-major packed weights through per-lane addresses: the same codes reach
+    the same lanes, so the lm_head output is bit-identical either way."""
+    print(f"ring row-major vs tiled m={m}", flush=True)
+    n, k = 151936, 2560
+    g = torch.Generator(device=DEV).manual_seed(60 + m)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    packed = qlinear.quantize_w4(w)
+    t = qlinear.prepare(packed, "w4a16")
+    x = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    cfg = (8, 1, 1, 1)
+    assert torch.equal(qlinear.linear_w4a16(x, t, config=cfg), qlinear.linear_w4a16(x, packed, config=cfg))
