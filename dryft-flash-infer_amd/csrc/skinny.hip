@@ -56,6 +56,13 @@ __host__ __device__ inline SkinnyLayout skinny_layout(int m, int waves, int rw) 
   return L;
 }
 
+// LDS of a launch: the two chunk buffers, then (4-bit weights) the shared code-bias totals of
+// two steps, [2][2 groups][MT][16 tokens] floats.
+template <class F, int MT>
+__host__ __device__ inline int skinny_lds(const SkinnyLayout& L) {
+  return 2 * L.chunk + (std::is_same<F, FmtW4>::value ? 2 * 2 * MT * 16 * 4 : 0);
+}
+
 // x chunks (16 bytes, 8 values) of one K step that each thread stages: 16 MT rows.
 template <class F, int WAVES, int MT>
 struct SkinnyStage {
@@ -172,6 +179,86 @@ __device__ __forceinline__ void skinny_step(f32x4 (&acc)[RW][MT], const uint4 (&
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][mt][i] += tmp[r][mt][i] - tb[mt][i];
+  }
+}
+
+// W4A16 step with the code-bias chains shared: the chain of (group j, token fragment mt) depends
+// on the staged activation only, the same for every tile of the workgroup, so wave
+// (j MT + mt) % WAVES alone runs it and leaves its totals in bt_cur[j][mt][16 tokens]; the others
+// read them after the step's barrier. So each wave keeps its step's partials (pend) and group
+// scales (ps: the chunk buffer they came from is restaged during the next step) and adds them
+// one step later: skinny_apply_w4(step i - 1) then skinny_step_w4s(step i). The sums, their
+// roundings and their order are skinny_step's, so the output is the same bits.
+template <int MT, int RW>
+__device__ __forceinline__ void skinny_apply_w4(f32x4 (&acc)[RW][MT], const f32x4 (&pend)[2][RW][MT],
+                                                const f32x4 (&ps)[2][RW], const float* bt, int lane) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float tb[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tb[mt] = bt[(j * MT + mt) * 16 + (lane & 15)];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const f32x4 s4 = ps[j][r];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][mt][i] = fmaf(s4[i], pend[j][r][mt][i] - tb[mt], acc[r][mt][i]);
+    }
+  }
+}
+
+template <int MT, int RW, int WAVES>
+__device__ __forceinline__ void skinny_step_w4s(f32x4 (&pend)[2][RW][MT], f32x4 (&ps)[2][RW], const uint4 (&c)[RW][2],
+                                                const char* ch, const SkinnyLayout& L, float* bt_cur, int lane, int wave,
+                                                const int (&xoff)[MT], const int (&rowl)[RW]) {
+  const uint4 ab = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};  // bf16 136 = the code bias
+  const float* sc = reinterpret_cast<const float*>(ch + L.off_sc);
+  // The chains this wave runs: q = wave, wave + WAVES, .. below 2 MT, or wave % 2 MT once
+  // when the waves outnumber the chains (duplicates write the same bits). No branch: each chain
+  // reads its own fragments at a computed address.
+  constexpr int NCH = 2 * MT, PER = NCH > WAVES ? NCH / WAVES : 1;
+  static_assert(NCH <= WAVES || NCH % WAVES == 0, "chains spread evenly over the waves");
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int q = NCH > WAVES ? wave + u * WAVES : wave % NCH;
+    const int jq = q / MT, mq = q - jq * MT;
+    int xq = xoff[0];
+#pragma unroll
+    for (int mt = 1; mt < MT; ++mt) xq = mq == mt ? xoff[mt] : xq;
+    const char* bq = ch + xq + (jq * 128 + (lane >> 4) * 32) * 2;
+    f32x4 tb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      tb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ab), as_bf16x8(*reinterpret_cast<const uint4*>(bq + t * 16)),
+                                                   tb, 0, 0, 0);
+    if (lane < 16) bt_cur[q * 16 + lane] = tb[0];  // every row of the chain's result is the same
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) ps[j][r] = *reinterpret_cast<const f32x4*>(sc + j * L.sc_stride + rowl[r]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) pend[j][r][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int kb = (j * 128 + (lane >> 4) * 32) * 2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 av[RW];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const uint32_t wd = t == 0 ? c[r][j].x : t == 1 ? c[r][j].y : t == 2 ? c[r][j].z : c[r][j].w;
+        av[r] = uint4{nib_pair(wd, 0), nib_pair(wd, 4), nib_pair(wd, 8), nib_pair(wd, 12)};
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(ch + xoff[mt] + kb + t * 16);
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+          pend[j][r][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[r]), as_bf16x8(bv), pend[j][r][mt], 0, 0, 0);
+      }
+    }
   }
 }
 
@@ -330,10 +417,26 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xoff[mt] = min(16 * mt + (lane & 15), a.m - 1) * L.xstride;
 
+  // The SwiGLU instance of 4-bit weights at two token fragments on 4 waves (gate_up's 33-64
+  // token launches, two 32-token blocks) shares the code-bias chains (skinny_step_w4s):
+  // [step parity][2][MT][16] totals behind the two chunk buffers, a step's partials added after
+  // the next barrier. Measured per call over 36 distinct Qwen3-4B weights (us, own chains /
+  // shared): gate_up at 48 and 64 tokens 24.5 / 21.1 and 24.4 / 21.4; every other instance as
+  // fast or slower shared -- gate_up at 16 and 32 tokens (8 waves) 11.8 / 12.7 and 15.2 / 15.6,
+  // down at 16 / 32 / 64 tokens 9.4 / 10.0, 12.7 / 12.8, 15.8 / 15.8.
+  constexpr bool SB = std::is_same<F, FmtW4>::value && MT == 2 && WAVES == 4 && SW;
+  float* const btb = reinterpret_cast<float*>(lds + 2 * L.chunk);
+  f32x4 pend[2][RW][MT], ps[2][RW];
   // Every lambda is inlined: an outlined one would take the register arrays by address (scratch).
   auto body = [&](int i, auto pc) __attribute__((always_inline)) {
     constexpr int p = decltype(pc)::value;
-    skinny_step<F, MT, RW>(acc, buf[p], lds + (i & 1) * L.chunk, L, lane, xoff, rowl);
+    if constexpr (SB) {
+      if (i > 0) skinny_apply_w4<MT, RW>(acc, pend, ps, btb + ((i - 1) & 1) * (2 * MT * 16), lane);
+      skinny_step_w4s<MT, RW, WAVES>(pend, ps, buf[p], lds + (i & 1) * L.chunk, L, btb + (i & 1) * (2 * MT * 16),
+                                     lane, wave, xoff, rowl);
+    } else {
+      skinny_step<F, MT, RW>(acc, buf[p], lds + (i & 1) * L.chunk, L, lane, xoff, rowl);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int nx = min(step0 + i + PF, last);
     fetch_x(nx, rr[p]);
@@ -348,6 +451,8 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   static_for<0, PF>([&](auto pc) __attribute__((always_inline)) {  // the last nst % PF steps (uniform branches)
     if (i0 + decltype(pc)::value < nst) body(i0 + decltype(pc)::value, pc);
   });
+  if constexpr (SB)  // the last step's partials: its totals were published by the last barrier
+    skinny_apply_w4<MT, RW>(acc, pend, ps, btb + ((nst - 1) & 1) * (2 * MT * 16), lane);
 
   // Epilogue: lane holds rows 4 (lane >> 4) + 0..3 of each tile for token 16 mt + (lane & 15).
   // K-slice planes shared through tickets go through a buffer resource at device scope.
@@ -468,7 +573,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
 
 template <class F, int MT, int RW, int WAVES>
 hipError_t skinny_launch(const GemmArgs& a, const SkinnyLayout& L, int sps, hipStream_t st) {
-  const int lds = 2 * L.chunk;
+  const int lds = skinny_lds<F, MT>(L);
   const dim3 grid(a.tile_groups * a.splits * (a.tblocks == 2 ? 2 : 1)), block(WAVES * 64);
   const void* fn = a.mode == QLX_MODE_SWIGLU ? reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, true>)
                                               : reinterpret_cast<const void*>(&skinny_kernel<F, MT, RW, WAVES, false>);
@@ -589,7 +694,8 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
     return QLX_OK;
   }
   const SkinnyLayout L = skinny_layout<F>(m, plan->waves, plan->rw);
-  QLX_REQUIRE(2 * L.chunk <= kLdsLimit, "%s: %d bytes of LDS", name, 2 * L.chunk);
+  const int lds_bytes = skinny_lds<F, 4>(L);  // the widest token count's totals
+  QLX_REQUIRE(lds_bytes <= kLdsLimit, "%s: %d bytes of LDS", name, lds_bytes);
   hipError_t e = plan->waves == 8 ? skinny_mt<F, 8>(a, L, sps, st) : skinny_mt<F, 4>(a, L, sps, st);
   if (e != hipSuccess) return hip_status(e, name);
   if (splits > 1 && a.tickets == nullptr) {  // without tickets: the planes reduced in a second launch
