@@ -22,8 +22,14 @@ def _add_norm(x, delta, planes, weight, eps):
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    from .cuda_small import rms_norm as _rms
-    return _rms(x, weight, eps)
+    """RMSNorm over the last dimension of a contiguous ``[rows, n]`` tensor (norm.py:98-104): the
+    add-norm kernel with neither delta nor planes, and no residual written."""
+    rows, n = x.shape
+    _lib.require_device(x, weight)
+    out = torch.empty_like(x)
+    _lib.call("qlx_add_rms_norm", _lib.ptr(x), None, None, 0, _lib.ptr(weight), None, _lib.ptr(out),
+              rows, n, float(eps), _lib.stream(x.device))
+    return out
 
 
 def add_rms_norm(x, delta, weight, eps):
@@ -37,8 +43,16 @@ def add_rms_norm_partials(x, partials, weight, eps):
 
 
 def add_rms_norm_separate(x, delta, weight, eps):
-    return add_rms_norm(x, delta, weight, eps)
+    """The reference's two-kernel form (norm.py:141-144: a bf16 residual add, then ``rms_norm``
+    of it, chosen there for short decode matrices). Both steps round exactly as the fused kernel
+    does, so the one launch of ``add_rms_norm`` gives the same bits for a launch fewer: on MI355X
+    the fused kernel is the faster one at every row count (one workgroup per row, every load
+    issued before any is used)."""
+    return _add_norm(x, delta, None, weight, eps)
 
 
 def add_rms_norm_partials_separate(x, partials, weight, eps):
-    return add_rms_norm_partials(x, partials, weight, eps)
+    """The reference's sequential form (norm.py:147-154: the fp32 planes summed in slice order,
+    the bf16 casts of the projection and the residual, then ``rms_norm``): the same roundings in
+    the same order as ``add_rms_norm_partials``, which does them in one launch."""
+    return _add_norm(x, None, partials, weight, eps)

@@ -249,6 +249,13 @@ def test_plane_consumers_bit_exact():
             assert np.array_equal(bits16(y1), y0), (rows, splits, "exact-sum RMSNorm is bit-exact")
             r2, y2 = norm.add_rms_norm_partials(x, planes, w, 1e-6)
             assert torch.equal(r2, r1) and torch.equal(y2, y1)
+            r3, y3 = norm.add_rms_norm_partials_separate(x, planes, w, 1e-6)
+            assert torch.equal(r3, r1) and torch.equal(y3, y1)
+            assert torch.equal(norm.rms_norm(r1, w, 1e-6), y1), "rms_norm of the residual"
+            d = torch.randn(rows, 2560, dtype=torch.bfloat16, device=DEV)
+            r4, y4 = norm.add_rms_norm_separate(x, d, w, 1e-6)
+            r5, y5 = O.add_rms_norm(bits16(x), bits16(d), bits16(w), 1e-6)
+            assert np.array_equal(bits16(r4), r5) and np.array_equal(bits16(y4), y5), (rows, "separate form")
             reduced = torch.empty(rows, 2560, dtype=torch.bfloat16, device=DEV)
             cuda_fp8 = kmod("cuda_fp8")
             cuda_fp8._module_for(1, 1).kernel("reduce_partials")(0, 256, planes, reduced, reduced.numel(), splits)
