@@ -80,6 +80,27 @@ extern "C" int qlx_plan_linear(int fmt, int mode, int m, int n, int k, qlx_plan*
       q.splits = std::min(s, nsteps);
       qlx::layout(fi, q, m, n, k, a);
       q.splits = a.splits;
+      // 8-bit weights have twice W4A16's K steps per byte of row, and there more, smaller
+      // workgroups win on the whole-K shapes the rule above gives 8 tiles or 2 tile slots per
+      // workgroup. Measured on MI355X, us per call over 24 distinct Qwen3-4B weights (this rule's
+      // plan / the one above): SwiGLU gate_up at 4 waves, 2 per tile -- FP8 13.02 / 13.80,
+      // 15.09 / 15.49, 15.05 / 15.83, 15.72 / 16.13 at M = 1 / 2 / 4 / 8; W8A16 13.29 / 15.68,
+      // 14.33 / 14.63, 14.65 / 14.89 at M = 1 / 2 / 4 (15.42 / 15.28 at 8); FP8 qkv with a whole
+      // workgroup per tile -- 7.03 / 7.42, 9.15 / 9.30, 9.29 / 9.52, 9.57 / 9.89 (W8A16 qkv and
+      // every W4A16 shape are faster as above).
+      const bool bits8 = fmt == QLX_FMT_FP8 || fmt == QLX_FMT_W8A16;
+      if (bits8 && mode == QLX_MODE_SWIGLU && q.splits == 1 && q.waves == 8 && q.kw == 1 && q.rw == 1 &&
+          m <= (fmt == QLX_FMT_FP8 ? 8 : 4)) {
+        q.waves = 4;
+        q.kw = 2;
+        qlx::layout(fi, q, m, n, k, a);
+        q.splits = a.splits;
+      } else if (fmt == QLX_FMT_FP8 && mode == QLX_MODE_BF16 && q.splits == 1 && q.waves == 8 && q.kw == 4 &&
+                 q.rw == 1 && m <= 8) {
+        q.kw = 8;
+        qlx::layout(fi, q, m, n, k, a);
+        q.splits = a.splits;
+      }
       *plan = q;
       return QLX_OK;
     }
