@@ -400,11 +400,39 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
   // barrier per step publishes it. Steps past the slice are clamped to its last (cache hits).
   uint4 buf[PF][RW][F::LOADS];
   Staged rr[PF];
+  // Weights through a buffer resource (WBUF): a tile's K steps are consecutive 2 KB blocks, so a
+  // lane's chunk of step s sits s * 2048 bytes past its step-0 offset (woff, fixed for the
+  // launch: a wave keeps its tiles) and the step is the scalar offset -- no per-lane address
+  // arithmetic per refill. Measured per call over 24 distinct Qwen3-4B weights (us, per-lane
+  // addresses / buffer): W4A16 at 16 tokens gate_up 11.8 / 11.4, down 9.4 / 9.1; at 32 tokens
+  // gate_up (8 waves) 15.3 / 14.9; W8A16 at 16 tokens gate_up 16.6 / 15.2, down 11.4 / 11.2. The
+  // other instances measured as fast or slower with it (the 4-wave 33-64 token launches: W4A16
+  // down 15.7 / 15.9, W8A16 gate_up 28.4 / 30.1; FP8 at 32-64 tokens up to 0.7 us slower).
+  constexpr bool WBUF = (std::is_same<F, FmtW4>::value && (MT == 1 || WAVES == 8)) ||
+                        (std::is_same<F, FmtW8>::value && MT == 1);
+  const __amdgpu_buffer_rsrc_t wrs = skinny_rsrc(a.w, WBUF ? (unsigned)a.ntiles * (unsigned)a.nsteps * 2048u : 0u);
+  uint32_t woff[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+    woff[r] = WBUF ? (uint32_t)(reinterpret_cast<const char*>(F::chunk_ptr(a, lrow[r], 0, lane, 0)) -
+                                static_cast<const char*>(a.w))
+                   : 0u;
+  auto wload = [&](uint4 (&c)[F::LOADS], int r, int step) __attribute__((always_inline)) {
+    if constexpr (WBUF) {
+#pragma unroll
+      for (int j = 0; j < F::LOADS; ++j) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)(woff[r] + (uint32_t)j * 1024u), step * 2048, 2);
+        c[j] = uint4{v[0], v[1], v[2], v[3]};
+      }
+    } else {
+      load_chunk<F>(c, a, lrow[r], step, lane);
+    }
+  };
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
     fetch_x(min(step0 + p, last), rr[p]);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, lrow[r], min(step0 + p, last), lane);
+    for (int r = 0; r < RW; ++r) wload(buf[p][r], r, min(step0 + p, last));
   }
   put_x(lds, rr[0]);
   __syncthreads();
@@ -441,7 +469,7 @@ skinny_kernel(GemmArgs a0, SkinnyLayout L, int steps_per_slice) {
     const int nx = min(step0 + i + PF, last);
     fetch_x(nx, rr[p]);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) load_chunk<F>(buf[p][r], a, lrow[r], nx, lane);
+    for (int r = 0; r < RW; ++r) wload(buf[p][r], r, nx);
     __builtin_amdgcn_sched_barrier(0);
     put_x(lds + ((i + 1) & 1) * L.chunk, rr[(p + 1) % PF]);
     __syncthreads();
@@ -627,6 +655,8 @@ int skinny_run(const char* name, GemmArgs a, int m, int n, int k, int mode, cons
   QLX_REQUIRE(m >= 1 && m <= 64, "%s: m=%d must be in 1..64", name, m);
   QLX_REQUIRE(n >= 16 && n % 16 == 0 && k >= F::KSTEP && k % F::KSTEP == 0,
               "%s: n=%d k=%d do not fit the tiled format", name, n, k);
+  QLX_REQUIRE((long long)(n / 16) * (k / F::KSTEP) * 2048 < (1ll << 31),
+              "%s: the skinny GEMM reads weights of under 2 GiB (n=%d k=%d)", name, n, k);
   QLX_REQUIRE(mode == QLX_MODE_BF16 || mode == QLX_MODE_SWIGLU, "%s: mode %d", name, mode);
   QLX_REQUIRE(plan->waves == 4 || plan->waves == 8, "%s: waves must be 4 or 8", name);
   QLX_REQUIRE(plan->rw >= 1 && plan->rw <= skinny_rw_max(skinny_mt_of(m)),
