@@ -100,6 +100,9 @@ constexpr int kMaxLine = 32;  // maxima words per row block: one 128-byte line
 // Measured on the Qwen3-4B FP8 chain (us per step, without / with): M=1 1180 / 1319, M=2
 // 1486 / 1568, M=4 2029 / 2027, M=8 3287 / 2918, M=16 5148 / 3928.
 constexpr int kMaximaMinM = 4;
+// FP8 projections below this many weight bytes run on half the workgroups in chains of at most
+// kMaximaMinM tokens (the planner's loop says why): Qwen3-4B's qkv, o and down, not gate_up.
+constexpr long long kHalfBytes = 32LL << 20;
 
 // Workgroup p's share of a projection. Shares are rotated from projection to projection (each
 // starts where the previous one's workgroups ended), so that when a projection has fewer
@@ -1652,7 +1655,19 @@ int qlx_stack_build_step(int fmt, int m, const qlx_stack_call* calls, int ncalls
       // 3930, 2x 2642 / 3475, 3x 2462 / 3490, 4x 2412 / 3488, 6x 2422 / 3483).
       const bool slice_staged = fmt == QLX_FMT_FP8 && m > kMaximaMinM && src[c] >= 0 && !normed(c);
       const double stage_bytes = slice_staged ? 4.0 * 4.0 * fi.kstep * m : 0.0;
-      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, P, waves, q.kw, kLdsLimit - 64, sp[c], stage_bytes),
+      // FP8 chains without published maxima: a projection of under kHalfBytes of weights is
+      // planned on half the workgroups. Shares start where the previous projection's ended, so
+      // two such projections in a row (qkv -> o, down -> the next qkv) run on disjoint halves,
+      // and a consumer's poll never queues behind the weight prefetch its workgroup issued
+      // right after producing (memory counters complete in order). Measured on the Qwen3-4B
+      // chains, us per step, all workgroups / half: FP8 M=1 1175 / 1103, M=2 1610 / 1566, M=4
+      // 2085 / 2054, the one-launch decode step with attention 1579 / 1488; 3/8 of them the
+      // same, 3/4 no gain (the halves overlap), gate_up (50 MB) halved too 1789. W8A16 (1276 /
+      // 1411) and W4A16 (1047 / 1165), whose items compute more after their input arrives, and
+      // FP8 above kMaximaMinM tokens (2647 / 3097 at M=8) keep every workgroup.
+      const bool half = fmt == QLX_FMT_FP8 && m <= kMaximaMinM && (long long)q.n * q.k < kHalfBytes;
+      const int Pp = half ? std::max(1, P / 2) : P;
+      QLX_REQUIRE(plan_projection(fi, q.mode, m, q.n, q.k, Pp, waves, q.kw, kLdsLimit - 64, sp[c], stage_bytes),
                   "projection %d: no executor plan for n=%d k=%d", c, q.n, q.k);
       GemmArgs a = {};
       const int l = exec_lds(fi, sp[c].plan, m, q.n, q.k, a);
