@@ -149,21 +149,25 @@ __host__ __device__ inline void share_item(int p, int g, int U, int pe, int gran
 // (fewer for 4-bit weights, whose dequantization needs more registers). A chain whose row
 // blocks are never cut into K pieces runs a kernel without the piece reduction, whose
 // registers allow FP8 a deeper prefetch. Measured on the Qwen3-4B M=1 chain (us per step):
-// FP8 1217 / 1223 / 1205 / 1203 / 1229 at 6 / 8 / 9 / 10 / 11 steps; W8A16 1383 / 1405 /
+// FP8 1217 / 1223 / 1205 / 1203 / 1229 at 6 / 8 / 9 / 10 / 11 steps, and since its qkv, o and
+// down run on half the workgroups (twice the share each) 1219 / 1148 / 1107 / 1089 / 1167 at
+// 6 / 8 / 10 / 12 / 14 (12 spills 6 registers, 14 spills 25; M = 2 1572 / 1559 at 10 / 12,
+// M = 4 2062-2070 / 2059-2064); W8A16 1383 / 1405 /
 // 1400 at 6 / 7 / 8; W4A16 1224 / 1242 at 4 / 5. FP8 with the piece reduction (chains of
 // more than 4 tokens) at 6 steps spilled 5 registers; at 4 it spills none (M = 8 / 16 chains
 // 2411-2416 / 3541-3548 us at 6, 2386-2393 / 3518-3522 at 4 or 5); W4A16's at 4 spilled 14-20,
 // at 3 none (M = 8 chain 1541-1543 us at 4, 1478 at 3, 1484-1485 at 2). The instance with
 // attention stages (ATT) holds the attention path's registers too; the 36-layer one-launch
-// step (8 / 4 splits) at 7 / 8 / 9 / 10 steps: FP8 1657 / 1612 / 1595 / 1627 us; W8A16 at
-// 4 / 5 / 6 / 7: 1627 / 1651 / 1683 / 1723 (4 splits); W4A16 at 3 / 4 / 5: 1364 / 1369 / 1505.
+// step (8 / 4 splits) at 7 / 8 / 9 / 10 steps: FP8 1657 / 1612 / 1595 / 1627 us (with the
+// halves 1493 at 9, 1535 at 11); W8A16 at 4 / 5 / 6 / 7: 1627 / 1651 / 1683 / 1723 (4 splits);
+// W4A16 at 3 / 4 / 5: 1364 / 1369 / 1505.
 template <class F, bool PIECES, bool ATT = false>
 struct ExecDepth {
   static constexpr int PF = ATT ? 4 : 6;
 };
 template <bool ATT>
 struct ExecDepth<FmtFP8, false, ATT> {
-  static constexpr int PF = ATT ? 9 : 10;
+  static constexpr int PF = ATT ? 9 : 12;
 };
 template <bool ATT>
 struct ExecDepth<FmtFP8, true, ATT> {
